@@ -1,0 +1,103 @@
+"""ctypes binding of libmx_attn.so (the C ABI in include/mx_attn.h).
+
+This is the binding a Python caller of the C ABI would add; it mirrors the reference's own ctypes layer for its C API
+(python/dooms/_lib.py:113-229 in dooms.cpp 0.6.1): load the library, declare argument types, turn a non-zero code into
+an exception that carries the library's last-error message. There is no fallback: if the library is missing the import
+of an entry point raises.
+"""
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libmx_attn.so")
+
+OK = 0
+INVALID_ARGUMENT = 1
+UNSUPPORTED = 4
+RESOURCE_EXHAUSTED = 5
+INTERNAL = 7
+CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSUPPORTED",
+              RESOURCE_EXHAUSTED: "RESOURCE_EXHAUSTED", INTERNAL: "INTERNAL"}
+
+# Every symbol include/mx_attn.h declares.
+EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_decode",
+           "mx_attn_decode_workspace_bytes")
+
+
+class MxAttnDesc(ctypes.Structure):
+    """mx_attn_desc (include/mx_attn.h)."""
+    _fields_ = [
+        ("n_head", ctypes.c_int32), ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("n_q", ctypes.c_int32), ("p0", ctypes.c_int32), ("n_kv", ctypes.c_int32), ("causal", ctypes.c_int32),
+        ("reserved", ctypes.c_int32), ("q_stride", ctypes.c_int64), ("kv_stride", ctypes.c_int64),
+        ("out_stride", ctypes.c_int64), ("scale", ctypes.c_float),
+    ]
+
+
+class MxAttnError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{CODE_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises FileNotFoundError if it was never built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} is missing: build it with `python -m dooms_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        L.mx_attn_abi_version.restype = ctypes.c_int32
+        L.mx_attn_abi_version.argtypes = []
+        L.mx_attn_last_error.restype = ctypes.c_char_p
+        L.mx_attn_last_error.argtypes = []
+        L.mx_attn_prefill.restype = ctypes.c_int32
+        L.mx_attn_prefill.argtypes = [ctypes.POINTER(MxAttnDesc), P, P, P, P, P, P]
+        L.mx_attn_decode.restype = ctypes.c_int32
+        L.mx_attn_decode.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), P,
+                                     ctypes.POINTER(P), ctypes.POINTER(P), P, P, P, ctypes.c_size_t, P]
+        L.mx_attn_decode_workspace_bytes.restype = ctypes.c_size_t
+        L.mx_attn_decode_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.c_int32]
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().mx_attn_last_error().decode()
+
+
+def check(code: int) -> None:
+    if code != OK:
+        raise MxAttnError(code, last_error())
+
+
+def make_desc(n_head, n_head_kv, head_dim, n_q, q_stride, kv_stride, out_stride, scale, p0=0, n_kv=0, causal=1,
+              reserved=0) -> MxAttnDesc:
+    return MxAttnDesc(n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim, n_q=n_q, p0=p0, n_kv=n_kv,
+                      causal=causal, reserved=reserved, q_stride=q_stride, kv_stride=kv_stride,
+                      out_stride=out_stride, scale=scale)
+
+
+def prefill_raw(desc: MxAttnDesc, q: int, k: int, v: int, out: int, lse: int, stream: int) -> int:
+    """mx_attn_prefill on raw device addresses; returns the code."""
+    return lib().mx_attn_prefill(ctypes.byref(desc), q, k, v, out, lse or None, stream or None)
+
+
+def decode_raw(desc: MxAttnDesc, kv_len, q: int, k_ptrs, v_ptrs, out: int, lse: int, ws: int, ws_bytes: int,
+               stream: int) -> int:
+    """mx_attn_decode on raw device addresses; kv_len / k_ptrs / v_ptrs are Python sequences; returns the code."""
+    n = len(kv_len)
+    lens = (ctypes.c_int32 * n)(*kv_len)
+    kp = (ctypes.c_void_p * n)(*k_ptrs)
+    vp = (ctypes.c_void_p * n)(*v_ptrs)
+    return lib().mx_attn_decode(ctypes.byref(desc), n, lens, q, kp, vp, out, lse or None, ws or None, ws_bytes,
+                                stream or None)
+
+
+def decode_workspace_bytes(desc: MxAttnDesc, batch: int, max_kv_len: int) -> int:
+    return lib().mx_attn_decode_workspace_bytes(ctypes.byref(desc), batch, max_kv_len)

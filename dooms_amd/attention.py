@@ -1,0 +1,83 @@
+"""torch-tensor front end of the C ABI (plumbing: torch only supplies device memory and the stream).
+
+Every call goes through libmx_attn.so; there is no CPU or PyTorch fallback. Tensors must be CUDA (HIP) float16 with a
+unit stride along the feature dimension; row strides are taken from the tensors.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != torch.float16:
+        raise ValueError(f"{name} must be float16, got {t.dtype}")
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D [rows][features] with unit feature stride")
+    return t
+
+
+def prefill(q, k_cache, v_cache, *, n_head, n_head_kv, head_dim, p0=0, causal=True, n_kv=None, scale=None,
+            out=None, lse=None, want_lse=False):
+    """mx_attn_prefill: q [n_q][>= n_head*hd], caches [n_kv][>= n_head_kv*hd]. Returns (out, lse or None)."""
+    _rows(q, "q"), _rows(k_cache, "k_cache"), _rows(v_cache, "v_cache")
+    if k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("k_cache and v_cache must share a row stride")
+    n_q = q.shape[0]
+    if out is None:
+        out = torch.empty(n_q, n_head * head_dim, dtype=torch.float16, device=q.device)
+    _rows(out, "out")
+    if want_lse and lse is None:
+        lse = torch.empty(n_q, n_head, dtype=torch.float32, device=q.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, q.stride(0), k_cache.stride(0), out.stride(0), scale,
+                       p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0)
+    _lib.check(_lib.prefill_raw(d, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                lse.data_ptr() if lse is not None else 0, _stream()))
+    return out, lse
+
+
+def decode_workspace_bytes(*, n_head, n_head_kv, head_dim, n_q, batch, max_kv_len, causal=False) -> int:
+    d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, n_head * head_dim, n_head_kv * head_dim,
+                       n_head * head_dim, 1.0, causal=1 if causal else 0)
+    return _lib.decode_workspace_bytes(d, batch, max_kv_len)
+
+
+def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1, causal=False, scale=None,
+           out=None, lse=None, want_lse=False, workspace=None):
+    """mx_attn_decode: q [batch*n_q][>= n_head*hd]; k_caches/v_caches lists of [>= kv_len[b]][>= n_head_kv*hd]
+    tensors (entries may repeat); kv_len list of ints. Returns (out, lse or None)."""
+    batch = len(kv_len)
+    if len(k_caches) != batch or len(v_caches) != batch:
+        raise ValueError("k_caches, v_caches and kv_len must have one entry per sequence")
+    _rows(q, "q")
+    kv_stride = k_caches[0].stride(0)
+    for t in list(k_caches) + list(v_caches):
+        _rows(t, "cache")
+        if t.stride(0) != kv_stride:
+            raise ValueError("every cache must share one row stride")
+    if out is None:
+        out = torch.empty(q.shape[0], n_head * head_dim, dtype=torch.float16, device=q.device)
+    _rows(out, "out")
+    if want_lse and lse is None:
+        lse = torch.empty(q.shape[0], n_head, dtype=torch.float32, device=q.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, q.stride(0), kv_stride, out.stride(0), scale,
+                       causal=1 if causal else 0)
+    need = _lib.decode_workspace_bytes(d, batch, max(kv_len))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(_lib.decode_raw(d, list(kv_len), q.data_ptr(), [t.data_ptr() for t in k_caches],
+                               [t.data_ptr() for t in v_caches], out.data_ptr(),
+                               lse.data_ptr() if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
+                               _stream()))
+    return out, lse

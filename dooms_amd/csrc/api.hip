@@ -1,0 +1,220 @@
+// C ABI of the attention hot path (include/mx_attn.h): argument checks, split planning and kernel launches.
+//
+// Error behaviour follows the reference's C API (include/dooms/dooms_c.h:24-36 in dooms.cpp 0.6.1): an integer code with
+// dooms_code's numbering, never an abort, and a thread-local message for the last failure. Every check runs on the host
+// before anything is enqueued, so a rejected call leaves the stream untouched.
+#include "mx_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+
+#include "mx_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const char * fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks shared by prefill and decode.
+int32_t check_desc(const mx_attn_desc * d) {
+    if (!d) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
+    if (d->reserved != 0) return fail(MX_ATTN_INVALID_ARGUMENT, "desc->reserved must be 0");
+    if (d->n_head < 1 || d->n_head_kv < 1)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "n_head (%d) and n_head_kv (%d) must be >= 1", d->n_head, d->n_head_kv);
+    if (d->n_head % d->n_head_kv != 0)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "n_head (%d) is not a multiple of n_head_kv (%d)", d->n_head, d->n_head_kv);
+    if (d->head_dim < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "head_dim (%d) must be >= 1", d->head_dim);
+    if (d->head_dim != 64 && d->head_dim != 128)
+        return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is not supported (64 or 128)", d->head_dim);
+    if (d->n_q < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_q (%d) must be >= 0", d->n_q);
+    if (d->causal != 0 && d->causal != 1) return fail(MX_ATTN_INVALID_ARGUMENT, "causal must be 0 or 1");
+    if (!std::isfinite(d->scale)) return fail(MX_ATTN_INVALID_ARGUMENT, "scale is not finite");
+    const int64_t qw = (int64_t)d->n_head * d->head_dim, kvw = (int64_t)d->n_head_kv * d->head_dim;
+    if (d->q_stride < qw) return fail(MX_ATTN_INVALID_ARGUMENT, "q_stride (%lld) < n_head * head_dim (%lld)", (long long)d->q_stride, (long long)qw);
+    if (d->out_stride < qw)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "out_stride (%lld) < n_head * head_dim (%lld)", (long long)d->out_stride, (long long)qw);
+    if (d->kv_stride < kvw)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "kv_stride (%lld) < n_head_kv * head_dim (%lld)", (long long)d->kv_stride, (long long)kvw);
+    if (d->q_stride % 8 || d->kv_stride % 8 || d->out_stride % 8)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "strides must be multiples of 8 elements (16-byte rows)");
+    return MX_ATTN_OK;
+}
+
+int32_t hip_status(hipError_t e, const char * what) {
+    if (e == hipSuccess) return MX_ATTN_OK;
+    return fail(MX_ATTN_INTERNAL, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Decode split plan. Splits are a multiple of kDecodeChunkQuantum keys, sized so that the launch has about
+// target_workgroups() workgroups (2 per CU on MI355X's 256 CUs, 8 waves per CU) and never more splits per sequence
+// than ceil(len / quantum), which bounds the workspace by the longest sequence alone.
+int target_workgroups() {
+    const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
+    const int v = s ? std::atoi(s) : 0;
+    return v > 0 ? v : 512;
+}
+
+struct DecodeShape {
+    int rows, rt, n_rowtiles;
+};
+
+DecodeShape decode_shape(const mx_attn_desc * d) {
+    DecodeShape s;
+    s.rows = d->n_q * (d->n_head / d->n_head_kv);
+    s.rt = mx::decode_rows_per_tile(s.rows);
+    s.n_rowtiles = (s.rows + s.rt - 1) / s.rt;
+    return s;
+}
+
+size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len) {
+    const DecodeShape s = decode_shape(d);
+    const int64_t seqs = std::min<int64_t>(batch, mx::kMaxSeqPerLaunch);
+    const int64_t max_split = ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum;
+    if (max_split <= 1) return 0;
+    return (size_t)(seqs * d->n_head_kv * s.n_rowtiles * max_split * s.rt * (d->head_dim + 4) * (int64_t)sizeof(float));
+}
+
+}  // namespace
+
+extern "C" {
+
+MX_ATTN_API int32_t mx_attn_abi_version(void) { return MX_ATTN_ABI_VERSION; }
+
+MX_ATTN_API const char * mx_attn_last_error(void) { return g_last_error.c_str(); }
+
+MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * q, const uint16_t * k_cache, const uint16_t * v_cache,
+                                    uint16_t * out, float * lse, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    const mx_attn_desc & d = *desc;
+    if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
+    if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
+    if (d.n_q == 0) return MX_ATTN_OK;
+    const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
+    if (n_kv > INT32_MAX) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 + n_q overflows");
+    if (d.causal && n_kv < (int64_t)d.p0 + d.n_q)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "causal prefill needs n_kv (%lld) >= p0 + n_q (%lld)", (long long)n_kv, (long long)d.p0 + d.n_q);
+    if (!q || !k_cache || !v_cache || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must not be null");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must be 16-byte aligned");
+    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
+
+    mx::PrefillParams p;
+    p.q = reinterpret_cast<const mx::half_t *>(q);
+    p.k = reinterpret_cast<const mx::half_t *>(k_cache);
+    p.v = reinterpret_cast<const mx::half_t *>(v_cache);
+    p.out = reinterpret_cast<mx::half_t *>(out);
+    p.lse = lse;
+    p.q_stride = d.q_stride;
+    p.kv_stride = d.kv_stride;
+    p.out_stride = d.out_stride;
+    p.n_head = d.n_head;
+    p.n_head_kv = d.n_head_kv;
+    p.group = d.n_head / d.n_head_kv;
+    p.n_q = d.n_q;
+    p.p0 = d.p0;
+    p.n_kv = (int32_t)n_kv;
+    p.causal = d.causal;
+    p.n_qtiles = (d.n_q + mx::kPrefillRows - 1) / mx::kPrefillRows;
+    p.scale_log2 = d.scale * 1.4426950408889634f;
+    return hip_status(mx::launch_prefill(p, d.head_dim, static_cast<hipStream_t>(stream)), "prefill launch");
+}
+
+MX_ATTN_API size_t mx_attn_decode_workspace_bytes(const mx_attn_desc * desc, int32_t batch, int32_t max_kv_len) {
+    if (check_desc(desc)) return 0;
+    if (batch < 1 || max_kv_len < 0) {
+        fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1 and max_kv_len (%d) >= 0", batch, max_kv_len);
+        return 0;
+    }
+    return decode_ws_bytes(desc, batch, max_kv_len);
+}
+
+MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const uint16_t * q,
+                                   const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out, float * lse,
+                                   void * workspace, size_t ws_bytes, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    const mx_attn_desc & d = *desc;
+    if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
+    if (d.n_q == 0) return MX_ATTN_OK;
+    if (!kv_len || !k_caches || !v_caches) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len, k_caches and v_caches must not be null");
+    if (!q || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must not be null");
+    if (!aligned16(q) || !aligned16(out)) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
+    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
+    int32_t max_len = 0;
+    for (int32_t b = 0; b < batch; b++) {
+        const int32_t n = kv_len[b];
+        if (n < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d: every sequence needs at least one key", b, n);
+        if (d.causal && n < d.n_q)
+            return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d < n_q = %d: causal rows must all be in the cache", b, n, d.n_q);
+        if (!k_caches[b] || !v_caches[b]) return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d are null", b);
+        if (!aligned16(k_caches[b]) || !aligned16(v_caches[b]))
+            return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d must be 16-byte aligned", b);
+        max_len = std::max(max_len, n);
+    }
+    const size_t need = decode_ws_bytes(desc, batch, max_len);
+    if (need > 0 && !workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null but %zu bytes are needed", need);
+    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+    if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+
+    const DecodeShape s = decode_shape(desc);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int32_t b0 = 0; b0 < batch; b0 += mx::kMaxSeqPerLaunch) {
+        const int n_seq = std::min<int32_t>(mx::kMaxSeqPerLaunch, batch - b0);
+        mx::DecodeParams p;
+        p.q = reinterpret_cast<const mx::half_t *>(q);
+        p.out = reinterpret_cast<mx::half_t *>(out);
+        p.lse = lse;
+        p.part = static_cast<float *>(workspace);
+        p.q_stride = d.q_stride;
+        p.kv_stride = d.kv_stride;
+        p.out_stride = d.out_stride;
+        p.n_head = d.n_head;
+        p.n_head_kv = d.n_head_kv;
+        p.group = d.n_head / d.n_head_kv;
+        p.n_q = d.n_q;
+        p.causal = d.causal;
+        p.rows = s.rows;
+        p.n_rowtiles = s.n_rowtiles;
+        p.seq0 = b0;
+        p.scale_log2 = d.scale * 1.4426950408889634f;
+        // split plan: total key-work of the launch over the target workgroup count, in whole quanta
+        int64_t keys = 0;
+        for (int i = 0; i < n_seq; i++) keys += kv_len[b0 + i];
+        const int64_t work = keys * d.n_head_kv * s.n_rowtiles;
+        const int64_t quantum = mx::kDecodeChunkQuantum;
+        int64_t chunk = (work + target_workgroups() - 1) / target_workgroups();
+        chunk = std::max<int64_t>(quantum, (chunk + quantum - 1) / quantum * quantum);
+        p.chunk = (int32_t)std::min<int64_t>(chunk, INT32_MAX / 2);
+        p.max_split = 1;
+        for (int i = 0; i < n_seq; i++) {
+            const int32_t n = kv_len[b0 + i];
+            p.seq[i].k = reinterpret_cast<const mx::half_t *>(k_caches[b0 + i]);
+            p.seq[i].v = reinterpret_cast<const mx::half_t *>(v_caches[b0 + i]);
+            p.seq[i].len = n;
+            p.seq[i].n_split = (int32_t)((n + p.chunk - 1) / p.chunk);
+            p.max_split = std::max(p.max_split, p.seq[i].n_split);
+        }
+        for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
+        if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, st), "decode launch")) return rc;
+    }
+    return MX_ATTN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Kernel parameter blocks and launchers shared between the C ABI layer (api.hip) and the kernels. Parameters travel by
+// value as kernel arguments, so a call needs no device-side metadata buffer and can be captured in a HIP graph.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx {
+
+typedef _Float16 half_t;
+
+// Sequences per decode launch: their cache pointers, lengths and split counts ride in the kernel arguments.
+constexpr int kMaxSeqPerLaunch = 32;
+// Keys per split are a multiple of this (4 waves x 32-key blocks), and never fewer.
+constexpr int kDecodeChunkQuantum = 128;
+
+struct DecodeSeq {
+    const half_t * k;
+    const half_t * v;
+    int32_t len;      // keys in the cache
+    int32_t n_split;  // splits of `chunk` keys covering them
+};
+
+struct DecodeParams {
+    const half_t * q;
+    half_t * out;
+    float * lse;
+    float * part;  // [n_seq][n_head_kv][n_rowtiles][max_split][RT][head_dim + 4] f32: acc[head_dim], m, l, 2 spare
+    int64_t q_stride, kv_stride, out_stride;
+    int32_t n_head, n_head_kv, group, n_q, causal;
+    int32_t rows;        // n_q * group: query rows that share one key/value head
+    int32_t n_rowtiles;  // ceil(rows / RT)
+    int32_t chunk;       // keys per split
+    int32_t max_split;   // max over the launch's sequences of n_split
+    int32_t seq0;        // index of the launch's first sequence in the caller's batch (query/output rows)
+    float scale_log2;    // scale * log2(e): scores are kept in base-2 units
+    DecodeSeq seq[kMaxSeqPerLaunch];
+};
+
+struct PrefillParams {
+    const half_t * q;
+    const half_t * k;
+    const half_t * v;
+    half_t * out;
+    float * lse;
+    int64_t q_stride, kv_stride, out_stride;
+    int32_t n_head, n_head_kv, group, n_q, p0, n_kv, causal, n_qtiles;
+    float scale_log2;
+};
+
+int decode_rows_per_tile(int rows);
+hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, hipStream_t stream);
+
+constexpr int kPrefillRows = 128;  // query rows per workgroup
+hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
+
+}  // namespace mx

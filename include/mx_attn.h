@@ -1,0 +1,139 @@
+/*
+ * mx_attn.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in for the attention step of dooms.cpp's fixed-model decoders. The reference encodes its attention as Metal
+ * dispatches with a parameter struct and raw buffers; this header replaces them with plain C entry points that take a
+ * descriptor, device pointers and a HIP stream:
+ *
+ *   reference (file:line, relative to the dooms.cpp 0.6.1 tree)                      replaced by
+ *   -------------------------------------------------------------------------------   -----------------------------
+ *   attention_prefill<64|128>  src/backend/metal/llama_kernels.h:640-769,              mx_attn_prefill
+ *       dispatched by MetalLlamaDecoder::Impl::attention                               (causal GQA, chunk offset p0)
+ *       src/backend/metal/metal_llama_decoder.mm:284-296
+ *   attention (per-query causal)  llama_kernels.h:552-630, dispatched at               mx_attn_decode (n_q rows,
+ *       metal_llama_decoder.mm:298-306 and metal_whisper_decoder.mm:167-203            causal = 1)
+ *   attention_split + attention_combine  llama_kernels.h:856-929, dispatched at        mx_attn_decode (split-KV +
+ *       metal_llama_decoder.mm:252-271 and metal_whisper_decoder.mm:205-225            log-sum-exp merge)
+ *   partial buffer split_part  metal_llama_decoder.mm:672-677                          mx_attn_decode_workspace_bytes
+ *   dooms_last_error / dooms_code  include/dooms/dooms_c.h:24-36                       mx_attn_last_error / MX_ATTN_*
+ *   AttnParams / SplitParams  llama_kernels.h:496-507, 844-854                         mx_attn_desc
+ *
+ * What the boundary takes over from the reference and what it leaves to the caller:
+ *   - Q, K, V and the output are IEEE binary16 (passed as uint16_t bit patterns, so the header needs no half type);
+ *     scores, the softmax statistics and the accumulation are f32. The reference keeps q/out in f32 and rounds q to half
+ *     inside the prefill kernel (llama_kernels.h:660); here the caller hands over half already.
+ *   - Rotary embedding and the cache append (rope_store, llama_kernels.h:520-545) happen before the call: K/V rows for
+ *     every position the call reads are already in the caches, Q is already rotated.
+ *   - Caches follow the reference layout: row `pos` of a layer's cache holds n_head_kv * head_dim halves (head kvh at
+ *     column kvh * head_dim), consecutive rows kv_stride elements apart (metal_llama_decoder.mm:664,
+ *     llama_kernels.h:535,593). Query row r holds n_head * head_dim halves, head h at column h * head_dim; rows
+ *     q_stride apart. Output rows likewise with out_stride.
+ *   - Query head h reads key/value head h / (n_head / n_head_kv) (llama_kernels.h:560,656,873).
+ *
+ * Threading: every call is asynchronous and ordered on `stream`; nothing inside synchronizes with the host. Calls on
+ * distinct streams with distinct output/workspace buffers may run concurrently. The library allocates no device memory.
+ *
+ * Errors: entry points return one of the MX_ATTN_* codes (numbering of dooms_code, dooms_c.h:24-33) and never abort; the
+ * message of the last failure on the calling thread is returned by mx_attn_last_error().
+ */
+#ifndef MX_ATTN_H
+#define MX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MX_ATTN_API __attribute__((visibility("default")))
+#define MX_ATTN_ABI_VERSION 1
+
+/* Return codes: the numbering of dooms_code (include/dooms/dooms_c.h:24-33). */
+#define MX_ATTN_OK 0
+#define MX_ATTN_INVALID_ARGUMENT 1    /* null pointer, bad stride, n_head % n_head_kv != 0, kv_len < n_q, ... */
+#define MX_ATTN_UNSUPPORTED 4         /* head_dim not in {64, 128}, or a GQA group / batch this build does not run */
+#define MX_ATTN_RESOURCE_EXHAUSTED 5  /* the workspace is smaller than mx_attn_decode_workspace_bytes asks for */
+#define MX_ATTN_INTERNAL 7            /* the HIP runtime reported an error (launch failure, ...) */
+
+/* A HIP stream (hipStream_t); NULL is the legacy default stream. */
+typedef void * mx_attn_stream;
+
+/*
+ * One attention problem: a superset of the reference's AttnParams (llama_kernels.h:496-507) without the rotary fields,
+ * plus the non-causal key count of SplitParams (llama_kernels.h:844-854).
+ */
+typedef struct mx_attn_desc {
+    int32_t n_head;      /* query heads */
+    int32_t n_head_kv;   /* key/value heads; n_head % n_head_kv == 0 */
+    int32_t head_dim;    /* 64 or 128 */
+    int32_t n_q;         /* query rows (per sequence for mx_attn_decode) */
+    int32_t p0;          /* mx_attn_prefill: cache position of query row 0 (the chunk offset); decode: ignored */
+    int32_t n_kv;        /* mx_attn_prefill: keys in the cache (0 means p0 + n_q); decode: ignored (kv_len[]) */
+    int32_t causal;      /* 1: query row t sees keys j <= p0 + t (prefill) or j <= kv_len - n_q + t (decode); 0: all */
+    int32_t reserved;    /* must be 0 */
+    int64_t q_stride;    /* elements between query rows   (>= n_head * head_dim) */
+    int64_t kv_stride;   /* elements between cache rows   (>= n_head_kv * head_dim) */
+    int64_t out_stride;  /* elements between output rows  (>= n_head * head_dim) */
+    float scale;         /* score scale, normally 1 / sqrt(head_dim); 0 is valid (uniform attention) */
+} mx_attn_desc;
+
+/* MX_ATTN_ABI_VERSION of the library. */
+MX_ATTN_API int32_t mx_attn_abi_version(void);
+
+/* Message of the last failure on this thread ("" if none). Replaces dooms_last_error (dooms_c.h:36). */
+MX_ATTN_API const char * mx_attn_last_error(void);
+
+/*
+ * Prefill (prompt chunk) flash attention. Replaces attention_prefill<64|128> (llama_kernels.h:640-769) as dispatched by
+ * MetalLlamaDecoder::Impl::attention(enc, cache_off, M, p0, fused_rope = false) (metal_llama_decoder.mm:284-296), and the
+ * reference's chunked prompt loop against the growing cache (metal_llama_decoder.mm:703-723).
+ *
+ *   q       [n_q rows][q_stride]            query row t is at position p0 + t
+ *   k_cache [n_kv rows][kv_stride]          keys 0 .. n_kv - 1 (for a causal chunk n_kv = p0 + n_q)
+ *   v_cache [n_kv rows][kv_stride]
+ *   out     [n_q rows][out_stride]          softmax(scale * q k^T + mask) v per head, rounded to half
+ *   lse     [n_q rows][n_head] f32, or NULL: natural-log log-sum-exp of the scaled, masked scores of each row
+ *
+ * All pointers are device pointers. No workspace is needed.
+ */
+MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * q, const uint16_t * k_cache,
+                                    const uint16_t * v_cache, uint16_t * out, float * lse, mx_attn_stream stream);
+
+/*
+ * Decode attention over per-sequence caches: split-KV over the keys, then a log-sum-exp merge of the splits. Replaces the
+ * per-query `attention` kernel (llama_kernels.h:552-630; decode dispatch metal_llama_decoder.mm:298-306, Whisper self
+ * attention metal_whisper_decoder.mm:167-203) and attention_split + attention_combine (llama_kernels.h:856-929; long
+ * decode metal_llama_decoder.mm:252-271, Whisper cross-attention metal_whisper_decoder.mm:205-225).
+ *
+ *   batch            sequences (>= 1)
+ *   kv_len           HOST array [batch]: keys in sequence b's cache (>= n_q when causal, >= 1 otherwise)
+ *   q                device, [batch * n_q rows][q_stride]: row b * n_q + t is query t of sequence b
+ *   k_caches         HOST array [batch] of device pointers to sequence b's key cache ([kv_len[b]][kv_stride])
+ *   v_caches         HOST array [batch] of device pointers to sequence b's value cache
+ *                    (entries may repeat: beam search over one shared cross-attention cache)
+ *   out              device, [batch * n_q rows][out_stride]
+ *   lse              device, [batch * n_q rows][n_head] f32 natural-log LSE, or NULL
+ *   workspace        device scratch of at least mx_attn_decode_workspace_bytes(desc, batch, max_b kv_len[b]) bytes,
+ *                    256-byte aligned; its contents on entry do not matter
+ *
+ * With causal = 1 query row t of sequence b attends keys 0 .. kv_len[b] - n_q + t (the decoder's prompt rows appended
+ * at the end of the cache, as the reference's per-query kernel with p0 = kv_len - n_q); with causal = 0 every row
+ * attends all kv_len[b] keys (cross-attention, or one decode row). desc->p0 and desc->n_kv are ignored.
+ */
+MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const uint16_t * q,
+                                   const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out,
+                                   float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream);
+
+/*
+ * Workspace bytes mx_attn_decode needs for `batch` sequences of at most max_kv_len keys (the reference sizes its
+ * split_part buffer the same way from n_ctx: metal_llama_decoder.mm:672-677). Returns 0 and sets the last error for an
+ * invalid descriptor.
+ */
+MX_ATTN_API size_t mx_attn_decode_workspace_bytes(const mx_attn_desc * desc, int32_t batch, int32_t max_kv_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MX_ATTN_H */

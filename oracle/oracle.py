@@ -1,0 +1,80 @@
+"""numpy binding of liboracle.so (test infrastructure only; see oracle.c for what each function restates)."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_DIR, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _DIR], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i32, i64 = ctypes.c_int32, ctypes.c_int64
+        L.oracle_attention_f64.restype = ctypes.c_int
+        L.oracle_attention_f64.argtypes = [i32, i32, i32, i32, i32, i32, i32, ctypes.c_double, P, i64, P, P, i64,
+                                           P, i64, P]
+        L.oracle_cpu_attend_f32.restype = ctypes.c_int
+        L.oracle_cpu_attend_f32.argtypes = [i32, i32, i32, i32, i32, i32, i32, ctypes.c_float, P, i64, P, P, i64,
+                                            P, i64, i32]
+        L.oracle_f16_to_f32.restype = None
+        L.oracle_f16_to_f32.argtypes = [P, P, i64]
+        _lib = L
+    return _lib
+
+
+def _f16(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.float16 or a.ndim != 2:
+        raise ValueError("expected a 2-D float16 array")
+    return a
+
+
+def attention_f64(q, k, v, n_head, n_head_kv, head_dim, scale, p0=0, causal=True, n_kv=None):
+    """Brute-force f64 attention of query rows q [n_q][..] over caches k/v [n_kv][..] (float16 arrays).
+    Returns (out [n_q][n_head*hd] f64, lse [n_q][n_head] f64)."""
+    q, k, v = _f16(q), _f16(k), _f16(v)
+    n_q = q.shape[0]
+    n_kv = k.shape[0] if n_kv is None else n_kv
+    out = np.zeros((n_q, n_head * head_dim), np.float64)
+    lse = np.zeros((n_q, n_head), np.float64)
+    rc = lib().oracle_attention_f64(n_head, n_head_kv, head_dim, n_q, p0, n_kv, 1 if causal else 0, float(scale),
+                                    q.ctypes.data, q.shape[1], k.ctypes.data, v.ctypes.data, k.shape[1],
+                                    out.ctypes.data, out.shape[1], lse.ctypes.data)
+    if rc:
+        raise ValueError(f"oracle_attention_f64 rejected the arguments ({rc})")
+    return out, lse
+
+
+def cpu_attend_f32(q, k, v, n_head, n_head_kv, head_dim, scale, p0=0, causal=True, n_kv=None, n_threads=1):
+    """The restated reference CPU attention on float32 arrays (convert f16 with astype outside any timing)."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    n_q = q.shape[0]
+    n_kv = k.shape[0] if n_kv is None else n_kv
+    out = np.zeros((n_q, n_head * head_dim), np.float32)
+    rc = lib().oracle_cpu_attend_f32(n_head, n_head_kv, head_dim, n_q, p0, n_kv, 1 if causal else 0, float(scale),
+                                     q.ctypes.data, q.shape[1], k.ctypes.data, v.ctypes.data, k.shape[1],
+                                     out.ctypes.data, out.shape[1], n_threads)
+    if rc:
+        raise ValueError(f"oracle_cpu_attend_f32 failed ({rc})")
+    return out
+
+
+def f16_to_f32(a):
+    """Exact binary16 -> binary32 conversion by the oracle's own routine (checked against numpy's)."""
+    a = np.ascontiguousarray(a, dtype=np.float16)
+    out = np.empty(a.shape, np.float32)
+    lib().oracle_f16_to_f32(a.ctypes.data, out.ctypes.data, a.size)
+    return out

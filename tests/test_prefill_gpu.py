@@ -1,0 +1,141 @@
+"""Parity of mx_attn_prefill (causal GQA flash attention, MFMA) with the f64 oracle, through the C ABI.
+
+Reference: attention_prefill<64|128> (llama_kernels.h:632-769) as dispatched by MetalLlamaDecoder::Impl::attention
+(metal_llama_decoder.mm:284-296), and the chunked prompt loop against the growing cache (metal_llama_decoder.mm:703-723).
+Reference tests mirrored: flash prefill on a 45-token prompt in chunks of 20 (test_metal_llama_decoder.cpp:497-532),
+chunk-size invariance, non-causal MHA (test_backend_ggml.cpp:677-745).
+"""
+import numpy as np
+import pytest
+import torch
+
+from dooms_amd import attention as A
+from helpers import assert_close, normal_f16, ref_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def make(device, seed, n_q_total, n_head, n_head_kv, hd, sigma=1.0, kv_pad=0, q_pad=0):
+    rng = np.random.default_rng(seed)
+    q = normal_f16(rng, (n_q_total, n_head * hd + q_pad), sigma)
+    k = normal_f16(rng, (n_q_total, n_head_kv * hd + kv_pad), sigma)
+    v = normal_f16(rng, (n_q_total, n_head_kv * hd + kv_pad), sigma)
+    return q, k, v, [torch.from_numpy(a).to(device) for a in (q, k, v)]
+
+
+def check_prefill(device, seed, N, n_head, n_head_kv, hd, rows=None, heads=None, causal=True, sigma=1.0, scale=None,
+                  kv_pad=0, q_pad=0, chunk=None):
+    q, k, v, (dq, dk, dv) = make(device, seed, N, n_head, n_head_kv, hd, sigma, kv_pad, q_pad)
+    scale = 1.0 / np.sqrt(hd) if scale is None else scale
+    if chunk is None:
+        out, lse = A.prefill(dq, dk, dv, n_head=n_head, n_head_kv=n_head_kv, head_dim=hd, causal=causal,
+                             scale=scale, want_lse=True)
+    else:  # chunks at p0 = 0, chunk, 2 chunk, ... against the growing cache
+        out = torch.empty(N, n_head * hd, dtype=torch.float16, device=device)
+        lse = torch.empty(N, n_head, dtype=torch.float32, device=device)
+        for p0 in range(0, N, chunk):
+            m = min(chunk, N - p0)
+            A.prefill(dq[p0:p0 + m], dk[:p0 + m], dv[:p0 + m], n_head=n_head, n_head_kv=n_head_kv, head_dim=hd,
+                      p0=p0, scale=scale, out=out[p0:p0 + m], lse=lse[p0:p0 + m])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    gl = lse.cpu().numpy()
+    rows = np.arange(N) if rows is None else np.asarray(rows)
+    heads = np.arange(n_head) if heads is None else np.asarray(heads)
+    ro, rl = ref_attention(q, k, v, n_head, n_head_kv, hd, scale, causal=causal, rows=rows, heads=heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    assert_close(got[rows][:, cols], ro, hd, f"N={N}", gl[rows][:, heads], rl)
+    return got, gl
+
+
+def test_tiny_gqa(device):
+    check_prefill(device, 1, 45, 4, 2, 64)
+
+
+def test_tiny_gqa_chunks_of_20(device):
+    # test_metal_llama_decoder.cpp:497-532: a 45-token prompt through the flash kernel in chunks of 20
+    check_prefill(device, 1, 45, 4, 2, 64, chunk=20)
+
+
+@pytest.mark.parametrize("N", [1, 2, 31, 32, 63, 64, 65, 127, 128, 129, 200, 257])
+def test_ragged_lengths(device, N):
+    check_prefill(device, 100 + N, N, 4, 1, 128)
+
+
+# cfg2: Qwen2.5-0.5B prefill of a 512-token prompt
+def test_qwen05b_prefill_512(device):
+    check_prefill(device, 2, 512, 14, 2, 64)
+
+
+@pytest.mark.parametrize("chunk", [20, 128, 200, 512])
+def test_chunked_equals_oracle(device, chunk):
+    check_prefill(device, 3, 700, 14, 2, 64, rows=list(range(0, 700, 7)) + [699], chunk=chunk)
+
+
+def test_noncausal_mha(device):
+    # the IR SelfAttention shape class (non-causal MHA, test_backend_ggml.cpp:680)
+    check_prefill(device, 4, 210, 16, 16, 64, causal=False)
+
+
+@pytest.mark.parametrize("scale", [0.0, 0.1, 3.0])
+def test_scale_semantics(device, scale):
+    check_prefill(device, 5, 150, 4, 2, 64, scale=scale)
+
+
+def test_padded_strides(device):
+    # q and caches inside wider rows (a fused q|k|v buffer, say)
+    check_prefill(device, 6, 300, 8, 2, 128, kv_pad=256, q_pad=512)
+
+
+# cfg5 shape class: Qwen2.5-7B (28q/4kv, hd 128), sigma 0.5, in 2048-query chunks; reduced length here, full 32k below
+def test_qwen7b_chunked_4096(device):
+    rows = [0, 1, 2047, 2048, 2049, 3000, 4095]
+    check_prefill(device, 7, 4096, 28, 4, 128, rows=rows, sigma=0.5, chunk=2048)
+
+
+def test_qwen7b_32k_chunked_equals_one_shot(device):
+    """cfg5 at full size: 32768 causal tokens in 16 chunks of 2048 against the growing cache.
+
+    Size-independent properties: chunked == one-shot (bitwise: the kernel visits the same key blocks for every row
+    when chunk boundaries are multiples of its 128-row tile), and sampled rows against the f64 oracle.
+    """
+    N, nh, nkv, hd = 32768, 28, 4, 128
+    rng = np.random.default_rng(5)
+    q = normal_f16(rng, (N, nh * hd), 0.5)
+    k = normal_f16(rng, (N, nkv * hd), 0.5)
+    v = normal_f16(rng, (N, nkv * hd), 0.5)
+    dq, dk, dv = (torch.from_numpy(a).to(device) for a in (q, k, v))
+    one, lse1 = A.prefill(dq, dk, dv, n_head=nh, n_head_kv=nkv, head_dim=hd, want_lse=True)
+    out = torch.empty_like(one)
+    lse = torch.empty_like(lse1)
+    for p0 in range(0, N, 2048):
+        A.prefill(dq[p0:p0 + 2048], dk[:p0 + 2048], dv[:p0 + 2048], n_head=nh, n_head_kv=nkv, head_dim=hd, p0=p0,
+                  out=out[p0:p0 + 2048], lse=lse[p0:p0 + 2048])
+    torch.cuda.synchronize()
+    assert torch.equal(one, out)
+    assert torch.equal(lse1, lse)
+    rows = [0, 5, 2047, 16384, 30000, 32767]
+    heads = [0, 7, 27]
+    ro, rl = ref_attention(q, k, v, nh, nkv, hd, 1.0 / np.sqrt(hd), rows=rows, heads=heads)
+    got = out.cpu().numpy().astype(np.float64)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    assert_close(got[rows][:, cols], ro, hd, "32k", lse.cpu().numpy()[rows][:, heads], rl)
+
+
+def test_one_row_per_key_closed_form(device):
+    # one key: O = v0 exactly (up to f16 rounding of v0 itself)
+    rng = np.random.default_rng(8)
+    dq, dk, dv = (torch.from_numpy(normal_f16(rng, (1, 128))).to(device) for _ in range(3))
+    out, lse = A.prefill(dq, dk, dv, n_head=1, n_head_kv=1, head_dim=128, want_lse=True)
+    assert torch.equal(out, dv)
+
+
+def test_equal_keys_mean_of_v(device):
+    rng = np.random.default_rng(9)
+    N, hd = 300, 64
+    q = torch.from_numpy(normal_f16(rng, (N, hd))).to(device)
+    k = torch.from_numpy(np.tile(normal_f16(rng, (1, hd)), (N, 1))).to(device)
+    vn = normal_f16(rng, (N, hd))
+    out, _ = A.prefill(q, k, torch.from_numpy(vn).to(device), n_head=1, n_head_kv=1, head_dim=hd)
+    cm = np.cumsum(vn.astype(np.float64), axis=0) / np.arange(1, N + 1)[:, None]
+    np.testing.assert_allclose(out.cpu().numpy().astype(np.float64), cm, atol=2e-3, rtol=1e-2)
