@@ -1,0 +1,404 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention hot path on one MI355X: prints ONE JSON line.
+
+Headline (value): decode attention at the Llama-3-8B shape (32 q / 8 kv heads, head_dim 128, batch 1, 8192-token f16
+KV cache). One step = the decode attention of all 32 layers, each layer with its own K/V buffers (32 x 33.6 MB = 1.07 GB,
+well past the 256 MB Infinity Cache, so every step streams K/V from HBM). value = algorithmic bytes / time in GB/s.
+
+Beside it (same JSON line): prefill TFLOP/s on the Qwen2.5-7B 32k-token causal prompt in 2048-query chunks, the other
+BASELINE configurations, a same-run streaming-copy bandwidth, and the reference's CPU attention (restated in
+oracle/oracle.c) timed on this host's cores on a bounded sample.
+
+Timing: the value pass replays a HIP graph of one step (the decode step is 32 launches of a few microseconds, too short
+to issue from Python one by one); K steps are bracketed by synchronize() on both sides and timed with events on the
+stream the kernels run on. Per-kernel durations (roofline) come from event pairs around eager launches queued behind a
+busy kernel, so host issue time is not counted.
+
+Algorithmic work (what `achieved` divides):
+  decode bytes per (sequence, layer) = 2 * L * n_kv * hd * 2 (K+V, f16, each byte once) + 2 * n_head * hd * 2 (Q, O)
+  prefill FLOPs per head = 4 * hd * (unmasked (query, key) pairs); a chunk of M rows at offset p0 has M p0 + M(M+1)/2.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 MFMA
+METRIC = "decode-attn achieved HBM GB/s + prefill-attn TFLOP/s (fraction of peak)"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget per leg")
+    ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
+    return ap.parse_args()
+
+
+def busy(torch, ms=30.0):
+    """Keeps the stream busy for about `ms` so that launches queued behind it run back to back."""
+    try:
+        torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
+    except Exception:
+        a = torch.empty(4096, 4096, dtype=torch.float16, device="cuda")
+        for _ in range(int(ms / 0.15) + 1):
+            a @ a
+
+
+def time_graph(torch, step, steps, warmup):
+    """Captures step() into a HIP graph and returns ms per replay over `steps` replays (after `warmup`)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # eager once on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, g
+
+
+def time_launches(torch, launches, reps=1):
+    """Per-launch GPU durations (ms) of the callables in `launches`, queued behind a busy kernel."""
+    torch.cuda.synchronize()
+    busy(torch, 20.0 + 0.05 * len(launches) * reps)
+    evs = []
+    for _ in range(reps):
+        for f in launches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            f()
+            b.record()
+            evs.append((a, b))
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def decode_bytes(L, n_head, n_kv, hd):
+    return 2 * L * n_kv * hd * 2 + 2 * n_head * hd * 2
+
+
+def prefill_flops(M, p0, n_head, hd):
+    return 4 * hd * n_head * (M * p0 + M * (M + 1) // 2)
+
+
+class DecodeProblem:
+    """Per-layer caches and the raw C-ABI launch of one decode attention call per layer."""
+
+    def __init__(self, torch, gen, n_head, n_kv, hd, lens, layers, n_q=1, causal=False, shared=False):
+        from dooms_amd import _lib
+        self.torch, self._lib = torch, _lib
+        self.n_head, self.n_kv, self.hd, self.lens, self.layers, self.n_q = n_head, n_kv, hd, list(lens), layers, n_q
+        B = len(lens)
+        dev = "cuda"
+        self.q = torch.randn(B * n_q, n_head * hd, generator=gen, device=dev).half()
+        self.out = torch.empty(B * n_q, n_head * hd, dtype=torch.float16, device=dev)
+        self.k, self.v = [], []
+        for _ in range(layers):
+            ks, vs = [], []
+            for b, L in enumerate(lens):
+                if shared and b > 0:
+                    ks.append(ks[0]), vs.append(vs[0])
+                    continue
+                ks.append(torch.randn(L, n_kv * hd, generator=gen, device=dev).half())
+                vs.append(torch.randn(L, n_kv * hd, generator=gen, device=dev).half())
+            self.k.append(ks), self.v.append(vs)
+        self.desc = _lib.make_desc(n_head, n_kv, hd, n_q, n_head * hd, n_kv * hd, n_head * hd, 1.0 / math.sqrt(hd),
+                                   causal=1 if causal else 0)
+        need = _lib.decode_workspace_bytes(self.desc, B, max(lens))
+        self.ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        _lib.check(_lib.decode_workspace_init(self.ws.data_ptr(), self.ws.numel(),
+                                              torch.cuda.current_stream().cuda_stream))
+        self.kp = [[t.data_ptr() for t in ks] for ks in self.k]
+        self.vp = [[t.data_ptr() for t in vs] for vs in self.v]
+        self.unique_bytes = sum(t.numel() * 2 for ks in self.k for t in set(ks)) * 2
+
+    def launch(self, layer):
+        _lib = self._lib
+        _lib.check(_lib.decode_raw(self.desc, self.lens, self.q.data_ptr(), self.kp[layer], self.vp[layer],
+                                   self.out.data_ptr(), 0, self.ws.data_ptr(), self.ws.numel(),
+                                   self.torch.cuda.current_stream().cuda_stream))
+
+    def step(self):
+        for l in range(self.layers):
+            self.launch(l)
+
+    def bytes_per_launch(self, shared=False):
+        kv = sum(2 * L * self.n_kv * self.hd * 2 for L in (self.lens[:1] if shared else self.lens))
+        return kv + len(self.lens) * self.n_q * 2 * self.n_head * self.hd * 2
+
+
+class PrefillProblem:
+    def __init__(self, torch, gen, n_head, n_kv, hd, N, chunk, layers=1, sigma=1.0):
+        from dooms_amd import _lib
+        self.torch, self._lib = torch, _lib
+        self.n_head, self.n_kv, self.hd, self.N, self.chunk, self.layers = n_head, n_kv, hd, N, chunk, layers
+        dev = "cuda"
+        self.q = [(torch.randn(N, n_head * hd, generator=gen, device=dev) * sigma).half() for _ in range(layers)]
+        self.k = [(torch.randn(N, n_kv * hd, generator=gen, device=dev) * sigma).half() for _ in range(layers)]
+        self.v = [(torch.randn(N, n_kv * hd, generator=gen, device=dev) * sigma).half() for _ in range(layers)]
+        self.out = torch.empty(N, n_head * hd, dtype=torch.float16, device=dev)
+        self.chunks = [(p0, min(chunk, N - p0)) for p0 in range(0, N, chunk)]
+        self.descs = [_lib.make_desc(n_head, n_kv, hd, M, n_head * hd, n_kv * hd, n_head * hd, 1.0 / math.sqrt(hd),
+                                     p0=p0, causal=1) for p0, M in self.chunks]
+        rs = n_head * hd * 2
+        self.qoff = [p0 * rs for p0, _ in self.chunks]
+
+    def launch(self, layer, ci):
+        _lib = self._lib
+        p0, _ = self.chunks[ci]
+        _lib.check(_lib.prefill_raw(self.descs[ci], self.q[layer].data_ptr() + self.qoff[ci], self.k[layer].data_ptr(),
+                                    self.v[layer].data_ptr(), self.out.data_ptr() + self.qoff[ci], 0,
+                                    self.torch.cuda.current_stream().cuda_stream))
+
+    def step(self):
+        for l in range(self.layers):
+            for ci in range(len(self.chunks)):
+                self.launch(l, ci)
+
+    def flops_per_layer(self):
+        return sum(prefill_flops(M, p0, self.n_head, self.hd) for p0, M in self.chunks)
+
+
+def cpu_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, avail
+
+
+def cpu_decode_baseline(torch, prob, budget_s, threads):
+    """The reference's CPU attention (oracle/oracle.c restatement) on the same decode workload, layer by layer until
+    the time budget is spent. Returns (GB/s, layers timed, seconds)."""
+    from oracle import oracle as O
+    q = prob.q.float().cpu().numpy()
+    hd, nh, nkv = prob.hd, prob.n_head, prob.n_kv
+    host = []
+    for l in range(min(prob.layers, 4)):  # the sample cycles over 4 layers' caches
+        host.append([(prob.k[l][b].float().cpu().numpy(), prob.v[l][b].float().cpu().numpy()) for b in range(len(prob.lens))])
+    done, t_total, nbytes = 0, 0.0, 0
+    while t_total < budget_s or done == 0:
+        kv = host[done % len(host)]
+        t0 = time.perf_counter()
+        for b, L in enumerate(prob.lens):
+            O.cpu_attend_f32(q[b:b + 1], kv[b][0], kv[b][1], nh, nkv, hd, 1.0 / math.sqrt(hd), causal=False,
+                             n_threads=threads)
+        t_total += time.perf_counter() - t0
+        nbytes += prob.bytes_per_launch()
+        done += 1
+    return nbytes / t_total / 1e9, done, t_total
+
+
+def cpu_prefill_baseline(torch, prob, budget_s, threads):
+    """The restated CPU attention on sampled query rows of the prefill workload: rows taken from the end of the prompt
+    (the most expensive ones) until the budget is spent; TFLOP/s over the unmasked pairs actually computed."""
+    from oracle import oracle as O
+    N, hd, nh, nkv = prob.N, prob.hd, prob.n_head, prob.n_kv
+    k = prob.k[0].float().cpu().numpy()
+    v = prob.v[0].float().cpu().numpy()
+    q = prob.q[0].float().cpu().numpy()
+    rows, t_total, flops = 0, 0.0, 0
+    step = 8
+    while t_total < budget_s or rows == 0:
+        t1 = N - rows
+        t0r = max(0, t1 - step)
+        t0 = time.perf_counter()
+        O.cpu_attend_f32(q[t0r:t1], k[:t1], v[:t1], nh, nkv, hd, 1.0 / math.sqrt(hd), p0=t0r, causal=True,
+                         n_threads=threads)
+        t_total += time.perf_counter() - t0
+        flops += sum(4 * hd * nh * (t + 1) for t in range(t0r, t1))
+        rows += t1 - t0r
+        if t0r == 0:
+            break
+    return flops / t_total / 1e12, rows, t_total
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: the attention hot path has no multi-GPU path here "
+                                   "(run with --gpus 1)", "n_gpus": args.gpus}))
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    from dooms_amd import _lib
+    _lib.lib()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    K, W = args.steps, args.warmup
+    result = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic"}
+    extra = {}
+
+    # same-run streaming copy (read + write), 1 GiB
+    a = torch.empty(1 << 29, dtype=torch.float16, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    extra["copy_GBps"] = round(2 * a.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del a, b
+
+    model, ncpu = cpu_info()
+    threads = max(1, min(16, ncpu))
+
+    if args.only in ("decode", "all"):
+        # ---- headline: cfg3 decode, batch 1, L = 8192, 32 layers per step ----
+        L = 8192
+        dp = DecodeProblem(torch, gen, 32, 8, 128, [L], layers=32)
+        ms, _ = time_graph(torch, dp.step, K, W)
+        bpl = dp.bytes_per_launch()
+        value = 32 * bpl / (ms * 1e-3) / 1e9
+        durs = time_launches(torch, [lambda l=l: dp.launch(l) for l in range(32)], reps=3)
+        avg = float(np.mean(durs))
+        achieved = bpl / (avg * 1e-3) / 1e9
+        result.update({
+            "value": round(value, 1), "ms_per_step": round(ms, 4),
+            "config": {"workload": "cfg3 Llama-3-8B decode attention: 32 q / 8 kv heads, head_dim 128, batch 1, "
+                                   "8192-token f16 KV cache, one query row; one step = 32 layers, each with its own "
+                                   "K/V (1.07 GB per step)",
+                       "batch": 1, "kv_len": L, "layers_per_step": 32, "n_head": 32, "n_head_kv": 8, "head_dim": 128,
+                       "timing": "HIP graph replay of the 32-launch step, events on the launch stream"},
+            "roofline": {"bound": "hbm", "kernel": "decode_split_kernel<128,4>", "achieved": round(achieved, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": None, "bytes_per_launch": bpl, "avg_launch_us": round(avg * 1e3, 3)},
+        })
+        if not args.no_cpu:
+            v1, n1, t1 = cpu_decode_baseline(torch, dp, args.cpu_seconds, threads)
+            v0, n0, t0 = cpu_decode_baseline(torch, dp, args.cpu_seconds / 4, 1)
+            result["cpu_baseline"] = {
+                "value": round(v1, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"{n1} layers of the same workload (batch 1, L=8192, 32/8 heads) through the restated "
+                          f"CpuWhisperDecoder::attend (f32, double sum), {threads} threads over (row, head) tasks, "
+                          f"{t1:.1f} s; host CPU: {model}, {ncpu} cores available",
+                "single_thread_value": round(v0, 3), "single_thread_sample": f"{n0} layers, {t0:.1f} s"}
+        del dp
+        torch.cuda.empty_cache()
+
+        # ---- cfg3 batched: lengths U[1024, 8192] by seed 3 ----
+        rng = np.random.default_rng(3)
+        for B in (4, 16):
+            lens = [int(x) for x in rng.integers(1024, 8193, size=B)]
+            layers = max(2, int(math.ceil(1.2e9 / (sum(lens) * 4096))))
+            bp = DecodeProblem(torch, gen, 32, 8, 128, lens, layers=layers)
+            ms_b, _ = time_graph(torch, bp.step, K, W)
+            extra[f"decode_b{B}"] = {"GBps": round(layers * bp.bytes_per_launch() / (ms_b * 1e-3) / 1e9, 1),
+                                     "us_per_layer": round(ms_b * 1e3 / layers, 2), "kv_lens": lens,
+                                     "layers_rotated": layers}
+            del bp
+            torch.cuda.empty_cache()
+
+        # ---- cfg1 Qwen2.5-0.5B decode (513 keys, 24 layers) ----
+        qp = DecodeProblem(torch, gen, 14, 2, 64, [513], layers=24)
+        ms_q, _ = time_graph(torch, qp.step, K, W)
+        extra["decode_qwen05b_513"] = {"us_per_layer": round(ms_q * 1e3 / 24, 3),
+                                       "GBps": round(24 * qp.bytes_per_launch() / (ms_q * 1e-3) / 1e9, 1)}
+        del qp
+        # ---- cfg4 Whisper large-v3-turbo (4 decoder layers): self 448, cross 1500, batch 1 and beam 5 ----
+        for beams in (1, 5):
+            ws = DecodeProblem(torch, gen, 20, 20, 64, [448] * beams, layers=4)
+            ms_s, _ = time_graph(torch, ws.step, K, W)
+            wc = DecodeProblem(torch, gen, 20, 20, 64, [1500], layers=4, n_q=beams)
+            ms_c, _ = time_graph(torch, wc.step, K, W)
+            extra[f"whisper_beam{beams}"] = {
+                "self_us_per_layer": round(ms_s * 1e3 / 4, 3),
+                "self_GBps": round(4 * ws.bytes_per_launch() / (ms_s * 1e-3) / 1e9, 1),
+                "cross_us_per_layer": round(ms_c * 1e3 / 4, 3),
+                "cross_GBps": round(4 * wc.bytes_per_launch() / (ms_c * 1e-3) / 1e9, 1)}
+            del ws, wc
+        torch.cuda.empty_cache()
+
+    if args.only in ("prefill", "all"):
+        # ---- cfg5 Qwen2.5-7B 32k causal prefill in 2048-query chunks ----
+        pp = PrefillProblem(torch, gen, 28, 4, 128, 32768, 2048, sigma=0.5)
+        ms_p, _ = time_graph(torch, pp.step, max(3, K // 4), max(1, W // 2))
+        fl = pp.flops_per_layer()
+        tflops = fl / (ms_p * 1e-3) / 1e12
+        durs = time_launches(torch, [lambda ci=ci: pp.launch(0, ci) for ci in range(len(pp.chunks))], reps=2)
+        kt = float(np.sum(durs)) / 2
+        ach = fl / (kt * 1e-3) / 1e12
+        pre = {"metric": "prefill-attn TFLOP/s", "value": round(tflops, 1), "unit": "TFLOP/s",
+               "ms_per_step": round(ms_p, 3),
+               "workload": "cfg5 Qwen2.5-7B causal prefill: 28 q / 4 kv heads, head_dim 128, 32768 tokens in 16 "
+                           "chunks of 2048 queries against the growing f16 cache, N(0, 0.5) inputs; FLOPs count "
+                           "unmasked pairs only (7.697 TFLOP per step)",
+               "flops_per_step": fl,
+               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128>", "achieved": round(ach, 1),
+                            "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / F16_PEAK_TFLOPS, 4),
+                            "traffic": None, "avg_launch_us": round(kt / len(pp.chunks) * 1e3, 2)}}
+        if not args.no_cpu:
+            v1, rows, t1 = cpu_prefill_baseline(torch, pp, args.cpu_seconds, threads)
+            pre["cpu_baseline"] = {"value": round(v1, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                                   "sample": f"the last {rows} query rows of the 32k prompt (all 28 heads, causal, "
+                                             f"every visible key) through the restated CpuWhisperDecoder::attend, "
+                                             f"{threads} threads, {t1:.1f} s; host CPU: {model}"}
+        result["prefill"] = pre
+        del pp
+        torch.cuda.empty_cache()
+
+        # ---- cfg2 Qwen2.5-0.5B 512-token prompt: per layer and over 24 layers ----
+        p2 = PrefillProblem(torch, gen, 14, 2, 64, 512, 512, layers=24)
+        ms_2, _ = time_graph(torch, p2.step, K, W)
+        d2 = time_launches(torch, [lambda l=l: p2.launch(l, 0) for l in range(24)], reps=2)
+        fl2 = p2.flops_per_layer()
+        extra["prefill_qwen05b_512"] = {
+            "ms_24_layers": round(ms_2, 4), "us_per_layer": round(float(np.mean(d2)) * 1e3, 2),
+            "TFLOPs": round(24 * fl2 / (ms_2 * 1e-3) / 1e12, 2),
+            "reference_published_ms": 13.9,
+            "reference_note": "M1 Pro GPU time of prompt attention for a 512-token prompt (site/data.js:142-146); "
+                              "a different metric and machine, so vs_baseline stays null"}
+        del p2
+
+    if "value" not in result:  # --only prefill: the prefill figure is the line's value
+        pre = result["prefill"]
+        result.update({"value": pre["value"], "unit": pre["unit"], "ms_per_step": pre["ms_per_step"],
+                       "config": {"workload": pre["workload"]}, "roofline": pre["roofline"]})
+        if "cpu_baseline" in pre:
+            result["cpu_baseline"] = pre["cpu_baseline"]
+    result["extra"] = extra
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -21,7 +21,7 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
 
 # Every symbol include/mx_attn.h declares.
 EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_decode",
-           "mx_attn_decode_workspace_bytes")
+           "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init")
 
 
 class MxAttnDesc(ctypes.Structure):
@@ -63,6 +63,8 @@ def lib() -> ctypes.CDLL:
                                      ctypes.POINTER(P), ctypes.POINTER(P), P, P, P, ctypes.c_size_t, P]
         L.mx_attn_decode_workspace_bytes.restype = ctypes.c_size_t
         L.mx_attn_decode_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.c_int32]
+        L.mx_attn_decode_workspace_init.restype = ctypes.c_int32
+        L.mx_attn_decode_workspace_init.argtypes = [P, ctypes.c_size_t, P]
         _lib = L
     return _lib
 
@@ -97,6 +99,10 @@ def decode_raw(desc: MxAttnDesc, kv_len, q: int, k_ptrs, v_ptrs, out: int, lse: 
     vp = (ctypes.c_void_p * n)(*v_ptrs)
     return lib().mx_attn_decode(ctypes.byref(desc), n, lens, q, kp, vp, out, lse or None, ws or None, ws_bytes,
                                 stream or None)
+
+
+def decode_workspace_init(ws: int, ws_bytes: int, stream: int) -> int:
+    return lib().mx_attn_decode_workspace_init(ws or None, ws_bytes, stream or None)
 
 
 def decode_workspace_bytes(desc: MxAttnDesc, batch: int, max_kv_len: int) -> int:

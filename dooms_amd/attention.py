@@ -51,6 +51,13 @@ def decode_workspace_bytes(*, n_head, n_head_kv, head_dim, n_q, batch, max_kv_le
     return _lib.decode_workspace_bytes(d, batch, max_kv_len)
 
 
+def new_workspace(nbytes: int, device) -> torch.Tensor:
+    """A decode workspace of nbytes (torch's caching allocator aligns it to 512 bytes), zeroed by the library."""
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+    _lib.check(_lib.decode_workspace_init(ws.data_ptr(), ws.numel(), _stream()))
+    return ws
+
+
 def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1, causal=False, scale=None,
            out=None, lse=None, want_lse=False, workspace=None):
     """mx_attn_decode: q [batch*n_q][>= n_head*hd]; k_caches/v_caches lists of [>= kv_len[b]][>= n_head_kv*hd]
@@ -73,9 +80,8 @@ def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1,
         scale = 1.0 / math.sqrt(head_dim)
     d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, q.stride(0), kv_stride, out.stride(0), scale,
                        causal=1 if causal else 0)
-    need = _lib.decode_workspace_bytes(d, batch, max(kv_len))
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        workspace = new_workspace(_lib.decode_workspace_bytes(d, batch, max(kv_len)), q.device)
     _lib.check(_lib.decode_raw(d, list(kv_len), q.data_ptr(), [t.data_ptr() for t in k_caches],
                                [t.data_ptr() for t in v_caches], out.data_ptr(),
                                lse.data_ptr() if lse is not None else 0, workspace.data_ptr(), workspace.numel(),

@@ -63,12 +63,12 @@ int32_t hip_status(hipError_t e, const char * what) {
 }
 
 // Decode split plan. Splits are a multiple of kDecodeChunkQuantum keys, sized so that the launch has about
-// target_workgroups() workgroups (2 per CU on MI355X's 256 CUs, 8 waves per CU) and never more splits per sequence
-// than ceil(len / quantum), which bounds the workspace by the longest sequence alone.
+// target_workgroups() workgroups (one per CU on MI355X's 256 CUs; fewer, longer splits keep the in-kernel merge short)
+// and never more splits per sequence than ceil(len / quantum), which bounds the workspace by the longest sequence.
 int target_workgroups() {
     const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
     const int v = s ? std::atoi(s) : 0;
-    return v > 0 ? v : 512;
+    return v > 0 ? v : 256;
 }
 
 struct DecodeShape {
@@ -83,12 +83,27 @@ DecodeShape decode_shape(const mx_attn_desc * d) {
     return s;
 }
 
-size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len) {
+// Workspace layout: the split counters (one uint32 per (sequence of a launch, kv head, row tile)), padded to 256 bytes,
+// then the partials. Launches of more than kMaxSeqPerLaunch sequences run one after another on the stream and reuse
+// both (every launch leaves the counters at 0).
+struct WsLayout {
+    size_t counter_bytes, part_bytes;
+};
+
+WsLayout decode_ws_layout(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len) {
     const DecodeShape s = decode_shape(d);
     const int64_t seqs = std::min<int64_t>(batch, mx::kMaxSeqPerLaunch);
     const int64_t max_split = ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum;
-    if (max_split <= 1) return 0;
-    return (size_t)(seqs * d->n_head_kv * s.n_rowtiles * max_split * s.rt * (d->head_dim + 4) * (int64_t)sizeof(float));
+    WsLayout w{0, 0};
+    if (max_split <= 1) return w;  // one split per sequence: no partials, no counters
+    w.counter_bytes = (size_t)((seqs * d->n_head_kv * s.n_rowtiles * 4 + 255) / 256 * 256);
+    w.part_bytes = (size_t)(seqs * d->n_head_kv * s.n_rowtiles * max_split * s.rt * (d->head_dim + 4) * (int64_t)sizeof(float));
+    return w;
+}
+
+size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len) {
+    const WsLayout w = decode_ws_layout(d, batch, max_kv_len);
+    return w.counter_bytes + w.part_bytes;
 }
 
 }  // namespace
@@ -145,6 +160,13 @@ MX_ATTN_API size_t mx_attn_decode_workspace_bytes(const mx_attn_desc * desc, int
     return decode_ws_bytes(desc, batch, max_kv_len);
 }
 
+MX_ATTN_API int32_t mx_attn_decode_workspace_init(void * workspace, size_t ws_bytes, mx_attn_stream stream) {
+    if (ws_bytes == 0) return MX_ATTN_OK;
+    if (!workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null");
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    return hip_status(mx::launch_fill_zero(workspace, ws_bytes, static_cast<hipStream_t>(stream)), "workspace init");
+}
+
 MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const uint16_t * q,
                                    const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out, float * lse,
                                    void * workspace, size_t ws_bytes, mx_attn_stream stream) {
@@ -170,8 +192,9 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
     const size_t need = decode_ws_bytes(desc, batch, max_len);
     if (need > 0 && !workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null but %zu bytes are needed", need);
     if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
-    if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    const WsLayout wl = decode_ws_layout(desc, batch, max_len);
 
     const DecodeShape s = decode_shape(desc);
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -181,7 +204,8 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
         p.q = reinterpret_cast<const mx::half_t *>(q);
         p.out = reinterpret_cast<mx::half_t *>(out);
         p.lse = lse;
-        p.part = static_cast<float *>(workspace);
+        p.counters = static_cast<uint32_t *>(workspace);
+        p.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + wl.counter_bytes);
         p.q_stride = d.q_stride;
         p.kv_stride = d.kv_stride;
         p.out_stride = d.out_stride;

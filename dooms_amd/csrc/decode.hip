@@ -1,4 +1,5 @@
-// Decode attention over per-sequence f16 KV caches: split-KV ("flash-decoding") plus a log-sum-exp merge.
+// Decode attention over per-sequence f16 KV caches: split-KV ("flash-decoding") with the log-sum-exp merge in the same
+// kernel.
 //
 // Reference behaviour (dooms.cpp 0.6.1): the per-query kernel `attention` (src/backend/metal/llama_kernels.h:552-630) for
 // short decodes and Whisper self-attention, `attention_split` (llama_kernels.h:856-910) for decodes of >= 512 positions
@@ -13,10 +14,16 @@
 //   * Scores on the matrix cores: S^T (16 keys x 16 rows) = K (16 keys x head_dim) . Q^T, v_mfma_f32_16x16x32_f16. K goes
 //     from HBM straight into the MFMA operand registers with 16-byte loads (4 lanes cover 64 contiguous bytes of a row).
 //   * Probabilities times values on the vector ALUs: each lane owns 8 contiguous head dimensions of a value row (one
-//     16-byte load) and accumulates rows x 8 f32 sums with mixed f16/f32 FMAs; the probabilities come from LDS as
-//     broadcast reads. At decode's 4 FLOP per byte this keeps the ALUs well under the HBM rate.
-//   * The 4 waves of a workgroup take interleaved 32-key blocks of the split and are merged through LDS, so one partial
-//     (m, l, acc[head_dim]) per split and row reaches HBM; splits are then merged by a second, small kernel.
+//     16-byte load) and accumulates rows x 8 f32 sums; the probabilities come from LDS as broadcast reads. At decode's
+//     4 FLOP per byte this keeps the ALUs well under the HBM rate.
+//   * Each wave walks 32-key blocks of its workgroup's split with the next block's K/V already in flight (register
+//     double buffer); the 4 waves are merged through LDS.
+//   * Splits are merged inside the same launch: each workgroup publishes its partial (acc[head_dim], m, l per row) with
+//     device-scope atomic stores, waits for their completion, and bumps a per-tile counter; the workgroup that brings the
+//     counter to the split count merges and resets it to 0. Publishing with atomic stores (coherent at device scope by
+//     construction) instead of plain stores plus a release fence avoids the fence's full L2 write-back, which on a
+//     multi-XCD part serializes the workgroups; and merging in-kernel saves a second launch (~2.5 us on MI355X, more
+//     than half of the ideal time of an 8192-token Llama-3-8B decode step).
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
@@ -28,19 +35,41 @@ constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kBlockKeys = 32;  // keys per wave iteration
 
+constexpr int kMergeChunk = 32;  // splits whose partials one thread has in flight at once during the merge
+
+// Relaxed device-scope atomic accesses of float pairs: coherent across the XCDs without cache maintenance.
+__device__ __forceinline__ void publish2(float * p, float a, float b) {
+    const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void collect2(const float * p, float & a, float & b) {
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    a = __uint_as_float((uint32_t)v);
+    b = __uint_as_float((uint32_t)(v >> 32));
+}
+
+template <int HD>
+struct KvBlock {
+    static constexpr int KS = HD / 32;            // MFMA steps along head_dim
+    static constexpr int LPR = HD / 8;            // lanes per value row (8 halves per lane)
+    static constexpr int KPL = kWave / LPR;       // value rows per wave load
+    static constexpr int NLV = kBlockKeys / KPL;  // value loads per lane per block
+    u32x4 k[2][KS];
+    u32x4 v[NLV];
+};
+
 // HD: head_dim. RT: query rows per tile (4, 8 or 16; the MFMA tile always has 16 rows, the extra ones are zero).
 template <int HD, int RT>
-__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeParams p) {
-    constexpr int KS = HD / 32;           // MFMA steps along head_dim
-    constexpr int LPR = HD / 8;           // lanes per value row (8 halves per lane)
-    constexpr int KPL = kWave / LPR;      // value rows per wave load
-    constexpr int NLV = kBlockKeys / KPL; // value loads per lane per block
-    constexpr int PS = RT;                // floats per key in the probability buffer
+__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) {
+    using B = KvBlock<HD>;
+    constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
 
-    __shared__ float s_p[kDecodeWaves][kBlockKeys * PS];
+    __shared__ float s_p[kDecodeWaves][kBlockKeys * RT];
     __shared__ float s_corr[kDecodeWaves][RT];
     __shared__ float s_m[kDecodeWaves][RT], s_l[kDecodeWaves][RT];
     __shared__ float s_o[kDecodeWaves][RT * HD];
+    __shared__ int s_last;
 
     const int s = blockIdx.x;
     int y = blockIdx.y;
@@ -58,8 +87,27 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
     const int G = p.group;
     const int64_t seq_row0 = (int64_t)(p.seq0 + bl) * p.n_q;  // first query row of the sequence
 
-    // ---- this lane's score row (lane % 16) and its query operand ----
-    const int srow = lane % 16, sgrp = lane / 16;
+    const half_t * kbase = sq.k + (int64_t)g * HD;
+    const half_t * vbase = sq.v + (int64_t)g * HD;
+    const int srow = lane % 16, sgrp = lane / 16;          // score lanes: row srow, keys 4 sgrp .. + 4 of a 16-key tile
+    const int vslot = lane / LPR, vcol = 8 * (lane % LPR); // value lanes: key slot, first head dim
+
+    auto load_block = [&](int jb, B & blk) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const int key = min(jb + 16 * mt + srow, L - 1);
+            const half_t * kp = kbase + (int64_t)key * p.kv_stride + 8 * sgrp;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) blk.k[mt][ks] = load16(kp + 32 * ks);
+        }
+#pragma unroll
+        for (int i = 0; i < NLV; i++) {
+            const int key = min(jb + KPL * i + vslot, L - 1);
+            blk.v[i] = load16(vbase + (int64_t)key * p.kv_stride + vcol);
+        }
+    };
+
+    // ---- this lane's score row and its query operand ----
     const int rr = rt * RT + srow;  // row index inside the (sequence, kv head) problem: rr = t * G + gi
     const bool srow_ok = srow < RT && rr < p.rows;
     const int st = rr / G, sh = g * G + rr % G;
@@ -75,9 +123,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
         }
     }
 
-    const half_t * kbase = sq.k + (int64_t)g * HD;
-    const half_t * vbase = sq.v + (int64_t)g * HD;
-    const int vslot = lane / LPR, vcol = 8 * (lane % LPR);
+    // the first block of keys and values goes out right behind the query
+    int jb = j0 + kBlockKeys * wave;
+    B cur, nxt;
+    if (jb < j1) load_block(jb, cur);
 
     float m_run = kNegInf, l_run = 0.f;  // per score lane (row srow); l is this lane's partial sum
     float o[RT][8];
@@ -86,28 +135,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
 #pragma unroll
         for (int e = 0; e < 8; e++) o[r][e] = 0.f;
 
-    for (int jb = j0 + kBlockKeys * wave; jb < j1; jb += kBlockKeys * kDecodeWaves) {
-        // issue every load of the block first: keys into MFMA operands, values into registers
-        u32x4 kr[2][KS], vr[NLV];
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            const int key = min(jb + 16 * mt + lane % 16, L - 1);
-            const half_t * kp = kbase + (int64_t)key * p.kv_stride + 8 * sgrp;
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) kr[mt][ks] = load16(kp + 32 * ks);
-        }
-#pragma unroll
-        for (int i = 0; i < NLV; i++) {
-            const int key = min(jb + KPL * i + vslot, L - 1);
-            vr[i] = load16(vbase + (int64_t)key * p.kv_stride + vcol);
-        }
+    for (; jb < j1; jb += kBlockKeys * kDecodeWaves) {
+        const int jn = jb + kBlockKeys * kDecodeWaves;
+        if (jn < j1) load_block(jn, nxt);
         // S^T = K Q^T, 2 tiles of 16 keys
         float sc[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
             float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) acc = mfma16x16x32(as_half8(kr[mt][ks]), qb[ks], acc);
+            for (int ks = 0; ks < KS; ks++) acc = mfma16x16x32(as_half8(cur.k[mt][ks]), qb[ks], acc);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int key = jb + 16 * mt + 4 * sgrp + v;
@@ -139,7 +176,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) s_p[wave][(16 * mt + 4 * sgrp + v) * PS + srow] = sc[mt][v];
+                for (int v = 0; v < 4; v++) s_p[wave][(16 * mt + 4 * sgrp + v) * RT + srow] = sc[mt][v];
             if (sgrp == 0) s_corr[wave][srow] = corr;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -155,8 +192,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
             for (int e = 0; e < 8; e++) o[r][e] *= cr[r];
 #pragma unroll
         for (int i = 0; i < NLV; i++) {
-            const half8_t vv = as_half8(vr[i]);
-            const float * pk = &s_p[wave][(KPL * i + vslot) * PS];
+            const half8_t vv = as_half8(cur.v[i]);
+            const float * pk = &s_p[wave][(KPL * i + vslot) * RT];
             float pr[RT];
 #pragma unroll
             for (int r = 0; r < RT; r++) pr[r] = pk[r];
@@ -168,6 +205,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cur = nxt;
     }
 
     // ---- wave totals: l over the 4 score-lane groups, O over the value slots ----
@@ -194,79 +232,116 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodePara
     }
     __syncthreads();
 
-    // ---- merge the 4 waves; write the output (one split) or this split's partial ----
+    // ---- merge the 4 waves; write the output (one split) or publish this split's partial ----
+    // Each thread owns head-dim pairs (r, 2 dp .. + 2) of the tile's RT x HD outputs.
     const bool single = sq.n_split == 1;
-    for (int idx = threadIdx.x; idx < RT * HD; idx += kDecodeThreads) {
-        const int r = idx / HD, d = idx % HD;
+    const int64_t tile = ((int64_t)bl * p.n_head_kv + g) * p.n_rowtiles + rt;  // (sequence, kv head, row tile)
+    float * part_tile = p.part + tile * p.max_split * RT * (HD + 4);
+    constexpr int64_t SS = (int64_t)RT * (HD + 4);  // floats between the partials of consecutive splits
+    constexpr int NP = RT * HD / 2;                 // output pairs of the tile
+    for (int idx = threadIdx.x; idx < NP; idx += kDecodeThreads) {
+        const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
         const int row = rt * RT + r;
         if (row >= p.rows) continue;
         float M = kNegInf;
 #pragma unroll
         for (int w = 0; w < kDecodeWaves; w++)
             if (s_l[w][r] > 0.f) M = fmaxf(M, s_m[w][r]);
-        float tot = 0.f, acc = 0.f;
+        float tot = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int w = 0; w < kDecodeWaves; w++) {
             if (!(s_l[w][r] > 0.f)) continue;
             const float wt = exp2_fast(s_m[w][r] - M);
             tot += s_l[w][r] * wt;
-            acc += s_o[w][r * HD + d] * wt;
+            a0 += s_o[w][r * HD + d] * wt;
+            a1 += s_o[w][r * HD + d + 1] * wt;
         }
-        const int t = row / G, h = g * G + row % G;
         if (single) {
-            p.out[(seq_row0 + t) * p.out_stride + (int64_t)h * HD + d] = (half_t)(acc / tot);
+            const int t = row / G, h = g * G + row % G;
+            half_t * op = p.out + (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d;
+            op[0] = (half_t)(a0 / tot);
+            op[1] = (half_t)(a1 / tot);
             if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
         } else {
-            const int64_t pidx = ((((int64_t)bl * p.n_head_kv + g) * p.n_rowtiles + rt) * p.max_split + s) * RT + r;
-            float * pe = p.part + pidx * (HD + 4);
-            pe[d] = acc;
-            if (d == 0) {
-                pe[HD] = M;
-                pe[HD + 1] = tot;
-            }
+            float * pe = part_tile + s * SS + (int64_t)r * (HD + 4);
+            publish2(pe + d, a0, a1);
+            if (d == 0) publish2(pe + HD, M, tot);
         }
     }
-}
+    if (single) return;
 
-// Merge of the split partials of one (sequence, query row, head): out = sum_s 2^{m_s - M} acc_s / sum_s 2^{m_s - M} l_s
-// over the splits with l_s > 0 (the reference's attention_combine, llama_kernels.h:912-929, with base-2 statistics).
-template <int HD, int RT>
-__global__ __launch_bounds__(HD) void decode_merge_kernel(DecodeParams p) {
-    const int bl = blockIdx.y;
-    const DecodeSeq sq = p.seq[bl];
-    if (sq.n_split == 1) return;  // written by the split kernel
-    const int th = blockIdx.x;  // t * n_head + h
-    const int t = th / p.n_head, h = th % p.n_head;
-    const int G = p.group, g = h / G, row = t * G + h % G, rt = row / RT, r = row % RT;
-    const int d = threadIdx.x;
-    const int64_t base = (((int64_t)bl * p.n_head_kv + g) * p.n_rowtiles + rt) * p.max_split;
-    float M = kNegInf;
-    for (int s = 0; s < sq.n_split; s++) {
-        const float * pe = p.part + ((base + s) * RT + r) * (HD + 4);
-        if (pe[HD + 1] > 0.f) M = fmaxf(M, pe[HD]);
+    // Every thread waits until its partial stores are complete (performed at device scope), then one thread counts the
+    // split in. The merging workgroup reads the partials with device-scope atomic loads after seeing the final count.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = done == (uint32_t)(sq.n_split - 1);
     }
-    float tot = 0.f, acc = 0.f;
-    for (int s = 0; s < sq.n_split; s++) {
-        const float * pe = p.part + ((base + s) * RT + r) * (HD + 4);
-        const float l = pe[HD + 1];
-        if (!(l > 0.f)) continue;
-        const float wt = exp2_fast(pe[HD] - M);
-        tot += l * wt;
-        acc += pe[d] * wt;
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // ---- cross-split merge (attention_combine, llama_kernels.h:912-929). Each thread merges its output pairs on its
+    // own: per chunk of kMergeChunk splits it issues every load first ((m, l) of its row and its pair, for all the
+    // chunk's splits; the row's (m, l) loads of a wave coalesce), then folds them with a running maximum. One memory
+    // round trip per chunk, no LDS, no barrier. ----
+    const int ns = sq.n_split;
+    constexpr int PPT = (NP + kDecodeThreads - 1) / kDecodeThreads;  // output pairs per thread
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+        const int idx = threadIdx.x + j * kDecodeThreads;
+        if (idx >= NP) break;
+        const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
+        const int row = rt * RT + r;
+        if (row >= p.rows) continue;
+        const float * pr = part_tile + (int64_t)r * (HD + 4);
+        float M = kNegInf, tot = 0.f, a0 = 0.f, a1 = 0.f;
+        for (int k0 = 0; k0 < ns; k0 += kMergeChunk) {
+            float m[kMergeChunk], l[kMergeChunk], u[kMergeChunk], v[kMergeChunk];
+#pragma unroll
+            for (int e = 0; e < kMergeChunk; e++) {
+                const int k = min(k0 + e, ns - 1);  // past the end: repeat the last split, weighted 0 below
+                collect2(pr + k * SS + HD, m[e], l[e]);
+                collect2(pr + k * SS + d, u[e], v[e]);
+            }
+            float cm = M;
+#pragma unroll
+            for (int e = 0; e < kMergeChunk; e++)
+                if (k0 + e < ns && l[e] > 0.f) cm = fmaxf(cm, m[e]);
+            const float c = cm == M ? 1.f : exp2_fast(M - cm);  // rescale of what was summed so far
+            tot *= c;
+            a0 *= c;
+            a1 *= c;
+            M = cm;
+#pragma unroll
+            for (int e = 0; e < kMergeChunk; e++) {
+                const float w = (k0 + e < ns && l[e] > 0.f) ? exp2_fast(m[e] - M) : 0.f;
+                tot = __builtin_fmaf(l[e], w, tot);
+                a0 = __builtin_fmaf(u[e], w, a0);
+                a1 = __builtin_fmaf(v[e], w, a1);
+            }
+        }
+        const int t = row / G, h = g * G + row % G;
+        const float inv = 1.f / tot;
+        half_t * op = p.out + (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d;
+        op[0] = (half_t)(a0 * inv);
+        op[1] = (half_t)(a1 * inv);
+        if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
     }
-    const int64_t qrow = (int64_t)(p.seq0 + bl) * p.n_q + t;
-    p.out[qrow * p.out_stride + (int64_t)h * HD + d] = (half_t)(acc / tot);
-    if (d == 0 && p.lse) p.lse[qrow * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
+    if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int HD, int RT>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
-    const dim3 grid(p.max_split, n_seq * p.n_head_kv * p.n_rowtiles);
-    hipLaunchKernelGGL((decode_split_kernel<HD, RT>), grid, dim3(kDecodeThreads), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.max_split == 1) return e;
-    hipLaunchKernelGGL((decode_merge_kernel<HD, RT>), dim3(p.n_q * p.n_head, n_seq), dim3(HD), 0, stream, p);
+    const int tiles = n_seq * p.n_head_kv * p.n_rowtiles;
+    hipLaunchKernelGGL((decode_kernel<HD, RT>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
     return hipGetLastError();
+}
+
+// Zero fill (the split counters start at 0); a kernel rather than a memset so that a caller may capture it in a graph.
+__global__ void fill_zero_kernel(uint32_t * p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
 }
 
 }  // namespace
@@ -282,6 +357,14 @@ hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt
     if (rt == 4) return launch_decode_t<128, 4>(p, n_seq, stream);
     if (rt == 8) return launch_decode_t<128, 8>(p, n_seq, stream);
     return launch_decode_t<128, 16>(p, n_seq, stream);
+}
+
+hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream) {
+    const size_t n = bytes / 4;
+    if (n == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<uint32_t *>(p), n);
+    return hipGetLastError();
 }
 
 }  // namespace mx

@@ -26,6 +26,7 @@ struct DecodeParams {
     half_t * out;
     float * lse;
     float * part;  // [n_seq][n_head_kv][n_rowtiles][max_split][RT][head_dim + 4] f32: acc[head_dim], m, l, 2 spare
+    uint32_t * counters;  // [n_seq][n_head_kv][n_rowtiles]: splits finished per tile; back at 0 after every call
     int64_t q_stride, kv_stride, out_stride;
     int32_t n_head, n_head_kv, group, n_q, causal;
     int32_t rows;        // n_q * group: query rows that share one key/value head
@@ -50,6 +51,7 @@ struct PrefillParams {
 
 int decode_rows_per_tile(int rows);
 hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, hipStream_t stream);
+hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 
 constexpr int kPrefillRows = 128;  // query rows per workgroup
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);

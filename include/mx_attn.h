@@ -115,7 +115,9 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
  *   out              device, [batch * n_q rows][out_stride]
  *   lse              device, [batch * n_q rows][n_head] f32 natural-log LSE, or NULL
  *   workspace        device scratch of at least mx_attn_decode_workspace_bytes(desc, batch, max_b kv_len[b]) bytes,
- *                    256-byte aligned; its contents on entry do not matter
+ *                    256-byte aligned, zeroed once by mx_attn_decode_workspace_init before its first use: it holds
+ *                    split counters that every call leaves at zero again. Calls that share a workspace must be
+ *                    ordered on one stream. NULL is allowed when the size needed is 0.
  *
  * With causal = 1 query row t of sequence b attends keys 0 .. kv_len[b] - n_q + t (the decoder's prompt rows appended
  * at the end of the cache, as the reference's per-query kernel with p0 = kv_len - n_q); with causal = 0 every row
@@ -124,6 +126,14 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
 MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const uint16_t * q,
                                    const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out,
                                    float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream);
+
+/*
+ * Zero-fills a decode workspace on `stream` (with a kernel, not a memset, so that a caller may capture it in a HIP
+ * graph). Call it once after allocating the workspace; mx_attn_decode keeps it ready for the next call. It has no
+ * counterpart in the reference, whose split partials need no counters (attention_combine runs as a second dispatch,
+ * llama_kernels.h:912-929); here the merge runs in the split kernel itself.
+ */
+MX_ATTN_API int32_t mx_attn_decode_workspace_init(void * workspace, size_t ws_bytes, mx_attn_stream stream);
 
 /*
  * Workspace bytes mx_attn_decode needs for `batch` sequences of at most max_kv_len keys (the reference sizes its
