@@ -1,0 +1,159 @@
+"""The C ABI (include/mx_attn.h, dooms_amd/libmx_attn.so) on the CPU: the library loads, exports exactly what the header
+declares, the descriptor layout agrees between C and the binding, and every argument check returns the documented code
+(the dooms_code numbering, include/dooms/dooms_c.h:24-33 in the reference) with a message, before anything touches a GPU.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import threading
+
+import pytest
+
+from dooms_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mx_attn.h")
+A = 256  # a 256-byte aligned fake device address: never dereferenced, every call below fails its checks first
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"MX_ATTN_API\s+[\w\s\*]+?\b(mx_attn_\w+)\s*\(", text)))
+
+
+def exported():
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    return sorted(l.split()[-1] for l in out.splitlines() if " T " in l)
+
+
+def test_library_loads():
+    assert _lib.lib().mx_attn_abi_version() == 1
+
+
+def test_exports_exactly_the_header():
+    assert declared() == sorted(_lib.EXPORTS)
+    assert exported() == declared()
+
+
+def test_desc_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mx_attn.h"\n'
+                   'int main(void){printf("%zu %zu %zu %zu %zu\\n", sizeof(mx_attn_desc), offsetof(mx_attn_desc, reserved),'
+                   ' offsetof(mx_attn_desc, q_stride), offsetof(mx_attn_desc, out_stride), offsetof(mx_attn_desc, scale));'
+                   'return 0;}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    D = _lib.MxAttnDesc
+    assert got == [ctypes.sizeof(D), D.reserved.offset, D.q_stride.offset, D.out_stride.offset, D.scale.offset]
+
+
+def desc(**kw):
+    base = dict(n_head=32, n_head_kv=8, head_dim=128, n_q=1, q_stride=4096, kv_stride=1024, out_stride=4096,
+                scale=0.0883883)
+    base.update(kw)
+    return _lib.make_desc(**base)
+
+
+def prefill(d, q=A, k=A, v=A, out=A, lse=0):
+    return _lib.lib().mx_attn_prefill(ctypes.byref(d) if d is not None else None, q, k, v, out, lse or None, None)
+
+
+def decode(d, lens=(100,), kp=None, vp=None, q=A, out=A, lse=0, ws=A, ws_bytes=1 << 30, batch=None):
+    n = len(lens)
+    L = (ctypes.c_int32 * max(n, 1))(*lens)
+    K = (ctypes.c_void_p * max(n, 1))(*(kp or [A] * n))
+    V = (ctypes.c_void_p * max(n, 1))(*(vp or [A] * n))
+    return _lib.lib().mx_attn_decode(ctypes.byref(d), n if batch is None else batch, L, q, K, V, out, lse or None,
+                                     ws or None, ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(reserved=1), _lib.INVALID_ARGUMENT, "reserved"),
+    (dict(n_head=0), _lib.INVALID_ARGUMENT, "n_head"),
+    (dict(n_head=14, n_head_kv=3), _lib.INVALID_ARGUMENT, "multiple"),
+    (dict(head_dim=0), _lib.INVALID_ARGUMENT, "head_dim"),
+    (dict(head_dim=80, q_stride=2560, kv_stride=640, out_stride=2560), _lib.UNSUPPORTED, "not supported"),
+    (dict(head_dim=96, q_stride=3072, kv_stride=768, out_stride=3072), _lib.UNSUPPORTED, "not supported"),
+    (dict(n_q=-1), _lib.INVALID_ARGUMENT, "n_q"),
+    (dict(causal=2), _lib.INVALID_ARGUMENT, "causal"),
+    (dict(scale=float("nan")), _lib.INVALID_ARGUMENT, "scale"),
+    (dict(scale=float("inf")), _lib.INVALID_ARGUMENT, "scale"),
+    (dict(q_stride=4088), _lib.INVALID_ARGUMENT, "q_stride"),
+    (dict(kv_stride=1016), _lib.INVALID_ARGUMENT, "kv_stride"),
+    (dict(out_stride=100), _lib.INVALID_ARGUMENT, "out_stride"),
+    (dict(q_stride=4100), _lib.INVALID_ARGUMENT, "multiples of 8"),
+])
+def test_descriptor_checks(kw, code, msg):
+    for call in (lambda d: prefill(d), lambda d: decode(d)):
+        assert call(desc(**kw)) == code
+        assert msg in _lib.last_error()
+
+
+def test_null_descriptor():
+    assert prefill(None) == _lib.INVALID_ARGUMENT
+    assert "desc is null" in _lib.last_error()
+
+
+def test_prefill_checks():
+    assert prefill(desc(p0=-1)) == _lib.INVALID_ARGUMENT and "p0" in _lib.last_error()
+    assert prefill(desc(n_kv=-1)) == _lib.INVALID_ARGUMENT
+    assert prefill(desc(n_q=10, p0=5, n_kv=12)) == _lib.INVALID_ARGUMENT and "n_kv" in _lib.last_error()
+    assert prefill(desc(), q=0) == _lib.INVALID_ARGUMENT and "null" in _lib.last_error()
+    assert prefill(desc(), out=A + 2) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
+    assert prefill(desc(), lse=A + 2) == _lib.INVALID_ARGUMENT and "lse" in _lib.last_error()
+    # zero rows: nothing to do, no pointer is looked at
+    assert prefill(desc(n_q=0), q=0, k=0, v=0, out=0) == _lib.OK
+
+
+def test_decode_checks():
+    d = desc()
+    assert decode(d, batch=0) == _lib.INVALID_ARGUMENT and "batch" in _lib.last_error()
+    assert decode(d, lens=(100, 0)) == _lib.INVALID_ARGUMENT and "kv_len[1]" in _lib.last_error()
+    assert decode(desc(n_q=8, causal=1), lens=(5,)) == _lib.INVALID_ARGUMENT and "n_q" in _lib.last_error()
+    assert decode(d, lens=(100, 100), kp=[A, 0]) == _lib.INVALID_ARGUMENT and "sequence 1" in _lib.last_error()
+    assert decode(d, lens=(100,), vp=[A + 8]) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
+    assert decode(d, q=0) == _lib.INVALID_ARGUMENT
+    assert decode(d, lens=(5000,), ws_bytes=16) == _lib.RESOURCE_EXHAUSTED and "workspace" in _lib.last_error()
+    assert decode(d, lens=(5000,), ws=0) == _lib.INVALID_ARGUMENT and "workspace is null" in _lib.last_error()
+    assert decode(d, lens=(5000,), ws=A + 16) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
+    assert decode(desc(n_q=0), lens=(5,)) == _lib.OK
+
+
+def test_workspace_init_checks():
+    L = _lib.lib()
+    assert L.mx_attn_decode_workspace_init(None, 0, None) == _lib.OK
+    assert L.mx_attn_decode_workspace_init(None, 256, None) == _lib.INVALID_ARGUMENT
+    assert L.mx_attn_decode_workspace_init(A + 4, 256, None) == _lib.INVALID_ARGUMENT
+
+
+def test_workspace_size():
+    d = desc()
+    ws = lambda b, n: _lib.decode_workspace_bytes(d, b, n)
+    assert ws(1, 1) == 0 and ws(1, 128) == 0  # one split: no partials
+    assert ws(1, 129) > 0
+    assert ws(1, 8192) <= ws(1, 8193) <= ws(4, 8193) <= ws(32, 8193) == ws(100, 8193)  # launches of 32 reuse it
+    # counters (256-byte padded) plus 8192/128 = 64 splits x 8 kv heads x 4 rows x (128 + 4) floats
+    assert ws(1, 8192) == 256 + 64 * 8 * 4 * 132 * 4
+    assert _lib.decode_workspace_bytes(desc(n_head=3, n_head_kv=2), 1, 1000) == 0
+    assert "multiple" in _lib.last_error()
+
+
+def test_last_error_is_per_thread():
+    prefill(desc(head_dim=80))
+    assert "not supported" in _lib.last_error()
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(_lib.last_error()))
+    t.start()
+    t.join()
+    assert seen == [""]
+
+
+def test_python_front_end_refuses_host_tensors():
+    import torch
+    from dooms_amd import attention
+    x = torch.zeros(4, 128, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        attention.prefill(x, x, x, n_head=1, n_head_kv=1, head_dim=128)

@@ -1,0 +1,181 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it. CPU only.
+
+Each check is chosen so that a plausible mistake in the oracle fails it:
+  * torch's scaled_dot_product_attention in float64 (an independent library routine) with GQA, a causal mask with a
+    chunk offset, and non-causal rows: catches a wrong GQA head mapping, a wrong causal limit or offset, a missing or
+    misplaced scale, a transposed operand;
+  * closed forms: scale 0 -> mean of the visible values (test_backend_ggml.cpp:715-735), one key -> that value, equal
+    keys -> mean of the values, one dominant logit -> that value row;
+  * invariants: GQA equals MHA over repeated key/value heads; a causal row equals a non-causal row over its prefix;
+    the LSE equals log(sum(exp)) of the scores;
+  * the committed golden fixtures (tests/golden, written by tests/golden/make_golden.py);
+  * the f16 decoding routine against numpy on all 65536 bit patterns;
+  * the restated reference CPU attention (cpu_attend_f32) against the f64 oracle within f32 error (the reference's CPU
+    tolerance, test_backend_ggml.cpp:694: 2e-5), single- and multi-threaded bit-identical.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def rand_f16(rng, shape, sigma=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(np.float16)
+
+
+def torch_sdpa(q, k, v, n_head, n_head_kv, hd, scale, p0, causal):
+    n_q, n_kv = q.shape[0], k.shape[0]
+    G = n_head // n_head_kv
+    tq = torch.from_numpy(q.astype(np.float64)).view(n_q, n_head, hd).transpose(0, 1)
+    tk = torch.from_numpy(k.astype(np.float64)).view(n_kv, n_head_kv, hd).transpose(0, 1)
+    tv = torch.from_numpy(v.astype(np.float64)).view(n_kv, n_head_kv, hd).transpose(0, 1)
+    mask = torch.ones(n_q, n_kv, dtype=torch.bool)
+    if causal:
+        mask = torch.arange(n_kv)[None, :] <= (p0 + torch.arange(n_q))[:, None]
+    out = torch.nn.functional.scaled_dot_product_attention(tq[None], tk[None], tv[None], attn_mask=mask, scale=scale,
+                                                           enable_gqa=G > 1)[0]
+    s = scale * tq @ tk.repeat_interleave(G, dim=0).transpose(1, 2)
+    lse = torch.logsumexp(s.masked_fill(~mask, float("-inf")), dim=-1)
+    return out.transpose(0, 1).reshape(n_q, n_head * hd).numpy(), lse.transpose(0, 1).numpy()
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd,n_q,n_kv,p0,causal", [
+    (14, 2, 64, 1, 40, 39, 1),      # decode row, G = 7
+    (8, 2, 128, 12, 30, 18, 1),     # chunk at an offset, G = 4
+    (4, 4, 64, 9, 9, 0, 1),         # MHA prompt
+    (6, 3, 32, 5, 23, 0, 0),        # non-causal (cross-attention), G = 2
+    (4, 1, 16, 7, 7, 0, 1),         # G = 4, one kv head
+])
+def test_oracle_matches_torch_sdpa_f64(n_head, n_head_kv, hd, n_q, n_kv, p0, causal):
+    rng = np.random.default_rng(100 + n_head + n_q)
+    q, k, v = rand_f16(rng, (n_q, n_head * hd)), rand_f16(rng, (n_kv, n_head_kv * hd)), rand_f16(rng, (n_kv, n_head_kv * hd))
+    scale = 1.0 / np.sqrt(hd)
+    out, lse = O.attention_f64(q, k, v, n_head, n_head_kv, hd, scale, p0=p0, causal=bool(causal))
+    to, tl = torch_sdpa(q, k, v, n_head, n_head_kv, hd, scale, p0, causal)
+    np.testing.assert_allclose(out, to, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(lse, tl, rtol=0, atol=1e-12)
+
+
+def test_scale_zero_is_mean_of_visible_values():
+    rng = np.random.default_rng(1)
+    n_q, n_kv, p0, hd = 6, 10, 4, 16
+    q, k, v = rand_f16(rng, (n_q, 2 * hd)), rand_f16(rng, (n_kv, hd)), rand_f16(rng, (n_kv, hd))
+    out, lse = O.attention_f64(q, k, v, 2, 1, hd, 0.0, p0=p0, causal=True)
+    vd = v.astype(np.float64)
+    for t in range(n_q):
+        mean = vd[:p0 + t + 1].mean(axis=0)
+        np.testing.assert_allclose(out[t, :hd], mean, atol=1e-14)
+        np.testing.assert_allclose(out[t, hd:], mean, atol=1e-14)
+        np.testing.assert_allclose(lse[t], np.log(p0 + t + 1), atol=1e-14)
+
+
+def test_one_key_returns_that_value():
+    rng = np.random.default_rng(2)
+    q, k, v = rand_f16(rng, (1, 64)), rand_f16(rng, (1, 64)), rand_f16(rng, (1, 64))
+    out, lse = O.attention_f64(q, k, v, 1, 1, 64, 0.125, causal=False)
+    np.testing.assert_array_equal(out[0], v[0].astype(np.float64))
+    np.testing.assert_allclose(lse[0, 0], 0.125 * float(np.dot(q[0].astype(np.float64), k[0].astype(np.float64))),
+                               atol=1e-12)
+
+
+def test_equal_keys_give_mean_of_values():
+    rng = np.random.default_rng(3)
+    k = np.tile(rand_f16(rng, (1, 32)), (9, 1))
+    q, v = rand_f16(rng, (1, 32)), rand_f16(rng, (9, 32))
+    out, _ = O.attention_f64(q, k, v, 1, 1, 32, 0.3, causal=False)
+    np.testing.assert_allclose(out[0], v.astype(np.float64).mean(axis=0), atol=1e-14)
+
+
+def test_dominant_logit_selects_its_value_row():
+    hd = 16
+    q = np.zeros((1, hd), np.float16)
+    q[0, 0] = 60.0
+    k = np.zeros((5, hd), np.float16)
+    k[3, 0] = 60.0  # score 3600 * scale for key 3, 0 for the others
+    v = np.arange(5 * hd, dtype=np.float16).reshape(5, hd)
+    out, lse = O.attention_f64(q, k, v, 1, 1, hd, 1.0, causal=False)
+    np.testing.assert_allclose(out[0], v[3].astype(np.float64), atol=1e-9)
+    np.testing.assert_allclose(lse[0, 0], 3600.0, atol=1e-9)
+
+
+def test_gqa_equals_mha_on_repeated_kv_heads():
+    rng = np.random.default_rng(4)
+    n_head, n_kv, hd, n_q, L = 12, 3, 32, 4, 25
+    q, k, v = rand_f16(rng, (n_q, n_head * hd)), rand_f16(rng, (L, n_kv * hd)), rand_f16(rng, (L, n_kv * hd))
+    G = n_head // n_kv
+    # head h of the MHA problem reads kv head h // G: repeat each kv head G times, in order
+    rep = lambda a: np.concatenate([np.tile(a[:, g * hd:(g + 1) * hd], (1, G)) for g in range(n_kv)], axis=1)
+    a, la = O.attention_f64(q, k, v, n_head, n_kv, hd, 0.2, p0=L - n_q, causal=True)
+    b, lb = O.attention_f64(q, rep(k), rep(v), n_head, n_head, hd, 0.2, p0=L - n_q, causal=True)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(la, lb)
+
+
+def test_causal_row_is_noncausal_over_its_prefix():
+    rng = np.random.default_rng(5)
+    n_q, L, p0, hd = 5, 20, 15, 32
+    q, k, v = rand_f16(rng, (n_q, 2 * hd)), rand_f16(rng, (L, 2 * hd)), rand_f16(rng, (L, 2 * hd))
+    a, la = O.attention_f64(q, k, v, 2, 2, hd, 0.17, p0=p0, causal=True)
+    for t in range(n_q):
+        b, lb = O.attention_f64(q[t:t + 1], k[:p0 + t + 1], v[:p0 + t + 1], 2, 2, hd, 0.17, causal=False)
+        np.testing.assert_array_equal(a[t], b[0])
+        np.testing.assert_array_equal(la[t], lb[0])
+
+
+def test_lse_is_log_sum_exp_of_scores():
+    rng = np.random.default_rng(6)
+    q, k, v = rand_f16(rng, (1, 64)), rand_f16(rng, (50, 64)), rand_f16(rng, (50, 64))
+    _, lse = O.attention_f64(q, k, v, 1, 1, 64, 0.125, causal=False)
+    s = 0.125 * k.astype(np.float64) @ q[0].astype(np.float64)
+    np.testing.assert_allclose(lse[0, 0], np.log(np.exp(s).sum()), rtol=1e-13)
+
+
+def test_oracle_rejects_bad_shapes():
+    q = np.zeros((1, 64), np.float16)
+    with pytest.raises(ValueError):
+        O.attention_f64(q, q, q, 3, 2, 32, 1.0)  # 3 % 2 != 0
+
+
+def test_f16_decoding_matches_numpy_on_every_bit_pattern():
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = O.f16_to_f32(bits.view(np.float16))
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all()
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))), ids=os.path.basename)
+def test_golden_fixture(path):
+    z = np.load(path)
+    n_head, n_head_kv, hd, n_q, n_kv, p0, causal = (int(x) for x in z["meta"])
+    out, lse = O.attention_f64(z["q"], z["k"], z["v"], n_head, n_head_kv, hd, float(z["scale"]), p0=p0,
+                               causal=bool(causal), n_kv=n_kv)
+    np.testing.assert_allclose(out, z["out"], rtol=0, atol=1e-12)
+    np.testing.assert_allclose(lse, z["lse"], rtol=0, atol=1e-12)
+    to, tl = torch_sdpa(z["q"], z["k"], z["v"], n_head, n_head_kv, hd, float(z["scale"]), p0, causal)
+    np.testing.assert_allclose(z["out"], to, rtol=0, atol=1e-12)
+
+
+def test_golden_fixtures_present():
+    assert len(glob.glob(os.path.join(GOLDEN, "*.npz"))) >= 7
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_cpu_restatement_within_f32_error(causal):
+    rng = np.random.default_rng(7)
+    n_head, n_kv, hd, n_q, L = 8, 2, 64, 6, 300
+    q, k, v = rand_f16(rng, (n_q, n_head * hd)), rand_f16(rng, (L, n_kv * hd)), rand_f16(rng, (L, n_kv * hd))
+    scale = 1.0 / np.sqrt(hd)
+    ref, _ = O.attention_f64(q, k, v, n_head, n_kv, hd, scale, p0=L - n_q, causal=bool(causal))
+    got = O.cpu_attend_f32(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), n_head, n_kv, hd, scale,
+                           p0=L - n_q, causal=bool(causal))
+    assert np.abs(got - ref).max() < 2e-5
+    got4 = O.cpu_attend_f32(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), n_head, n_kv, hd, scale,
+                            p0=L - n_q, causal=bool(causal), n_threads=4)
+    np.testing.assert_array_equal(got, got4)
