@@ -6,13 +6,18 @@
 // m and sum l with the rescale factor exp(m_old - m_new), P rounded to half, O += P V, and O / l at the end.
 //
 // MI355X design:
-//   * One workgroup = 4 waves = 128 query rows of one query head; each wave owns 32 rows. Key/value blocks of 64 rows
-//     stream through LDS (K row-major, V transposed), shared by the 4 waves; the next block is loaded from HBM/L2 into
-//     registers while the current one is multiplied.
-//   * Transposed scores: S^T (keys x queries) = K Q^T on v_mfma_f32_32x32x16_f16. In the MFMA result each lane holds 16
-//     keys of ONE query (and the lane 32 away the other 16), so the row max and row sum need a single cross-lane step,
-//     and the probabilities are already in the register layout of the B operand of O^T += V^T P^T: P never goes through
-//     LDS. Q^T (the B operand of the first product) is loaded once into registers.
+//   * One workgroup = 4 waves = 128 query rows of one query head; each wave owns 32 rows. Two workgroups per CU (the
+//     register budget is held to 256 per lane), so each SIMD interleaves two waves: one wave's softmax runs on the
+//     vector ALU while the other's products run on the matrix core.
+//   * Key/value blocks of 64 rows pass through LDS, double-buffered: block i + 1 goes from registers into the free LDS
+//     buffer and block i + 2 is loaded from HBM/L2 into registers while block i is multiplied; one barrier per block.
+//     Both tiles are stored row-major, 16-byte chunks XOR-swizzled by row, so the K reads below and the transposing V
+//     reads are free of bank conflicts.
+//   * Transposed scores: S^T (keys x queries) = K Q^T on v_mfma_f32_32x32x16_f16. In the result each lane holds 16 keys
+//     of ONE query (the lane 32 away the other 16), so the row max and sum need one cross-lane step, and the
+//     probabilities already sit in the B-operand layout of O^T += V^T P^T: P never touches LDS. Q^T is loaded once into
+//     registers. The V^T operand comes straight from the row-major V tile through ds_read_b64_tr_b16, whose 16-lane
+//     transpose hands every lane four consecutive keys of one head dimension.
 //   * The softmax runs in base 2 (scale * log2 e folded into one multiply), masking only in blocks that cross the
 //     causal diagonal or the end of the cache; blocks past a wave's last row are skipped.
 //   * Workgroups are dealt out so that the heaviest query tiles start first and the heads of one GQA group run next to
@@ -26,24 +31,33 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kBK = 64;              // keys per block
-constexpr int kVtPitch = kBK + 4;    // halves per row of V^T in LDS (conflict-free 8-byte reads and 2-byte writes)
+constexpr int kBK = 64;  // keys per block
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte chunk slot of chunk c in tile row r: c XOR a row-dependent mask. HD 128 (a row spans all 64 banks): 16
+// consecutive rows at one chunk hit 16 distinct slots, and rows 4k .. 4k + 3 at a chunk pair {2x, 2x + 1} hit 8
+// distinct slots. HD 64 (two rows per bank sweep): the same, for rows of one parity.
+template <int HD>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (HD == 128) return 2 * (r % 8) + (r / 8) % 2;
+    else return 2 * ((r / 2) % 4) + (r / 8) % 2;
+}
 
 template <int HD>
 struct PrefillSmem {
-    static constexpr int kKPitch = HD + 8;  // halves per row of K in LDS
-    half_t k[kBK * kKPitch];
-    half_t vt[HD * kVtPitch];
+    half_t k[2][kBK * HD];
+    half_t v[2][kBK * HD];
 };
 
 template <int HD>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_kernel(PrefillParams p) {
     constexpr int KS = HD / 16;          // MFMA steps along head_dim for S^T
     constexpr int DT = HD / 32;          // 32-wide output tiles along head_dim
     constexpr int C8 = HD / 8;           // 16-byte chunks per key row
-    constexpr int NB = (kBK / 16) * (C8 / 4);  // (16 keys x 4 chunks) blocks per tile
+    constexpr int NB = (kBK / 16) * (C8 / 4);  // (16 keys x 4 chunks) load blocks per tile
     constexpr int NI = NB / kWaves;      // loads per thread per tile, for each of K and V
-    constexpr int KP = PrefillSmem<HD>::kKPitch;
     __shared__ PrefillSmem<HD> sm;
 
     // ---- work item: heavy query tiles first, GQA groups adjacent, contiguous ranges per XCD ----
@@ -66,25 +80,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     // keys this workgroup must visit
     const int last_row = min(q0 + kPrefillRows, p.n_q) - 1;
     const int kend = p.causal ? min(p.n_kv, p.p0 + last_row + 1) : p.n_kv;
-
-    // Q^T operand: lane holds Q[qrow][16 ks + 8 hgrp .. + 8]
-    half8_t qb[KS];
-    {
-        const half_t * qp = p.q + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (qrow < p.n_q) v = load16(qp + 16 * ks);
-            qb[ks] = as_half8(v);
-        }
-    }
-
-    float16_t o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) o[dt][v] = 0.f;
-    float m_run = kNegInf, l_run = 0.f;
+    const int nblk = (kend + kBK - 1) / kBK;
 
     const half_t * kg = p.k + (int64_t)kvh * HD;
     const half_t * vg = p.v + (int64_t)kvh * HD;
@@ -101,26 +97,58 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
             vreg[i] = load16(vg + off);
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
-            const int key = 16 * (b % (kBK / 16)) + lane % 16;
+            const int r = 16 * (b % (kBK / 16)) + lane % 16;
             const int c8 = 4 * (b / (kBK / 16)) + lane / 16;
-            *reinterpret_cast<u32x4 *>(&sm.k[key * KP + 8 * c8]) = kreg[i];
-            const half8_t vv = as_half8(vreg[i]);
-#pragma unroll
-            for (int e = 0; e < 8; e++) sm.vt[(8 * c8 + e) * kVtPitch + key] = vv[e];
+            const int o = r * HD + 8 * (c8 ^ swz<HD>(r));
+            *reinterpret_cast<u32x4 *>(&sm.k[buf][o]) = kreg[i];
+            *reinterpret_cast<u32x4 *>(&sm.v[buf][o]) = vreg[i];
         }
     };
 
-    if (kend > 0) load_tile(0);
-    for (int kb = 0; kb < kend; kb += kBK) {
-        __syncthreads();  // the previous block's products are done with LDS
-        store_tile();
-        __syncthreads();
-        if (kb + kBK < kend) load_tile(kb + kBK);
+    // Q^T operand: lane holds Q[qrow][16 ks + 8 hgrp .. + 8]
+    half8_t qb[KS];
+    {
+        const half_t * qp = p.q + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (qrow < p.n_q) v = load16(qp + 16 * ks);
+            qb[ks] = as_half8(v);
+        }
+    }
+    if (nblk > 0) {
+        load_tile(0);
+        store_tile(0);
+        if (nblk > 1) load_tile(kBK);
+    }
+
+    float16_t o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[dt][v] = 0.f;
+    float m_run = kNegInf, l_run = 0.f;
+
+    // lane-invariant parts of the LDS read addresses
+    const int tr_row = (lane % 16) / 4;                 // row offset inside a 4-key group of the transposing read
+    const int tr_c16 = 2 * ((lane / 16) % 2) + (lane % 4) / 2;  // 16-byte chunk (before the dt offset)
+    const int tr_half = 4 * (lane % 2);                 // 8-byte half inside the chunk, in elements
+
+    for (int ib = 0; ib < nblk; ib++) {
+        const int kb = ib * kBK;
+        const int buf = ib & 1;
+        __syncthreads();  // block ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
+        if (ib + 1 < nblk) {
+            store_tile(buf ^ 1);
+            if (ib + 2 < nblk) load_tile(kb + 2 * kBK);
+        }
         if (p.causal && kb > wave_last) continue;  // every key of the block is past this wave's rows
+        const half_t * ks_ = sm.k[buf];
+        const half_t * vs_ = sm.v[buf];
 
         // S^T = K Q^T: 2 tiles of 32 keys
         float16_t sc[2];
@@ -129,11 +157,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
             float16_t acc;
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[v] = 0.f;
-            const half_t * kr = &sm.k[(32 * mt + l32) * KP + 8 * hgrp];
+            const int r = 32 * mt + l32;
+            const half_t * kr = ks_ + r * HD;
+            const int sw = swz<HD>(r);
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const half8_t a = as_half8(*reinterpret_cast<const u32x4 *>(kr + 16 * ks));
-                acc = mfma32x32x16(a, qb[ks], acc);
+            for (int kk = 0; kk < KS; kk++) {
+                const half8_t a = as_half8(*reinterpret_cast<const u32x4 *>(kr + 8 * ((2 * kk + hgrp) ^ sw)));
+                acc = mfma32x32x16(a, qb[kk], acc);
             }
             sc[mt] = acc;
         }
@@ -173,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
             for (int v = 0; v < 16; v++) o[dt][v] *= corr;
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
-        // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7 -- the same keys the V^T operand reads below.
+        // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V.
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             half8_t pb;
@@ -181,11 +211,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
             for (int e = 0; e < 8; e++) pb[e] = (half_t)sc[u / 2][8 * (u % 2) + e];
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
-                const half_t * vr = &sm.vt[(32 * dt + l32) * kVtPitch + 16 * u + 4 * hgrp];
-                const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr);
-                const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 8);
-                const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-                o[dt] = mfma32x32x16(as_half8(a), pb, o[dt]);
+                short4_t t[2];
+#pragma unroll
+                for (int s8 = 0; s8 < 2; s8++) {
+                    const int r = 16 * u + 8 * s8 + 4 * hgrp + tr_row;
+                    const int c = 4 * dt + tr_c16;
+                    const half_t * addr = vs_ + r * HD + 8 * (c ^ swz<HD>(r)) + tr_half;
+                    t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) short4_t *)(addr));
+                }
+                const short4_t lo = t[0], hi = t[1];
+                const half8_t a = __builtin_bit_cast(half8_t, (short __attribute__((ext_vector_type(8)))){
+                    lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                o[dt] = mfma32x32x16(a, pb, o[dt]);
             }
         }
     }
