@@ -11,15 +11,16 @@
 //     vector ALU while the other's products run on the matrix core.
 //   * Key/value blocks of 64 rows pass through LDS, double-buffered: block i + 1 goes from registers into the free LDS
 //     buffer and block i + 2 is loaded from HBM/L2 into registers while block i is multiplied; one barrier per block.
-//     Both tiles are stored row-major, 16-byte chunks XOR-swizzled by row, so the K reads below and the transposing V
-//     reads are free of bank conflicts.
+//     Both tiles are stored row-major with padded rows, so the K reads below and the transposing V reads are free of
+//     bank conflicts and address with compile-time offsets.
 //   * Transposed scores: S^T (keys x queries) = K Q^T on v_mfma_f32_32x32x16_f16. In the result each lane holds 16 keys
 //     of ONE query (the lane 32 away the other 16), so the row max and sum need one cross-lane step, and the
 //     probabilities already sit in the B-operand layout of O^T += V^T P^T: P never touches LDS. Q^T is loaded once into
 //     registers. The V^T operand comes straight from the row-major V tile through ds_read_b64_tr_b16, whose 16-lane
 //     transpose hands every lane four consecutive keys of one head dimension.
-//   * The softmax runs in base 2 (scale * log2 e folded into one multiply), masking only in blocks that cross the
-//     causal diagonal or the end of the cache; blocks past a wave's last row are skipped.
+//   * The softmax runs in base 2: the block maximum is taken on raw scores and scale * log2 e folded into the FMA that
+//     feeds v_exp_f32; masking only in blocks that cross the causal diagonal or the end of the cache; blocks past a
+//     wave's last row are skipped; the output is rescaled only when the running maximum of some row moved.
 //   * Workgroups are dealt out so that the heaviest query tiles start first and the heads of one GQA group run next to
 //     each other on the same XCD (shared K/V in that XCD's L2).
 #include "mx_common.hpp"
@@ -35,22 +36,20 @@ constexpr int kBK = 64;  // keys per block
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
-// 16-byte chunk slot of chunk c in tile row r: c XOR a row-dependent mask. HD 128 (a row spans all 64 banks): 16
-// consecutive rows at one chunk hit 16 distinct slots, and rows 4k .. 4k + 3 at a chunk pair {2x, 2x + 1} hit 8
-// distinct slots. HD 64 (two rows per bank sweep): the same, for rows of one parity.
-template <int HD>
-__device__ __forceinline__ int swz(int r) {
-    if constexpr (HD == 128) return 2 * (r % 8) + (r / 8) % 2;
-    else return 2 * ((r / 2) % 4) + (r / 8) % 2;
-}
-
+// LDS tiles are row-major with padded rows: K rows HD + 8 halves apart (the 16-byte reads of 16 consecutive rows at one
+// column land on 16 distinct 4-bank groups), V rows HD + 16 halves apart (the 4 rows x 32 bytes a 16-lane group reads
+// through the transposing read land on disjoint banks). Every read address is a per-lane base plus a compile-time
+// offset, so the loop spends no ALU on addressing.
 template <int HD>
 struct PrefillSmem {
-    half_t k[2][kBK * HD];
-    half_t v[2][kBK * HD];
+    static constexpr int KP = HD + 8;
+    static constexpr int VP = HD + 16;
+    half_t k[2][kBK * KP];
+    half_t v[2][kBK * VP];
 };
 
-template <int HD>
+// POS: the scale is > 0, so the block maximum can be taken on raw scores and the scale folded into the exponent's FMA.
+template <int HD, bool POS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PrefillParams p) {
     constexpr int KS = HD / 16;          // MFMA steps along head_dim for S^T
@@ -58,6 +57,7 @@ void prefill_kernel(PrefillParams p) {
     constexpr int C8 = HD / 8;           // 16-byte chunks per key row
     constexpr int NB = (kBK / 16) * (C8 / 4);  // (16 keys x 4 chunks) load blocks per tile
     constexpr int NI = NB / kWaves;      // loads per thread per tile, for each of K and V
+    constexpr int KP = PrefillSmem<HD>::KP, VP = PrefillSmem<HD>::VP;
     __shared__ PrefillSmem<HD> sm;
 
     // ---- work item: heavy query tiles first, GQA groups adjacent, contiguous ranges per XCD ----
@@ -103,9 +103,8 @@ void prefill_kernel(PrefillParams p) {
             const int b = i * kWaves + wave;
             const int r = 16 * (b % (kBK / 16)) + lane % 16;
             const int c8 = 4 * (b / (kBK / 16)) + lane / 16;
-            const int o = r * HD + 8 * (c8 ^ swz<HD>(r));
-            *reinterpret_cast<u32x4 *>(&sm.k[buf][o]) = kreg[i];
-            *reinterpret_cast<u32x4 *>(&sm.v[buf][o]) = vreg[i];
+            *reinterpret_cast<u32x4 *>(&sm.k[buf][r * KP + 8 * c8]) = kreg[i];
+            *reinterpret_cast<u32x4 *>(&sm.v[buf][r * VP + 8 * c8]) = vreg[i];
         }
     };
 
@@ -125,6 +124,10 @@ void prefill_kernel(PrefillParams p) {
         store_tile(0);
         if (nblk > 1) load_tile(kBK);
     }
+    // Wait here for the query operand (and the prologue's loads): inside the loop the only loads in flight are then the
+    // prefetch of a later block, whose registers the block's math does not read, so no wait inside the loop has to
+    // drain them (a wait the compiler would otherwise place before the first product, serializing loads and math).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
     float16_t o[DT];
 #pragma unroll
@@ -133,10 +136,11 @@ void prefill_kernel(PrefillParams p) {
         for (int v = 0; v < 16; v++) o[dt][v] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
 
-    // lane-invariant parts of the LDS read addresses
-    const int tr_row = (lane % 16) / 4;                 // row offset inside a 4-key group of the transposing read
-    const int tr_c16 = 2 * ((lane / 16) % 2) + (lane % 4) / 2;  // 16-byte chunk (before the dt offset)
-    const int tr_half = 4 * (lane % 2);                 // 8-byte half inside the chunk, in elements
+    // per-lane LDS read bases (halves); everything else is a compile-time offset
+    const int k_base = l32 * KP + 8 * hgrp;  // K[32 mt + l32][16 kk + 8 hgrp]
+    // transposing read: lane a of 16-lane group c supplies V[4 hgrp + a / 4][16 (c % 2) + 4 (a % 4)] (+ 16 u + 8 s8 rows,
+    // + 32 dt columns) and receives V[rows + 0..3][32 dt + lane % 32]
+    const int v_base = (4 * hgrp + (lane % 16) / 4) * VP + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
 
     for (int ib = 0; ib < nblk; ib++) {
         const int kb = ib * kBK;
@@ -157,34 +161,34 @@ void prefill_kernel(PrefillParams p) {
             float16_t acc;
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[v] = 0.f;
-            const int r = 32 * mt + l32;
-            const half_t * kr = ks_ + r * HD;
-            const int sw = swz<HD>(r);
+            const half_t * kr = ks_ + k_base + 32 * mt * KP;
 #pragma unroll
             for (int kk = 0; kk < KS; kk++) {
-                const half8_t a = as_half8(*reinterpret_cast<const u32x4 *>(kr + 8 * ((2 * kk + hgrp) ^ sw)));
+                const half8_t a = as_half8(*reinterpret_cast<const u32x4 *>(kr + 16 * kk));
                 acc = mfma32x32x16(a, qb[kk], acc);
             }
             sc[mt] = acc;
         }
-        // scale, mask, block max
+        // block max (raw scores when the scale is positive), masking only where a block crosses the diagonal or the end
         const bool need_mask = (p.causal && kb + kBK - 1 > p.p0 + q0 + 32 * wave) || kb + kBK > p.n_kv;
+        const float c = p.scale_log2;
         float bmax = kNegInf;
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                float x = sc[mt][v] * p.scale_log2;
+                float x = POS ? sc[mt][v] : sc[mt][v] * c;
                 if (need_mask) {
                     const int key = kb + 32 * mt + 8 * (v / 4) + 4 * hgrp + (v % 4);
-                    if (key >= p.n_kv || (p.causal && key > qpos)) x = kNegInf;
+                    x = (key >= p.n_kv || (p.causal && key > qpos)) ? kNegInf : x;
                 }
                 sc[mt][v] = x;
                 bmax = fmaxf(bmax, x);
             }
         bmax = fmaxf(bmax, shfl_xor(bmax, 32));
-        const float m_new = fmaxf(m_run, bmax);
-        const bool none = m_new == kNegInf;
+        const float m_new = fmaxf(m_run, POS ? bmax * c : bmax);
+        const bool none = m_new == kNegInf;       // no visible key yet in this row
+        const float m_use = none ? 0.f : m_new;   // then every exponent below is 2^-inf = 0
         const float corr = none ? 1.f : exp2_fast(m_run - m_new);
         m_run = m_new;
         float bsum = 0.f;
@@ -192,15 +196,17 @@ void prefill_kernel(PrefillParams p) {
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const float e = none ? 0.f : exp2_fast(sc[mt][v] - m_new);
+                const float e = exp2_fast(POS ? __builtin_fmaf(sc[mt][v], c, -m_use) : sc[mt][v] - m_use);
                 sc[mt][v] = e;
                 bsum += e;
             }
         l_run = l_run * corr + bsum;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {  // the running max moved in some row of the wave
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+            for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+                for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+        }
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
         // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V.
@@ -214,9 +220,7 @@ void prefill_kernel(PrefillParams p) {
                 short4_t t[2];
 #pragma unroll
                 for (int s8 = 0; s8 < 2; s8++) {
-                    const int r = 16 * u + 8 * s8 + 4 * hgrp + tr_row;
-                    const int c = 4 * dt + tr_c16;
-                    const half_t * addr = vs_ + r * HD + 8 * (c ^ swz<HD>(r)) + tr_half;
+                    const half_t * addr = vs_ + v_base + (16 * u + 8 * s8) * VP + 32 * dt;
                     t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (__attribute__((address_space(3))) short4_t *)(addr));
                 }
@@ -250,10 +254,14 @@ void prefill_kernel(PrefillParams p) {
 
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream) {
     const dim3 grid((uint32_t)p.n_qtiles * p.n_head);
-    if (head_dim == 64)
-        hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kThreads), 0, stream, p);
-    else
-        hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, stream, p);
+    const bool pos = p.scale_log2 > 0.f;
+    if (head_dim == 64) {
+        if (pos) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((prefill_kernel<64, false>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        if (pos) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(kThreads), 0, stream, p);
+    }
     return hipGetLastError();
 }
 
