@@ -20,7 +20,7 @@
 //     transpose hands every lane four consecutive keys of one head dimension.
 //   * The softmax runs in base 2: the block maximum is taken on raw scores and scale * log2 e folded into the FMA that
 //     feeds v_exp_f32; masking only in blocks that cross the causal diagonal or the end of the cache; blocks past a
-//     wave's last row are skipped; the output is rescaled only when the running maximum of some row moved.
+//     wave's last row are skipped.
 //   * Workgroups are dealt out so that the heaviest query tiles start first and the heads of one GQA group run next to
 //     each other on the same XCD (shared K/V in that XCD's L2).
 #include "mx_common.hpp"
@@ -71,7 +71,8 @@ void prefill_kernel(PrefillParams p) {
     const int h = kvh * G + gi;
     const int q0 = qt * kPrefillRows;
 
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform, in a scalar register
+    const int lane = threadIdx.x % kWave;
     const int l32 = lane % 32, hgrp = lane / 32;
     const int qrow = q0 + 32 * wave + l32;      // this lane's query row (chunk index)
     const int qpos = p.p0 + qrow;               // its cache position
@@ -169,22 +170,32 @@ void prefill_kernel(PrefillParams p) {
             }
             sc[mt] = acc;
         }
-        // block max (raw scores when the scale is positive), masking only where a block crosses the diagonal or the end
+        // block max (raw scores when the scale is positive); the mask only where a block crosses the diagonal or the
+        // end of the cache (a wave-uniform branch)
         const bool need_mask = (p.causal && kb + kBK - 1 > p.p0 + q0 + 32 * wave) || kb + kBK > p.n_kv;
         const float c = p.scale_log2;
         float bmax = kNegInf;
+        if (need_mask) {
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
+            for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                float x = POS ? sc[mt][v] : sc[mt][v] * c;
-                if (need_mask) {
+                for (int v = 0; v < 16; v++) {
                     const int key = kb + 32 * mt + 8 * (v / 4) + 4 * hgrp + (v % 4);
-                    x = (key >= p.n_kv || (p.causal && key > qpos)) ? kNegInf : x;
+                    const bool hide = key >= p.n_kv || (p.causal && key > qpos);
+                    const float x = hide ? kNegInf : (POS ? sc[mt][v] : sc[mt][v] * c);
+                    sc[mt][v] = x;
+                    bmax = fmaxf(bmax, x);
                 }
-                sc[mt][v] = x;
-                bmax = fmaxf(bmax, x);
-            }
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const float x = POS ? sc[mt][v] : sc[mt][v] * c;
+                    sc[mt][v] = x;
+                    bmax = fmaxf(bmax, x);
+                }
+        }
         bmax = fmaxf(bmax, shfl_xor(bmax, 32));
         const float m_new = fmaxf(m_run, POS ? bmax * c : bmax);
         const bool none = m_new == kNegInf;       // no visible key yet in this row
@@ -201,12 +212,10 @@ void prefill_kernel(PrefillParams p) {
                 bsum += e;
             }
         l_run = l_run * corr + bsum;
-        if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {  // the running max moved in some row of the wave
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
+        for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) o[dt][v] *= corr;
-        }
+            for (int v = 0; v < 16; v++) o[dt][v] *= corr;
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
         // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V.
