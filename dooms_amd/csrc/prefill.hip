@@ -20,7 +20,7 @@
 //     transpose hands every lane four consecutive keys of one head dimension.
 //   * The softmax runs in base 2: the block maximum is taken on raw scores and scale * log2 e folded into the FMA that
 //     feeds v_exp_f32; masking only in blocks that cross the causal diagonal or the end of the cache; blocks past a
-//     wave's last row are skipped.
+//     wave's last row are skipped; the output is rescaled only when the running maximum of some row moved.
 //   * Workgroups are dealt out so that the heaviest query tiles start first and the heads of one GQA group run next to
 //     each other on the same XCD (shared K/V in that XCD's L2).
 #include "mx_common.hpp"
@@ -71,7 +71,7 @@ void prefill_kernel(PrefillParams p) {
     const int h = kvh * G + gi;
     const int q0 = qt * kPrefillRows;
 
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform, in a scalar register
+    const int wave = threadIdx.x / kWave;  // wave-uniform, in a scalar register
     const int lane = threadIdx.x % kWave;
     const int l32 = lane % 32, hgrp = lane / 32;
     const int qrow = q0 + 32 * wave + l32;      // this lane's query row (chunk index)
@@ -155,20 +155,26 @@ void prefill_kernel(PrefillParams p) {
         const half_t * ks_ = sm.k[buf];
         const half_t * vs_ = sm.v[buf];
 
-        // S^T = K Q^T: 2 tiles of 32 keys
+        // S^T = K Q^T: 2 tiles of 32 keys. The K operand of step i + 1 is read before the product of step i, so each
+        // product waits only for reads issued one product earlier.
         float16_t sc[2];
+        {
+            constexpr int NS = 2 * KS;  // products: (mt, kk) in order
+            u32x4 ka[2];
+            auto kread = [&](int i) {
+                return *reinterpret_cast<const u32x4 *>(ks_ + k_base + 32 * (i / KS) * KP + 16 * (i % KS));
+            };
+            ka[0] = kread(0);
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            float16_t acc;
+            for (int i = 0; i < NS; i++) {
+                if (i + 1 < NS) ka[(i + 1) & 1] = kread(i + 1);
+                const int mt = i / KS, kk = i % KS;
+                if (kk == 0) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[v] = 0.f;
-            const half_t * kr = ks_ + k_base + 32 * mt * KP;
-#pragma unroll
-            for (int kk = 0; kk < KS; kk++) {
-                const half8_t a = as_half8(*reinterpret_cast<const u32x4 *>(kr + 16 * kk));
-                acc = mfma32x32x16(a, qb[kk], acc);
+                    for (int v = 0; v < 16; v++) sc[mt][v] = 0.f;
+                }
+                sc[mt] = mfma32x32x16(as_half8(ka[i & 1]), qb[kk], sc[mt]);
             }
-            sc[mt] = acc;
         }
         // block max (raw scores when the scale is positive); the mask only where a block crosses the diagonal or the
         // end of the cache (a wave-uniform branch)
@@ -212,31 +218,39 @@ void prefill_kernel(PrefillParams p) {
                 bsum += e;
             }
         l_run = l_run * corr + bsum;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {  // the running max moved in some row of the wave
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+            for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+                for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+        }
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
-        // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V.
+        // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V. The reads of
+        // product i + 1 are issued before product i.
+        {
+            constexpr int NP = 4 * DT;  // products: (u, dt) in order
+            short4_t vt[2][2];
+            auto vread = [&](int i, short4_t (&t)[2]) {
+                const int u = i / DT, dt = i % DT;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            half8_t pb;
+                for (int s8 = 0; s8 < 2; s8++)
+                    t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)(
+                        vs_ + v_base + (16 * u + 8 * s8) * VP + 32 * dt));
+            };
+            half8_t pb[4];
 #pragma unroll
-            for (int e = 0; e < 8; e++) pb[e] = (half_t)sc[u / 2][8 * (u % 2) + e];
+            for (int u = 0; u < 4; u++)
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                short4_t t[2];
+                for (int e = 0; e < 8; e++) pb[u][e] = (half_t)sc[u / 2][8 * (u % 2) + e];
+            vread(0, vt[0]);
 #pragma unroll
-                for (int s8 = 0; s8 < 2; s8++) {
-                    const half_t * addr = vs_ + v_base + (16 * u + 8 * s8) * VP + 32 * dt;
-                    t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) short4_t *)(addr));
-                }
-                const short4_t lo = t[0], hi = t[1];
+            for (int i = 0; i < NP; i++) {
+                if (i + 1 < NP) vread(i + 1, vt[(i + 1) & 1]);
+                const short4_t lo = vt[i & 1][0], hi = vt[i & 1][1];
                 const half8_t a = __builtin_bit_cast(half8_t, (short __attribute__((ext_vector_type(8)))){
                     lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-                o[dt] = mfma32x32x16(a, pb, o[dt]);
+                o[i % DT] = mfma32x32x16(a, pb[i / DT], o[i % DT]);
             }
         }
     }
