@@ -146,7 +146,8 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
     p.p0 = d.p0;
     p.n_kv = (int32_t)n_kv;
     p.causal = d.causal;
-    p.n_qtiles = (d.n_q + mx::kPrefillRows - 1) / mx::kPrefillRows;
+    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head);
+    p.n_qtiles = (d.n_q + rows - 1) / rows;
     p.scale_log2 = d.scale * 1.4426950408889634f;
     return hip_status(mx::launch_prefill(p, d.head_dim, static_cast<hipStream_t>(stream)), "prefill launch");
 }

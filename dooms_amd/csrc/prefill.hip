@@ -6,9 +6,9 @@
 // m and sum l with the rescale factor exp(m_old - m_new), P rounded to half, O += P V, and O / l at the end.
 //
 // MI355X design:
-//   * One workgroup = 4 waves = 128 query rows of one query head; each wave owns 32 rows. Two workgroups per CU (the
-//     register budget is held to 256 per lane), so each SIMD interleaves two waves: one wave's softmax runs on the
-//     vector ALU while the other's products run on the matrix core.
+//   * One workgroup = 8 waves = 256 query rows of one query head (4 waves = 128 rows for short prompts); each wave owns
+//     32 rows. The register budget is held to 256 per lane, so each SIMD interleaves two waves: one wave's softmax runs
+//     on the vector ALU while the other's products run on the matrix core; all waves of a CU share each K/V tile.
 //   * Key/value blocks of 64 rows pass through LDS, double-buffered: block i + 1 goes from registers into the free LDS
 //     buffer and block i + 2 is loaded from HBM/L2 into registers while block i is multiplied; one barrier per block.
 //     Both tiles are stored row-major with padded rows, so the K reads below and the transposing V reads are free of
@@ -30,8 +30,6 @@ namespace mx {
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * kWave;
 constexpr int kBK = 64;  // keys per block
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -49,9 +47,11 @@ struct PrefillSmem {
 };
 
 // POS: the scale is > 0, so the block maximum can be taken on raw scores and the scale folded into the exponent's FMA.
-template <int HD, bool POS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// W: waves per workgroup (32 query rows each); all W waves share each K/V tile in LDS.
+template <int HD, bool POS, int W>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PrefillParams p) {
+    constexpr int kWaves = W, kPrefillRows = 32 * W;
     constexpr int KS = HD / 16;          // MFMA steps along head_dim for S^T
     constexpr int DT = HD / 32;          // 32-wide output tiles along head_dim
     constexpr int C8 = HD / 8;           // 16-byte chunks per key row
@@ -275,15 +275,33 @@ void prefill_kernel(PrefillParams p) {
 
 }  // namespace
 
-hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream) {
+// Waves per workgroup: 8 (256 query rows, every K/V tile shared by all 8 waves of a CU) when that gives workgroups for
+// at least half of the CUs (measured: a 2048-row chunk of 28 heads, 224 workgroups, runs ~20 % faster than with 448
+// workgroups of 4 waves), else 4 (128 rows), so that short prompts spread over the chip.
+constexpr int kCUs = 256;
+int prefill_waves(int n_q, int n_head) {
+    const int64_t tiles8 = (int64_t)((n_q + 255) / 256) * n_head;
+    return tiles8 >= kCUs / 2 ? 8 : 4;
+}
+
+int prefill_rows_per_workgroup(int n_q, int n_head) { return 32 * prefill_waves(n_q, n_head); }
+
+template <int HD, bool POS>
+void launch_prefill_t(const PrefillParams & p, int waves, hipStream_t stream) {
     const dim3 grid((uint32_t)p.n_qtiles * p.n_head);
+    if (waves == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8>), grid, dim3(8 * kWave), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4>), grid, dim3(4 * kWave), 0, stream, p);
+}
+
+hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream) {
     const bool pos = p.scale_log2 > 0.f;
+    const int waves = prefill_waves(p.n_q, p.n_head);
     if (head_dim == 64) {
-        if (pos) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((prefill_kernel<64, false>), grid, dim3(kThreads), 0, stream, p);
+        if (pos) launch_prefill_t<64, true>(p, waves, stream);
+        else launch_prefill_t<64, false>(p, waves, stream);
     } else {
-        if (pos) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(kThreads), 0, stream, p);
+        if (pos) launch_prefill_t<128, true>(p, waves, stream);
+        else launch_prefill_t<128, false>(p, waves, stream);
     }
     return hipGetLastError();
 }
