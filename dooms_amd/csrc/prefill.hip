@@ -35,13 +35,14 @@ constexpr int kBK = 64;  // keys per block
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // LDS tiles are row-major with padded rows: K rows HD + 8 halves apart (the 16-byte reads of 16 consecutive rows at one
-// column land on 16 distinct 4-bank groups), V rows HD + 16 halves apart (the 4 rows x 32 bytes a 16-lane group reads
-// through the transposing read land on disjoint banks). Every read address is a per-lane base plus a compile-time
+// column land on 16 distinct 4-bank groups), V rows HD + 32 halves apart (a row step of 16 banks mod 64: the 4 rows x
+// 32 bytes that each 16-lane group reads through the transposing read, for both groups of a 32-lane phase, land on 64
+// distinct banks; the tile store writes 4 rows x 4 chunks per 16 lanes, also 16 distinct 4-bank groups). Every read address is a per-lane base plus a compile-time
 // offset, so the loop spends no ALU on addressing.
 template <int HD>
 struct PrefillSmem {
     static constexpr int KP = HD + 8;
-    static constexpr int VP = HD + 16;
+    static constexpr int VP = HD + 32;
     half_t k[2][kBK * KP];
     half_t v[2][kBK * VP];
 };
@@ -85,27 +86,29 @@ void prefill_kernel(PrefillParams p) {
 
     const half_t * kg = p.k + (int64_t)kvh * HD;
     const half_t * vg = p.v + (int64_t)kvh * HD;
-    // tile-load mapping: block b = i * 4 + wave covers keys 16 (b % 4) + lane % 16 and chunks 4 (b / 4) + lane / 16
+    // tile-load mapping, block b = i * W + wave of 16 rows x 4 chunks (64 contiguous bytes per row):
+    //   K: row 16 (b % 4) + lane % 16, chunk 4 (b / 4) + lane / 16 (16 lanes of one LDS write phase: 16 rows, one chunk)
+    //   V: row 16 (b % 4) + 4 (lane / 16) + (lane % 16) / 4, chunk 4 (b / 4) + lane % 4 (16 lanes: 4 rows x 4 chunks)
     u32x4 kreg[NI], vreg[NI];
+    auto krow = [&](int b) { return 16 * (b % (kBK / 16)) + lane % 16; };
+    auto kchunk = [&](int b) { return 4 * (b / (kBK / 16)) + lane / 16; };
+    auto vrow = [&](int b) { return 16 * (b % (kBK / 16)) + 4 * (lane / 16) + (lane % 16) / 4; };
+    auto vchunk = [&](int b) { return 4 * (b / (kBK / 16)) + lane % 4; };
     auto load_tile = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
-            const int key = min(kb + 16 * (b % (kBK / 16)) + lane % 16, p.n_kv - 1);
-            const int c8 = 4 * (b / (kBK / 16)) + lane / 16;
-            const int64_t off = (int64_t)key * p.kv_stride + 8 * c8;
-            kreg[i] = load16(kg + off);
-            vreg[i] = load16(vg + off);
+            const int kkey = min(kb + krow(b), p.n_kv - 1), vkey = min(kb + vrow(b), p.n_kv - 1);
+            kreg[i] = load16(kg + (int64_t)kkey * p.kv_stride + 8 * kchunk(b));
+            vreg[i] = load16(vg + (int64_t)vkey * p.kv_stride + 8 * vchunk(b));
         }
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
-            const int r = 16 * (b % (kBK / 16)) + lane % 16;
-            const int c8 = 4 * (b / (kBK / 16)) + lane / 16;
-            *reinterpret_cast<u32x4 *>(&sm.k[buf][r * KP + 8 * c8]) = kreg[i];
-            *reinterpret_cast<u32x4 *>(&sm.v[buf][r * VP + 8 * c8]) = vreg[i];
+            *reinterpret_cast<u32x4 *>(&sm.k[buf][krow(b) * KP + 8 * kchunk(b)]) = kreg[i];
+            *reinterpret_cast<u32x4 *>(&sm.v[buf][vrow(b) * VP + 8 * vchunk(b)]) = vreg[i];
         }
     };
 
