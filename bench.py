@@ -9,10 +9,11 @@ Beside it (same JSON line): prefill TFLOP/s on the Qwen2.5-7B 32k-token causal p
 BASELINE configurations, a same-run streaming-copy bandwidth, and the reference's CPU attention (restated in
 oracle/oracle.c) timed on this host's cores on a bounded sample.
 
-Timing: the value pass replays a HIP graph of one step (the decode step is 32 launches of a few microseconds, too short
+Timing: every figure replays a HIP graph of one step (the decode step is 32 launches of a few microseconds, too short
 to issue from Python one by one); K steps are bracketed by synchronize() on both sides and timed with events on the
-stream the kernels run on. Per-kernel durations (roofline) come from event pairs around eager launches queued behind a
-busy kernel, so host issue time is not counted.
+stream the kernels run on. The roofline's per-launch duration is that timed region divided by the launches in it
+(so it includes the gaps between back-to-back launches); rocprofv3's kernel durations for the same command are in
+profiles/. HBM traffic per launch comes from rocprofv3 --pmc runs recorded in profiles/traffic.json.
 
 Algorithmic work (what `achieved` divides):
   decode bytes per (sequence, layer) = 2 * L * n_kv * hd * 2 (K+V, f16, each byte once) + 2 * n_head * hd * 2 (Q, O)
@@ -42,18 +43,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget per leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "all", "decode-headline", "prefill-headline"], default="all",
+                    help="*-headline: only the headline workload of that path (for profiling one kernel)")
     return ap.parse_args()
-
-
-def busy(torch, ms=30.0):
-    """Keeps the stream busy for about `ms` so that launches queued behind it run back to back."""
-    try:
-        torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
-    except Exception:
-        a = torch.empty(4096, 4096, dtype=torch.float16, device="cuda")
-        for _ in range(int(ms / 0.15) + 1):
-            a @ a
 
 
 def time_graph(torch, step, steps, warmup):
@@ -79,20 +71,14 @@ def time_graph(torch, step, steps, warmup):
     return t0.elapsed_time(t1) / steps, g
 
 
-def time_launches(torch, launches, reps=1):
-    """Per-launch GPU durations (ms) of the callables in `launches`, queued behind a busy kernel."""
-    torch.cuda.synchronize()
-    busy(torch, 20.0 + 0.05 * len(launches) * reps)
-    evs = []
-    for _ in range(reps):
-        for f in launches:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            f()
-            b.record()
-            evs.append((a, b))
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs]
+def measured_traffic(key):
+    """HBM bytes per launch of a headline kernel as measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs and
+    committed in profiles/traffic.json (with the commands and the copy-kernel scale factors), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)["workloads"][key]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def decode_bytes(L, n_head, n_kv, hd):
@@ -282,16 +268,16 @@ def main():
     model, ncpu = cpu_info()
     threads = max(1, min(16, ncpu))
 
-    if args.only in ("decode", "all"):
+    if args.only in ("decode", "all", "decode-headline"):
         # ---- headline: cfg3 decode, batch 1, L = 8192, 32 layers per step ----
         L = 8192
         dp = DecodeProblem(torch, gen, 32, 8, 128, [L], layers=32)
         ms, _ = time_graph(torch, dp.step, K, W)
         bpl = dp.bytes_per_launch()
         value = 32 * bpl / (ms * 1e-3) / 1e9
-        durs = time_launches(torch, [lambda l=l: dp.launch(l) for l in range(32)], reps=3)
-        avg = float(np.mean(durs))
-        achieved = bpl / (avg * 1e-3) / 1e9
+        avg_us = ms * 1e3 / 32  # one launch per layer, back to back in the graph
+        achieved = bpl / (avg_us * 1e-6) / 1e9
+        traffic = measured_traffic("decode_llama3_8b_b1_L8192")
         result.update({
             "value": round(value, 1), "ms_per_step": round(ms, 4),
             "config": {"workload": "cfg3 Llama-3-8B decode attention: 32 q / 8 kv heads, head_dim 128, batch 1, "
@@ -299,9 +285,10 @@ def main():
                                    "K/V (1.07 GB per step)",
                        "batch": 1, "kv_len": L, "layers_per_step": 32, "n_head": 32, "n_head_kv": 8, "head_dim": 128,
                        "timing": "HIP graph replay of the 32-launch step, events on the launch stream"},
-            "roofline": {"bound": "hbm", "kernel": "decode_split_kernel<128,4>", "achieved": round(achieved, 1),
+            "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,4>", "achieved": round(achieved, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                         "traffic": None, "bytes_per_launch": bpl, "avg_launch_us": round(avg * 1e3, 3)},
+                         "traffic": traffic, "bytes_per_launch": bpl, "avg_launch_us": round(avg_us, 3),
+                         "launch_timing": "graph-timed region / launches (includes the gaps between launches)"},
         })
         if not args.no_cpu:
             v1, n1, t1 = cpu_decode_baseline(torch, dp, args.cpu_seconds, threads)
@@ -315,6 +302,7 @@ def main():
         del dp
         torch.cuda.empty_cache()
 
+    if args.only in ("decode", "all"):
         # ---- cfg3 batched: lengths U[1024, 8192] by seed 3 ----
         rng = np.random.default_rng(3)
         for B in (4, 16):
@@ -348,24 +336,24 @@ def main():
             del ws, wc
         torch.cuda.empty_cache()
 
-    if args.only in ("prefill", "all"):
+    if args.only in ("prefill", "all", "prefill-headline"):
         # ---- cfg5 Qwen2.5-7B 32k causal prefill in 2048-query chunks ----
         pp = PrefillProblem(torch, gen, 28, 4, 128, 32768, 2048, sigma=0.5)
         ms_p, _ = time_graph(torch, pp.step, max(3, K // 4), max(1, W // 2))
         fl = pp.flops_per_layer()
         tflops = fl / (ms_p * 1e-3) / 1e12
-        durs = time_launches(torch, [lambda ci=ci: pp.launch(0, ci) for ci in range(len(pp.chunks))], reps=2)
-        kt = float(np.sum(durs)) / 2
-        ach = fl / (kt * 1e-3) / 1e12
+        avg_us = ms_p * 1e3 / len(pp.chunks)
         pre = {"metric": "prefill-attn TFLOP/s", "value": round(tflops, 1), "unit": "TFLOP/s",
                "ms_per_step": round(ms_p, 3),
                "workload": "cfg5 Qwen2.5-7B causal prefill: 28 q / 4 kv heads, head_dim 128, 32768 tokens in 16 "
                            "chunks of 2048 queries against the growing f16 cache, N(0, 0.5) inputs; FLOPs count "
                            "unmasked pairs only (7.697 TFLOP per step)",
                "flops_per_step": fl,
-               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128>", "achieved": round(ach, 1),
-                            "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / F16_PEAK_TFLOPS, 4),
-                            "traffic": None, "avg_launch_us": round(kt / len(pp.chunks) * 1e3, 2)}}
+               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128,true,8>", "achieved": round(tflops, 1),
+                            "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / F16_PEAK_TFLOPS, 4),
+                            "traffic": measured_traffic("prefill_qwen7b_32k"), "avg_launch_us": round(avg_us, 2),
+                            "launch_timing": "graph-timed region / launches; FLOPs per launch differ by chunk, so "
+                                             "achieved = all FLOPs / all launch time"}}
         if not args.no_cpu:
             v1, rows, t1 = cpu_prefill_baseline(torch, pp, args.cpu_seconds, threads)
             pre["cpu_baseline"] = {"value": round(v1, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
@@ -376,20 +364,20 @@ def main():
         del pp
         torch.cuda.empty_cache()
 
+    if args.only in ("prefill", "all"):
         # ---- cfg2 Qwen2.5-0.5B 512-token prompt: per layer and over 24 layers ----
         p2 = PrefillProblem(torch, gen, 14, 2, 64, 512, 512, layers=24)
         ms_2, _ = time_graph(torch, p2.step, K, W)
-        d2 = time_launches(torch, [lambda l=l: p2.launch(l, 0) for l in range(24)], reps=2)
         fl2 = p2.flops_per_layer()
         extra["prefill_qwen05b_512"] = {
-            "ms_24_layers": round(ms_2, 4), "us_per_layer": round(float(np.mean(d2)) * 1e3, 2),
+            "ms_24_layers": round(ms_2, 4), "us_per_layer": round(ms_2 * 1e3 / 24, 2),
             "TFLOPs": round(24 * fl2 / (ms_2 * 1e-3) / 1e12, 2),
             "reference_published_ms": 13.9,
             "reference_note": "M1 Pro GPU time of prompt attention for a 512-token prompt (site/data.js:142-146); "
                               "a different metric and machine, so vs_baseline stays null"}
         del p2
 
-    if "value" not in result:  # --only prefill: the prefill figure is the line's value
+    if "value" not in result:  # --only prefill*: the prefill figure is the line's value
         pre = result["prefill"]
         result.update({"value": pre["value"], "unit": pre["unit"], "ms_per_step": pre["ms_per_step"],
                        "config": {"workload": pre["workload"]}, "roofline": pre["roofline"]})
