@@ -13,9 +13,10 @@
 //     processed together, so each K/V byte is read from HBM once, not G times as in the reference's per-head kernels.
 //   * Scores on the matrix cores: S^T (16 keys x 16 rows) = K (16 keys x head_dim) . Q^T, v_mfma_f32_16x16x32_f16. K goes
 //     from HBM straight into the MFMA operand registers with 16-byte loads (4 lanes cover 64 contiguous bytes of a row).
-//   * Probabilities times values on the vector ALUs: each lane owns 8 contiguous head dimensions of a value row (one
-//     16-byte load) and accumulates rows x 8 f32 sums; the probabilities come from LDS as broadcast reads. At decode's
-//     4 FLOP per byte this keeps the ALUs well under the HBM rate.
+//   * Probabilities times values on the matrix cores too: O^T (head dims x rows) += V^T P^T. Each wave stages its 32-key
+//     V block row-major in LDS and reads the V^T operand back through ds_read_b64_tr_b16 (whose 16-lane transpose
+//     hands each lane 4 consecutive keys of one head dimension); P^T is the score MFMA's result layout, rounded to
+//     f16, so the probabilities never leave registers and the vector ALUs only run the softmax.
 //   * Each wave walks 32-key blocks of its workgroup's split with the next block's K/V already in flight (register
 //     double buffer); the 4 waves are merged through LDS.
 //   * Splits are merged inside the same launch: each workgroup publishes its partial (acc[head_dim], m, l per row) with
@@ -35,7 +36,9 @@ constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kBlockKeys = 32;  // keys per wave iteration
 
-constexpr int kMergeChunk = 32;  // splits whose partials one thread has in flight at once during the merge
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMergeChunk = 16;  // splits whose partials one thread has in flight at once during the merge
 
 // Relaxed device-scope atomic accesses of float pairs: coherent across the XCDs without cache maintenance.
 __device__ __forceinline__ void publish2(float * p, float a, float b) {
@@ -65,8 +68,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     using B = KvBlock<HD>;
     constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
 
-    __shared__ float s_p[kDecodeWaves][kBlockKeys * RT];
-    __shared__ float s_corr[kDecodeWaves][RT];
+    constexpr int VP = HD + 16;  // halves per row of a wave's V block in LDS (conflict-free transposing reads)
+    __shared__ half_t s_v[kDecodeWaves][kBlockKeys * VP];
     __shared__ float s_m[kDecodeWaves][RT], s_l[kDecodeWaves][RT];
     __shared__ float s_o[kDecodeWaves][RT * HD];
     __shared__ int s_last;
@@ -129,16 +132,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     if (jb < j1) load_block(jb, cur);
 
     float m_run = kNegInf, l_run = 0.f;  // per score lane (row srow); l is this lane's partial sum
-    float o[RT][8];
+    // O^T accumulators (16 head dims x 16 rows per tile): lane holds O[row srow][16 dtile + 4 sgrp + v], v = 0..3
+    float4_t o[HD / 16];
 #pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[r][e] = 0.f;
+    for (int dt = 0; dt < HD / 16; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    // transposing read of V^T: lane a of 16-lane group g supplies V[4 g + a / 4 (+ 16)][16 dtile + 4 (a % 4)] and
+    // receives V[4 g + 0..3 (+ 16)][16 dtile + a]
+    half_t * vw = s_v[wave];
+    const int v_rd = (4 * sgrp + (lane % 16) / 4) * VP + 4 * (lane % 4);
 
     for (; jb < j1; jb += kBlockKeys * kDecodeWaves) {
         const int jn = jb + kBlockKeys * kDecodeWaves;
         if (jn < j1) load_block(jn, nxt);
-        // S^T = K Q^T, 2 tiles of 16 keys
+        // S^T = K Q^T, 2 tiles of 16 keys: lane holds keys 16 mt + 4 sgrp + v of row srow
         float sc[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
@@ -159,48 +165,38 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
         bmax = fmaxf(bmax, shfl_xor(bmax, 16));
         bmax = fmaxf(bmax, shfl_xor(bmax, 32));
         const float m_new = fmaxf(m_run, bmax);
-        const bool none = m_new == kNegInf;  // no visible key yet for this row
+        const bool none = m_new == kNegInf;      // no visible key yet for this row
+        const float m_use = none ? 0.f : m_new;  // then every exponent below is 2^-inf = 0
         const float corr = none ? 1.f : exp2_fast(m_run - m_new);
+        half8_t pb;  // P^T operand: slot (sgrp, e) is key 16 (e / 4) + 4 sgrp + e % 4, the same keys the V^T reads fetch
         float bsum = 0.f;
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float pv = none ? 0.f : exp2_fast(sc[mt][v] - m_new);
-                sc[mt][v] = pv;
-                bsum += pv;
-            }
+        for (int e = 0; e < 8; e++) {
+            const float pv = exp2_fast(sc[e / 4][e % 4] - m_use);
+            bsum += pv;
+            pb[e] = (half_t)pv;
+        }
         l_run = l_run * corr + bsum;
         m_run = m_new;
-        if (srow < RT) {
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
+        for (int dt = 0; dt < HD / 16; dt++) o[dt] *= corr;
+        // the wave's V block into LDS, row-major (one 16-byte chunk per lane per load)
 #pragma unroll
-                for (int v = 0; v < 4; v++) s_p[wave][(16 * mt + 4 * sgrp + v) * RT + srow] = sc[mt][v];
-            if (sgrp == 0) s_corr[wave][srow] = corr;
-        }
+        for (int i = 0; i < NLV; i++)
+            *reinterpret_cast<u32x4 *>(vw + (KPL * i + vslot) * VP + vcol) = cur.v[i];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O = diag(corr) O + P V over this lane's value rows
-        float cr[RT];
+        // O^T += V^T P^T on the matrix cores, one 16x16x32 product per 16 head dims
 #pragma unroll
-        for (int r = 0; r < RT; r++) cr[r] = s_corr[wave][r];
-#pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) o[r][e] *= cr[r];
-#pragma unroll
-        for (int i = 0; i < NLV; i++) {
-            const half8_t vv = as_half8(cur.v[i]);
-            const float * pk = &s_p[wave][(KPL * i + vslot) * RT];
-            float pr[RT];
-#pragma unroll
-            for (int r = 0; r < RT; r++) pr[r] = pk[r];
-#pragma unroll
-            for (int r = 0; r < RT; r++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) o[r][e] = __builtin_fmaf(pr[r], (float)vv[e], o[r][e]);
+        for (int dt = 0; dt < HD / 16; dt++) {
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4_t *)(vw + v_rd + 16 * dt));
+            const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4_t *)(vw + v_rd + 16 * VP + 16 * dt));
+            const half8_t a = __builtin_bit_cast(half8_t, (short __attribute__((ext_vector_type(8)))){
+                lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+            o[dt] = mfma16x16x32(a, pb, o[dt]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -208,27 +204,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
         cur = nxt;
     }
 
-    // ---- wave totals: l over the 4 score-lane groups, O over the value slots ----
+    // ---- wave totals: l over the 4 score-lane groups; O is complete per lane (the products summed every key) ----
     l_run += shfl_xor(l_run, 16);
     l_run += shfl_xor(l_run, 32);
-#pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float v = o[r][e];
-#pragma unroll
-            for (int msk = LPR; msk < kWave; msk *= 2) v += shfl_xor(v, msk);
-            o[r][e] = v;
-        }
     if (lane < RT) {
         s_m[wave][lane] = m_run;
         s_l[wave][lane] = l_run;
     }
-    if (lane < LPR) {
+    if (srow < RT) {
 #pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) s_o[wave][r * HD + vcol + e] = o[r][e];
+        for (int dt = 0; dt < HD / 16; dt++)
+            *reinterpret_cast<float4_t *>(&s_o[wave][srow * HD + 16 * dt + 4 * sgrp]) = o[dt];
     }
     __syncthreads();
 
