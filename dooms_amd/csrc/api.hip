@@ -62,13 +62,17 @@ int32_t hip_status(hipError_t e, const char * what) {
     return fail(MX_ATTN_INTERNAL, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Decode split plan. Splits are a multiple of kDecodeChunkQuantum keys, sized so that the launch has about
-// target_workgroups() workgroups (one per CU on MI355X's 256 CUs; fewer, longer splits keep the in-kernel merge short)
-// and never more splits per sequence than ceil(len / quantum), which bounds the workspace by the longest sequence.
-int target_workgroups() {
+// Decode split plan. Splits are whole multiples of kDecodeChunkQuantum keys, and
+//   * at least kMinChunk keys and at most kMaxSplits splits per sequence: every extra split lengthens the in-kernel
+//     merge (measured: 64 splits of an 8192-key Llama-3-8B row cost ~5 us more than 32);
+//   * then as small as possible while the launch stays within workgroup_cap() workgroups (measured on MI355X for
+//     Llama-3-8B batches of 4 and 16: 1536 streams best; two workgroups per CU are resident at once, 512 in all).
+// The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
+constexpr int kMinChunk = 256, kMaxSplits = 32;
+int workgroup_cap() {
     const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
     const int v = s ? std::atoi(s) : 0;
-    return v > 0 ? v : 256;
+    return v > 0 ? v : 1536;
 }
 
 struct DecodeShape {
@@ -219,13 +223,27 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
         p.n_rowtiles = s.n_rowtiles;
         p.seq0 = b0;
         p.scale_log2 = d.scale * 1.4426950408889634f;
-        // split plan: total key-work of the launch over the target workgroup count, in whole quanta
-        int64_t keys = 0;
-        for (int i = 0; i < n_seq; i++) keys += kv_len[b0 + i];
-        const int64_t work = keys * d.n_head_kv * s.n_rowtiles;
+        // split plan (see workgroup_cap)
         const int64_t quantum = mx::kDecodeChunkQuantum;
-        int64_t chunk = (work + target_workgroups() - 1) / target_workgroups();
-        chunk = std::max<int64_t>(quantum, (chunk + quantum - 1) / quantum * quantum);
+        int64_t lmax = 0;
+        for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
+        auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
+        int64_t chunk = std::max<int64_t>(round_up(kMinChunk), round_up((lmax + kMaxSplits - 1) / kMaxSplits));
+        auto launch_wgs = [&](int64_t c) {
+            int64_t n = 0;
+            for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
+            return n * d.n_head_kv * s.n_rowtiles;
+        };
+        const int64_t cap = workgroup_cap();
+        if (launch_wgs(chunk) > cap) {  // smallest chunk within the cap: bisect over multiples of the quantum
+            int64_t lo = chunk / quantum, hi = round_up(lmax) / quantum;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi) / 2;
+                if (launch_wgs(mid * quantum) > cap) lo = mid + 1;
+                else hi = mid;
+            }
+            chunk = lo * quantum;
+        }
         p.chunk = (int32_t)std::min<int64_t>(chunk, INT32_MAX / 2);
         p.max_split = 1;
         for (int i = 0; i < n_seq; i++) {
