@@ -35,5 +35,23 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host_attention.cpp")
+TEST_BIN = os.path.join(ROOT, "tests", "cpp", "test_host_attention")
+
+
+def build_host_test() -> str:
+    """Compiles the C++ host-layer test (tests/cpp) against libmx_attn.so and the CPU oracle (oracle/liboracle.so)."""
+    oracle_dir = os.path.join(ROOT, "oracle")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall", "-Werror",
+           "-I", os.path.join(ROOT, "include"), "-I", os.path.join(PKG, "host"), TEST_SRC,
+           "-L", PKG, "-lmx_attn", "-L", oracle_dir, "-loracle",
+           "-Wl,-rpath,$ORIGIN/../../dooms_amd", "-Wl,-rpath,$ORIGIN/../../oracle", "-o", TEST_BIN + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on the host test ({r.returncode}):\n{r.stdout}{r.stderr}")
+    os.replace(TEST_BIN + ".tmp", TEST_BIN)
+    return TEST_BIN
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

@@ -1,0 +1,262 @@
+// C++ host layer above the C ABI (include/mx_attn.h): the attention step of dooms.cpp's fixed-model decoders, with the
+// reference's call shapes, so that a decoder written against the reference's interface calls this instead.
+//
+//   reference (dooms.cpp 0.6.1)                                               here
+//   MetalLlamaDecoder::Impl::attention(enc, cache_off, M, p0, fused_rope)      LlamaAttention::attention(layer, q, out, M, p0)
+//     (src/backend/metal/metal_llama_decoder.mm:238-307)
+//   MetalWhisperDecoder::Impl::self_attention(cache_off, p)                    WhisperAttention::self_attention(layer, q, out, p)
+//   MetalWhisperDecoder::Impl::self_attention_prompt(cache_off, p0, M)         WhisperAttention::self_attention_prompt(...)
+//   MetalWhisperDecoder::Impl::cross_attention(cache_off, M)                   WhisperAttention::cross_attention(layer, q, out, M)
+//     (src/backend/metal/metal_whisper_decoder.mm:167-225)
+//   Status / Code (src/core/status.h:13-81)                                     Status / Code below (same numbering)
+//
+// The caches keep the reference's layout: per layer [n_ctx][n_head_kv * head_dim] f16, layer l at l * n_ctx rows
+// (metal_llama_decoder.mm:657-667; the Whisper self cache [n_text_ctx][n_state] and cross cache [n_audio_ctx][n_state],
+// metal_whisper_decoder.mm:460-461). The caller owns them. Rotary embedding is the caller's (the reference's
+// rope_store, llama_kernels.h:520-545, with fused_rope for decode): q arrives rotated, and append() copies rotated
+// keys/values into the cache rows. Like the reference's decoders these objects are not thread-safe; all work is
+// ordered on the stream given at create, and nothing synchronizes with the host except create/destroy.
+//
+// Header-only: include it, link libmx_attn.so and the HIP runtime.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <utility>
+
+#include "mx_attn.h"
+
+namespace dooms_amd {
+
+enum class Code : int32_t {  // the numbering of dooms::Code / dooms_code for the codes this layer can return
+    Ok = MX_ATTN_OK,
+    InvalidArgument = MX_ATTN_INVALID_ARGUMENT,
+    Unsupported = MX_ATTN_UNSUPPORTED,
+    ResourceExhausted = MX_ATTN_RESOURCE_EXHAUSTED,
+    Internal = MX_ATTN_INTERNAL,
+};
+
+struct Status {
+    Code code = Code::Ok;
+    std::string message;
+    bool is_ok() const { return code == Code::Ok; }
+    static Status from(int32_t rc) { return rc == MX_ATTN_OK ? Status{} : Status{Code(rc), mx_attn_last_error()}; }
+    static Status hip(hipError_t e, const char * what) {
+        return e == hipSuccess ? Status{} : Status{Code::Internal, std::string(what) + ": " + hipGetErrorString(e)};
+    }
+};
+
+// Decode workspace owned by a decoder (allocated at create, as the reference allocates split_part,
+// metal_llama_decoder.mm:672-677).
+class Workspace {
+public:
+    Workspace() = default;
+    Workspace(const Workspace &) = delete;
+    Workspace & operator=(const Workspace &) = delete;
+    ~Workspace() {
+        if (ptr_) (void)hipFree(ptr_);
+    }
+    Status reserve(size_t bytes, hipStream_t stream) {
+        if (bytes <= bytes_) return {};
+        if (ptr_) (void)hipFree(ptr_);
+        ptr_ = nullptr;
+        bytes_ = 0;
+        if (Status st = Status::hip(hipMalloc(&ptr_, bytes), "workspace allocation"); !st.is_ok()) {
+            ptr_ = nullptr;
+            return Status{Code::ResourceExhausted, st.message};
+        }
+        bytes_ = bytes;
+        return Status::from(mx_attn_decode_workspace_init(ptr_, bytes_, stream));
+    }
+    void * data() const { return ptr_; }
+    size_t size() const { return bytes_; }
+
+private:
+    void * ptr_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+// ---- llama / Qwen2 ----
+
+struct LlamaAttentionConfig {  // the attention fields of LlamaDecoderConfig (metal_llama_decoder.h:20-39)
+    int32_t n_layer = 0;
+    int32_t n_ctx = 0;       // positions per layer cache
+    int32_t n_head = 0;
+    int32_t n_head_kv = 0;
+    int32_t head_dim = 0;    // 64 or 128
+};
+
+class LlamaAttention {
+public:
+    //   InvalidArgument  bad sizes or null caches     Unsupported  head_dim not 64/128     ResourceExhausted  workspace
+    static Status create(const LlamaAttentionConfig & c, uint16_t * k_cache, uint16_t * v_cache, hipStream_t stream,
+                         std::unique_ptr<LlamaAttention> & out) {
+        if (c.n_layer < 1 || c.n_ctx < 1 || c.n_head < 1 || c.n_head_kv < 1 || c.head_dim < 1)
+            return {Code::InvalidArgument, "n_layer, n_ctx, n_head, n_head_kv and head_dim must be >= 1"};
+        if (!k_cache || !v_cache) return {Code::InvalidArgument, "caches must not be null"};
+        if (c.n_head % c.n_head_kv) return {Code::InvalidArgument, "n_head must be a multiple of n_head_kv"};
+        if (c.head_dim != 64 && c.head_dim != 128)
+            return {Code::Unsupported, "head_dim " + std::to_string(c.head_dim) + " is not supported (64 or 128)"};
+        std::unique_ptr<LlamaAttention> a(new LlamaAttention(c, k_cache, v_cache, stream));
+        mx_attn_desc d = a->desc(1, 0, 0);
+        if (Status st = a->ws_.reserve(mx_attn_decode_workspace_bytes(&d, 1, c.n_ctx), stream); !st.is_ok()) return st;
+        out = std::move(a);
+        return {};
+    }
+
+    const LlamaAttentionConfig & config() const { return cfg_; }
+    int32_t kv_width() const { return cfg_.n_head_kv * cfg_.head_dim; }
+    int32_t q_width() const { return cfg_.n_head * cfg_.head_dim; }
+    uint16_t * k_layer(int32_t l) const { return k_ + (size_t)l * cfg_.n_ctx * kv_width(); }
+    uint16_t * v_layer(int32_t l) const { return v_ + (size_t)l * cfg_.n_ctx * kv_width(); }
+
+    // Copies M rows of (rotated) keys and values, rows k_stride / v_stride halves apart, into layer l's cache at
+    // positions p0 .. p0 + M - 1 (the cache write of rope_store).   ResourceExhausted  past n_ctx
+    Status append(int32_t layer, const uint16_t * k, int64_t k_stride, const uint16_t * v, int64_t v_stride, int32_t M,
+                  int32_t p0) {
+        if (layer < 0 || layer >= cfg_.n_layer || M < 1 || p0 < 0 || !k || !v)
+            return {Code::InvalidArgument, "append: bad layer, rows, position or pointer"};
+        if ((int64_t)p0 + M > cfg_.n_ctx) return {Code::ResourceExhausted, "append: the context would overflow"};
+        const size_t w = (size_t)kv_width() * 2;
+        if (Status st = Status::hip(hipMemcpy2DAsync(k_layer(layer) + (size_t)p0 * kv_width(), w, k, (size_t)k_stride * 2, w, M,
+                                                     hipMemcpyDeviceToDevice, stream_), "append k");
+            !st.is_ok())
+            return st;
+        return Status::hip(hipMemcpy2DAsync(v_layer(layer) + (size_t)p0 * kv_width(), w, v, (size_t)v_stride * 2, w, M,
+                                            hipMemcpyDeviceToDevice, stream_), "append v");
+    }
+
+    // Attention of M query rows at positions p0 .. p0 + M - 1 of layer l over cache rows 0 .. p0 + M - 1 (already
+    // appended): one decode row (M == 1) through the split-KV decode path, a prompt chunk through flash prefill. q rows
+    // are q_stride halves apart, out rows out_stride.
+    Status attention(int32_t layer, const uint16_t * q, int64_t q_stride, uint16_t * out, int64_t out_stride, int32_t M,
+                     int32_t p0) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (M < 1 || p0 < 0) return {Code::InvalidArgument, "need M >= 1 rows at a position p0 >= 0"};
+        if ((int64_t)p0 + M > cfg_.n_ctx) return {Code::ResourceExhausted, "the context would overflow"};
+        const uint16_t * k = k_layer(layer);
+        const uint16_t * v = v_layer(layer);
+        if (M == 1) {
+            mx_attn_desc d = desc(1, q_stride, out_stride);
+            d.causal = 0;
+            const int32_t n = p0 + 1;
+            return Status::from(mx_attn_decode(&d, 1, &n, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        }
+        mx_attn_desc d = desc(M, q_stride, out_stride);
+        d.p0 = p0;
+        d.causal = 1;
+        return Status::from(mx_attn_prefill(&d, q, k, v, out, nullptr, stream_));
+    }
+
+private:
+    LlamaAttention(const LlamaAttentionConfig & c, uint16_t * k, uint16_t * v, hipStream_t s) : cfg_(c), k_(k), v_(v), stream_(s) {}
+    mx_attn_desc desc(int32_t n_q, int64_t q_stride, int64_t out_stride) const {
+        mx_attn_desc d{};
+        d.n_head = cfg_.n_head;
+        d.n_head_kv = cfg_.n_head_kv;
+        d.head_dim = cfg_.head_dim;
+        d.n_q = n_q;
+        d.q_stride = q_stride ? q_stride : q_width();
+        d.kv_stride = kv_width();
+        d.out_stride = out_stride ? out_stride : q_width();
+        d.scale = 1.0f / std::sqrt((float)cfg_.head_dim);
+        return d;
+    }
+    LlamaAttentionConfig cfg_;
+    uint16_t * k_;
+    uint16_t * v_;
+    hipStream_t stream_;
+    Workspace ws_;
+};
+
+// ---- Whisper (MHA: n_head_kv = n_head, head_dim = n_state / n_head) ----
+
+struct WhisperAttentionConfig {  // the attention fields of WhisperDecoderConfig (whisper_text_decoder.h:16-30)
+    int32_t n_layer = 0;
+    int32_t n_state = 0;
+    int32_t n_head = 0;
+    int32_t n_text_ctx = 0;   // self-attention cache positions (448)
+    int32_t n_audio_ctx = 0;  // cross-attention positions (1500)
+    int32_t max_rows = 8;     // query rows per call: prompt rows, or beams for cross-attention
+};
+
+class WhisperAttention {
+public:
+    static Status create(const WhisperAttentionConfig & c, uint16_t * self_k, uint16_t * self_v, uint16_t * cross_k,
+                         uint16_t * cross_v, hipStream_t stream, std::unique_ptr<WhisperAttention> & out) {
+        if (c.n_layer < 1 || c.n_state < 1 || c.n_head < 1 || c.n_text_ctx < 1 || c.n_audio_ctx < 1 || c.max_rows < 1)
+            return {Code::InvalidArgument, "sizes must be >= 1"};
+        if (c.n_state % c.n_head) return {Code::InvalidArgument, "n_state must be a multiple of n_head"};
+        const int32_t hd = c.n_state / c.n_head;
+        if (hd != 64 && hd != 128) return {Code::Unsupported, "head_dim " + std::to_string(hd) + " is not supported (64 or 128)"};
+        if (!self_k || !self_v || !cross_k || !cross_v) return {Code::InvalidArgument, "caches must not be null"};
+        std::unique_ptr<WhisperAttention> a(new WhisperAttention(c, self_k, self_v, cross_k, cross_v, stream));
+        size_t ws = 0;
+        for (int32_t causal = 0; causal < 2; causal++) {
+            mx_attn_desc d = a->desc(c.max_rows, causal);
+            const size_t self_ws = mx_attn_decode_workspace_bytes(&d, 1, c.n_text_ctx);
+            const size_t cross_ws = mx_attn_decode_workspace_bytes(&d, 1, c.n_audio_ctx);
+            ws = std::max(ws, std::max(self_ws, cross_ws));
+        }
+        if (Status st = a->ws_.reserve(ws, stream); !st.is_ok()) return st;
+        out = std::move(a);
+        return {};
+    }
+
+    int32_t head_dim() const { return cfg_.n_state / cfg_.n_head; }
+    uint16_t * self_k(int32_t l) const { return sk_ + (size_t)l * cfg_.n_text_ctx * cfg_.n_state; }
+    uint16_t * self_v(int32_t l) const { return sv_ + (size_t)l * cfg_.n_text_ctx * cfg_.n_state; }
+    uint16_t * cross_k(int32_t l) const { return ck_ + (size_t)l * cfg_.n_audio_ctx * cfg_.n_state; }
+    uint16_t * cross_v(int32_t l) const { return cv_ + (size_t)l * cfg_.n_audio_ctx * cfg_.n_state; }
+
+    // One new token at position p (its key/value already in the self cache): attends positions 0 .. p.
+    Status self_attention(int32_t layer, const uint16_t * q, uint16_t * out, int32_t p) {
+        if (p < 0 || p >= cfg_.n_text_ctx) return {Code::ResourceExhausted, "text position out of the context"};
+        return run(layer, q, out, 1, p + 1, 0, self_k(layer), self_v(layer));
+    }
+    // M prompt tokens at positions p0 .. p0 + M - 1 (cached): row t attends positions 0 .. p0 + t.
+    Status self_attention_prompt(int32_t layer, const uint16_t * q, uint16_t * out, int32_t p0, int32_t M) {
+        if (p0 < 0 || M < 1 || (int64_t)p0 + M > cfg_.n_text_ctx) return {Code::ResourceExhausted, "prompt out of the context"};
+        return run(layer, q, out, M, p0 + M, 1, self_k(layer), self_v(layer));
+    }
+    // M query rows (greedy 1, or one per beam) over the layer's n_audio_ctx encoder keys/values.
+    Status cross_attention(int32_t layer, const uint16_t * q, uint16_t * out, int32_t M) {
+        return run(layer, q, out, M, cfg_.n_audio_ctx, 0, cross_k(layer), cross_v(layer));
+    }
+
+private:
+    WhisperAttention(const WhisperAttentionConfig & c, uint16_t * sk, uint16_t * sv, uint16_t * ck, uint16_t * cv, hipStream_t s)
+        : cfg_(c), sk_(sk), sv_(sv), ck_(ck), cv_(cv), stream_(s) {}
+    mx_attn_desc desc(int32_t n_q, int32_t causal) const {
+        mx_attn_desc d{};
+        d.n_head = cfg_.n_head;
+        d.n_head_kv = cfg_.n_head;
+        d.head_dim = head_dim();
+        d.n_q = n_q;
+        d.causal = causal;
+        d.q_stride = d.kv_stride = d.out_stride = cfg_.n_state;
+        d.scale = 1.0f / std::sqrt((float)head_dim());
+        return d;
+    }
+    Status run(int32_t layer, const uint16_t * q, uint16_t * out, int32_t M, int32_t n_keys, int32_t causal, const uint16_t * k,
+               const uint16_t * v) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (M < 1 || M > cfg_.max_rows) return {Code::InvalidArgument, "rows must be in [1, max_rows]"};
+        mx_attn_desc d = desc(M, causal);
+        return Status::from(mx_attn_decode(&d, 1, &n_keys, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+    }
+    WhisperAttentionConfig cfg_;
+    uint16_t * sk_;
+    uint16_t * sv_;
+    uint16_t * ck_;
+    uint16_t * cv_;
+    hipStream_t stream_;
+    Workspace ws_;
+};
+
+}  // namespace dooms_amd

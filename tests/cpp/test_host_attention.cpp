@@ -1,0 +1,207 @@
+// C++ host-layer test (dooms_amd/host/attention_host.hpp) in the reference's style: a dependency-free TEST/EXPECT
+// harness whose exit code is the number of failed tests (tests/unit/check.h:1-71 in dooms.cpp 0.6.1), and a decoder's
+// call sequence checked against an independent double-precision reference (the reference's own approach,
+// tests/unit/test_metal_llama_decoder.cpp:110-192), here the CPU oracle (oracle/oracle.c).
+//
+// Llama: a 45-token prompt in chunks of 20 through the flash path, then decode steps one at a time
+// (test_metal_llama_decoder.cpp:497-532 evaluates the same prompt in chunks of 20), two layers, GQA 4/2, head_dim 64.
+// Whisper: prompt rows, single-token self-attention steps, greedy and 5-beam cross-attention over 150 encoder rows.
+// Error paths: unsupported head_dim, context overflow, bad layer.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "attention_host.hpp"
+
+extern "C" int oracle_attention_f64(int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t n_q, int32_t p0, int32_t n_kv,
+                                    int32_t causal, double scale, const uint16_t * q, int64_t q_stride, const uint16_t * k,
+                                    const uint16_t * v, int64_t kv_stride, double * out, int64_t out_stride, double * lse);
+
+namespace {
+
+int g_failed = 0, g_checks = 0;
+std::vector<std::pair<const char *, std::function<void()>>> & registry() {
+    static std::vector<std::pair<const char *, std::function<void()>>> r;
+    return r;
+}
+struct Reg {
+    Reg(const char * n, std::function<void()> f) { registry().emplace_back(n, std::move(f)); }
+};
+#define TEST(name) static void name(); static Reg reg_##name(#name, name); static void name()
+#define EXPECT(cond) do { g_checks++; if (!(cond)) { g_failed++; std::fprintf(stderr, "  FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond); } } while (0)
+
+#define HIP_OK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { std::fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); std::exit(100); } } while (0)
+
+uint16_t to_half(float f) {
+    const _Float16 h = (_Float16)f;
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+double from_half(uint16_t b) {
+    _Float16 h;
+    std::memcpy(&h, &b, 2);
+    return (double)(float)h;
+}
+
+// splitmix64 and Box-Muller: portable seeded normals
+struct Rng {
+    uint64_t s;
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return ((next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+    float normal() { return (float)(std::sqrt(-2.0 * std::log(uniform())) * std::cos(6.283185307179586 * uniform())); }
+};
+std::vector<uint16_t> random_half(Rng & r, size_t n) {
+    std::vector<uint16_t> v(n);
+    for (auto & x : v) x = to_half(r.normal());
+    return v;
+}
+
+struct Dev {
+    uint16_t * p = nullptr;
+    explicit Dev(size_t n) { HIP_OK(hipMalloc(&p, n * 2)); }
+    ~Dev() { (void)hipFree(p); }
+};
+
+// |got - ref| <= 2e-3 + 1e-2 |ref| for every element
+bool close(const std::vector<uint16_t> & got, const std::vector<double> & ref, const char * what) {
+    double worst = 0;
+    size_t bad = 0;
+    for (size_t i = 0; i < ref.size(); i++) {
+        const double e = std::fabs(from_half(got[i]) - ref[i]);
+        worst = std::max(worst, e);
+        if (!(e <= 2e-3 + 1e-2 * std::fabs(ref[i]))) bad++;
+    }
+    if (bad) std::fprintf(stderr, "  %s: %zu elements out of tolerance, max abs err %.3e\n", what, bad, worst);
+    return bad == 0;
+}
+
+}  // namespace
+
+TEST(llama_prompt_in_chunks_then_decode_steps) {
+    using namespace dooms_amd;
+    const int n_layer = 2, n_ctx = 96, nh = 4, nkv = 2, hd = 64, qw = nh * hd, kw = nkv * hd;
+    Dev kc((size_t)n_layer * n_ctx * kw), vc((size_t)n_layer * n_ctx * kw);
+    std::unique_ptr<LlamaAttention> attn;
+    Status st = LlamaAttention::create({n_layer, n_ctx, nh, nkv, hd}, kc.p, vc.p, nullptr, attn);
+    EXPECT(st.is_ok());
+    if (!st.is_ok()) return;
+    Rng rng{7};
+    const int prompt = 45, steps = 12;
+    // per layer: all rows' rotated q, k, v (host copies for the reference)
+    std::vector<std::vector<uint16_t>> Q(n_layer), K(n_layer), V(n_layer);
+    for (int l = 0; l < n_layer; l++) {
+        Q[l] = random_half(rng, (size_t)(prompt + steps) * qw);
+        K[l] = random_half(rng, (size_t)(prompt + steps) * kw);
+        V[l] = random_half(rng, (size_t)(prompt + steps) * kw);
+    }
+    Dev dq((size_t)(prompt + steps) * qw), dk((size_t)(prompt + steps) * kw), dv((size_t)(prompt + steps) * kw),
+        dout((size_t)(prompt + steps) * qw);
+    auto run_rows = [&](int l, int p0, int M) -> bool {
+        HIP_OK(hipMemcpy(dq.p, Q[l].data() + (size_t)p0 * qw, (size_t)M * qw * 2, hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(dk.p, K[l].data() + (size_t)p0 * kw, (size_t)M * kw * 2, hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(dv.p, V[l].data() + (size_t)p0 * kw, (size_t)M * kw * 2, hipMemcpyHostToDevice));
+        Status a = attn->append(l, dk.p, kw, dv.p, kw, M, p0);
+        Status b = attn->attention(l, dq.p, qw, dout.p, qw, M, p0);
+        HIP_OK(hipDeviceSynchronize());
+        if (!a.is_ok() || !b.is_ok()) {
+            std::fprintf(stderr, "  %s %s\n", a.message.c_str(), b.message.c_str());
+            return false;
+        }
+        std::vector<uint16_t> got((size_t)M * qw);
+        HIP_OK(hipMemcpy(got.data(), dout.p, got.size() * 2, hipMemcpyDeviceToHost));
+        std::vector<double> ref((size_t)M * qw);
+        oracle_attention_f64(nh, nkv, hd, M, p0, p0 + M, 1, 1.0 / std::sqrt((double)hd), Q[l].data() + (size_t)p0 * qw, qw,
+                             K[l].data(), V[l].data(), kw, ref.data(), qw, nullptr);
+        return close(got, ref, (std::string("layer ") + std::to_string(l) + " rows at " + std::to_string(p0)).c_str());
+    };
+    for (int p0 = 0; p0 < prompt; p0 += 20)
+        for (int l = 0; l < n_layer; l++) EXPECT(run_rows(l, p0, std::min(20, prompt - p0)));
+    for (int p = prompt; p < prompt + steps; p++)
+        for (int l = 0; l < n_layer; l++) EXPECT(run_rows(l, p, 1));
+}
+
+TEST(llama_errors) {
+    using namespace dooms_amd;
+    Dev kc(1024), vc(1024);
+    std::unique_ptr<LlamaAttention> attn;
+    EXPECT(LlamaAttention::create({1, 4, 4, 2, 80}, kc.p, vc.p, nullptr, attn).code == Code::Unsupported);
+    EXPECT(LlamaAttention::create({1, 4, 4, 3, 64}, kc.p, vc.p, nullptr, attn).code == Code::InvalidArgument);
+    EXPECT(LlamaAttention::create({1, 4, 4, 2, 64}, nullptr, vc.p, nullptr, attn).code == Code::InvalidArgument);
+    EXPECT(LlamaAttention::create({1, 4, 4, 2, 64}, kc.p, vc.p, nullptr, attn).is_ok());
+    if (!attn) return;
+    EXPECT(attn->attention(1, kc.p, 0, vc.p, 0, 1, 0).code == Code::InvalidArgument);   // no layer 1
+    EXPECT(attn->attention(0, kc.p, 0, vc.p, 0, 2, 3).code == Code::ResourceExhausted);  // positions 3, 4 of 4
+    EXPECT(attn->append(0, kc.p, 128, vc.p, 128, 5, 0).code == Code::ResourceExhausted);
+}
+
+TEST(whisper_prompt_steps_and_cross_attention) {
+    using namespace dooms_amd;
+    const int n_state = 256, nh = 4, hd = 64, n_text = 32, n_audio = 150;
+    Dev sk((size_t)n_text * n_state), sv((size_t)n_text * n_state), ck((size_t)n_audio * n_state), cv((size_t)n_audio * n_state);
+    std::unique_ptr<WhisperAttention> w;
+    Status st = WhisperAttention::create({1, n_state, nh, n_text, n_audio, 8}, sk.p, sv.p, ck.p, cv.p, nullptr, w);
+    EXPECT(st.is_ok());
+    if (!st.is_ok()) return;
+    Rng rng{11};
+    const std::vector<uint16_t> SK = random_half(rng, (size_t)n_text * n_state), SV = random_half(rng, (size_t)n_text * n_state);
+    const std::vector<uint16_t> CK = random_half(rng, (size_t)n_audio * n_state), CV = random_half(rng, (size_t)n_audio * n_state);
+    const std::vector<uint16_t> Qs = random_half(rng, (size_t)n_text * n_state);
+    HIP_OK(hipMemcpy(sk.p, SK.data(), SK.size() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(sv.p, SV.data(), SV.size() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(ck.p, CK.data(), CK.size() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(cv.p, CV.data(), CV.size() * 2, hipMemcpyHostToDevice));
+    Dev dq(8 * n_state), dout(8 * n_state);
+    const double scale = 1.0 / 8.0;
+    auto check = [&](const uint16_t * qhost, int M, const std::vector<uint16_t> & Kh, const std::vector<uint16_t> & Vh, int n_kv,
+                     int p0, int causal, const char * what, const std::function<Status()> & call) {
+        HIP_OK(hipMemcpy(dq.p, qhost, (size_t)M * n_state * 2, hipMemcpyHostToDevice));
+        Status s = call();
+        HIP_OK(hipDeviceSynchronize());
+        EXPECT(s.is_ok());
+        std::vector<uint16_t> got((size_t)M * n_state);
+        HIP_OK(hipMemcpy(got.data(), dout.p, got.size() * 2, hipMemcpyDeviceToHost));
+        std::vector<double> ref((size_t)M * n_state);
+        oracle_attention_f64(nh, nh, hd, M, p0, n_kv, causal, scale, qhost, n_state, Kh.data(), Vh.data(), n_state, ref.data(),
+                             n_state, nullptr);
+        EXPECT(close(got, ref, what));
+    };
+    // prompt rows 0..4, then single steps at 5..9
+    check(Qs.data(), 5, SK, SV, 5, 0, 1, "self prompt", [&] { return w->self_attention_prompt(0, dq.p, dout.p, 0, 5); });
+    for (int p = 5; p < 10; p++)
+        check(Qs.data() + (size_t)p * n_state, 1, SK, SV, p + 1, p, 1, "self step", [&] { return w->self_attention(0, dq.p, dout.p, p); });
+    check(Qs.data(), 1, CK, CV, n_audio, 0, 0, "cross greedy", [&] { return w->cross_attention(0, dq.p, dout.p, 1); });
+    check(Qs.data(), 5, CK, CV, n_audio, 0, 0, "cross beam 5", [&] { return w->cross_attention(0, dq.p, dout.p, 5); });
+    EXPECT(w->self_attention(0, dq.p, dout.p, n_text).code == Code::ResourceExhausted);
+    EXPECT(w->cross_attention(0, dq.p, dout.p, 9).code == Code::InvalidArgument);  // more rows than max_rows
+    std::unique_ptr<WhisperAttention> w80;
+    EXPECT(WhisperAttention::create({1, 320, 4, 8, 8, 1}, sk.p, sv.p, ck.p, cv.p, nullptr, w80).code == Code::Unsupported);
+}
+
+int main() {
+    int dev_count = 0;
+    if (hipGetDeviceCount(&dev_count) != hipSuccess || dev_count < 1) {
+        std::fprintf(stderr, "no GPU\n");
+        return 125;
+    }
+    for (auto & [name, fn] : registry()) {
+        const int before = g_failed;
+        std::fprintf(stderr, "%s\n", name);
+        fn();
+        std::fprintf(stderr, "  %s\n", g_failed == before ? "ok" : "FAILED");
+    }
+    std::fprintf(stderr, "%d checks, %d failed\n", g_checks, g_failed);
+    return g_failed;
+}
