@@ -20,8 +20,12 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
               RESOURCE_EXHAUSTED: "RESOURCE_EXHAUSTED", INTERNAL: "INTERNAL"}
 
 # Every symbol include/mx_attn.h declares.
-EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_decode",
+EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_decode", "mx_attn_decode_rope",
            "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init")
+
+ROPE_NORMAL = 0  # adjacent pairs (2i, 2i + 1): llama
+ROPE_NEOX = 1    # split halves (i, i + head_dim / 2): qwen2
+ROPE_NONE = 2    # no rotation: Whisper
 
 
 class MxAttnDesc(ctypes.Structure):
@@ -32,6 +36,11 @@ class MxAttnDesc(ctypes.Structure):
         ("reserved", ctypes.c_int32), ("q_stride", ctypes.c_int64), ("kv_stride", ctypes.c_int64),
         ("out_stride", ctypes.c_int64), ("scale", ctypes.c_float),
     ]
+
+
+class MxAttnRope(ctypes.Structure):
+    """mx_attn_rope (include/mx_attn.h)."""
+    _fields_ = [("mode", ctypes.c_int32), ("base", ctypes.c_float)]
 
 
 class MxAttnError(RuntimeError):
@@ -61,6 +70,10 @@ def lib() -> ctypes.CDLL:
         L.mx_attn_decode.restype = ctypes.c_int32
         L.mx_attn_decode.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), P,
                                      ctypes.POINTER(P), ctypes.POINTER(P), P, P, P, ctypes.c_size_t, P]
+        L.mx_attn_decode_rope.restype = ctypes.c_int32
+        L.mx_attn_decode_rope.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.POINTER(MxAttnRope), ctypes.c_int32,
+                                          ctypes.POINTER(ctypes.c_int32), P, ctypes.POINTER(P), ctypes.POINTER(P), P,
+                                          P, P, ctypes.c_size_t, P]
         L.mx_attn_decode_workspace_bytes.restype = ctypes.c_size_t
         L.mx_attn_decode_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.c_int32]
         L.mx_attn_decode_workspace_init.restype = ctypes.c_int32
@@ -99,6 +112,18 @@ def decode_raw(desc: MxAttnDesc, kv_len, q: int, k_ptrs, v_ptrs, out: int, lse: 
     vp = (ctypes.c_void_p * n)(*v_ptrs)
     return lib().mx_attn_decode(ctypes.byref(desc), n, lens, q, kp, vp, out, lse or None, ws or None, ws_bytes,
                                 stream or None)
+
+
+def decode_rope_raw(desc: MxAttnDesc, mode: int, base: float, kv_len, qkv: int, k_ptrs, v_ptrs, out: int, lse: int,
+                    ws: int, ws_bytes: int, stream: int) -> int:
+    """mx_attn_decode_rope on raw device addresses; returns the code."""
+    n = len(kv_len)
+    lens = (ctypes.c_int32 * n)(*kv_len)
+    kp = (ctypes.c_void_p * n)(*k_ptrs)
+    vp = (ctypes.c_void_p * n)(*v_ptrs)
+    rope = MxAttnRope(mode=mode, base=base)
+    return lib().mx_attn_decode_rope(ctypes.byref(desc), ctypes.byref(rope), n, lens, qkv, kp, vp, out, lse or None,
+                                     ws or None, ws_bytes, stream or None)
 
 
 def decode_workspace_init(ws: int, ws_bytes: int, stream: int) -> int:

@@ -14,11 +14,11 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+def _rows(t: torch.Tensor, name: str, dtype=torch.float16) -> torch.Tensor:
     if not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor")
-    if t.dtype != torch.float16:
-        raise ValueError(f"{name} must be float16, got {t.dtype}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
     if t.dim() != 2 or t.stride(1) != 1:
         raise ValueError(f"{name} must be 2-D [rows][features] with unit feature stride")
     return t
@@ -86,4 +86,35 @@ def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1,
                                [t.data_ptr() for t in v_caches], out.data_ptr(),
                                lse.data_ptr() if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
                                _stream()))
+    return out, lse
+
+
+def decode_rope(qkv, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, rope_mode, rope_base=10000.0,
+                scale=None, out=None, lse=None, want_lse=False, workspace=None):
+    """mx_attn_decode_rope, the fused decode step: qkv f32 [batch][>= (n_head + 2 n_head_kv) hd] holds each sequence's
+    new token unrotated (q | k | v); the token goes to position kv_len[b] - 1 of k_caches[b] / v_caches[b] (f16,
+    written in place). Returns (out f32 [batch][n_head hd], lse or None)."""
+    batch = len(kv_len)
+    if len(k_caches) != batch or len(v_caches) != batch:
+        raise ValueError("k_caches, v_caches and kv_len must have one entry per sequence")
+    _rows(qkv, "qkv", torch.float32)
+    kv_stride = k_caches[0].stride(0)
+    for t in list(k_caches) + list(v_caches):
+        _rows(t, "cache")
+        if t.stride(0) != kv_stride:
+            raise ValueError("every cache must share one row stride")
+    if out is None:
+        out = torch.empty(batch, n_head * head_dim, dtype=torch.float32, device=qkv.device)
+    _rows(out, "out", torch.float32)
+    if want_lse and lse is None:
+        lse = torch.empty(batch, n_head, dtype=torch.float32, device=qkv.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    d = _lib.make_desc(n_head, n_head_kv, head_dim, 1, qkv.stride(0), kv_stride, out.stride(0), scale, causal=0)
+    if workspace is None:
+        workspace = new_workspace(_lib.decode_workspace_bytes(d, batch, max(kv_len)), qkv.device)
+    _lib.check(_lib.decode_rope_raw(d, rope_mode, rope_base, list(kv_len), qkv.data_ptr(),
+                                    [t.data_ptr() for t in k_caches], [t.data_ptr() for t in v_caches],
+                                    out.data_ptr(), lse.data_ptr() if lse is not None else 0, workspace.data_ptr(),
+                                    workspace.numel(), _stream()))
     return out, lse

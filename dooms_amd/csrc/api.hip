@@ -112,6 +112,104 @@ size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len
 
 }  // namespace
 
+namespace {
+
+// Shared by mx_attn_decode (rope == nullptr: half q rows and output) and mx_attn_decode_rope (f32 q|k|v rows and
+// output, the new token's key and value appended to the caches by the kernel).
+int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const void * q,
+                    const void * const * k_caches, const void * const * v_caches, void * out, float * lse,
+                    void * workspace, size_t ws_bytes, mx_attn_stream stream, const mx_attn_rope * rope) {
+    const mx_attn_desc & d = *desc;
+
+    if (!kv_len || !k_caches || !v_caches) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len, k_caches and v_caches must not be null");
+    if (!q || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must not be null");
+    if (!aligned16(q) || !aligned16(out)) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
+    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
+    int32_t max_len = 0;
+    for (int32_t b = 0; b < batch; b++) {
+        const int32_t n = kv_len[b];
+        if (n < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d: every sequence needs at least one key", b, n);
+        if (d.causal && n < d.n_q)
+            return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d < n_q = %d: causal rows must all be in the cache", b, n, d.n_q);
+        if (!k_caches[b] || !v_caches[b]) return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d are null", b);
+        if (!aligned16(k_caches[b]) || !aligned16(v_caches[b]))
+            return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d must be 16-byte aligned", b);
+        max_len = std::max(max_len, n);
+    }
+    const size_t need = decode_ws_bytes(desc, batch, max_len);
+    if (need > 0 && !workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null but %zu bytes are needed", need);
+    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+    if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    const WsLayout wl = decode_ws_layout(desc, batch, max_len);
+
+    const DecodeShape s = decode_shape(desc);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int32_t b0 = 0; b0 < batch; b0 += mx::kMaxSeqPerLaunch) {
+        const int n_seq = std::min<int32_t>(mx::kMaxSeqPerLaunch, batch - b0);
+        mx::DecodeParams p;
+        p.q = static_cast<const mx::half_t *>(q);
+        p.out = static_cast<mx::half_t *>(out);
+        p.rope = rope != nullptr;
+        p.qkv = static_cast<const float *>(q);
+        p.out32 = static_cast<float *>(out);
+        p.rope_mode = rope ? rope->mode : 2;
+        for (int i = 0; i < mx::kMaxHeadDim / 2; i++)
+            p.rope_freq[i] = (rope && rope->mode != 2 && i < d.head_dim / 2) ? std::pow(rope->base, -2.f * (float)i / (float)d.head_dim) : 0.f;
+        p.lse = lse;
+        p.counters = static_cast<uint32_t *>(workspace);
+        p.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + wl.counter_bytes);
+        p.q_stride = d.q_stride;
+        p.kv_stride = d.kv_stride;
+        p.out_stride = d.out_stride;
+        p.n_head = d.n_head;
+        p.n_head_kv = d.n_head_kv;
+        p.group = d.n_head / d.n_head_kv;
+        p.n_q = d.n_q;
+        p.causal = d.causal;
+        p.rows = s.rows;
+        p.n_rowtiles = s.n_rowtiles;
+        p.seq0 = b0;
+        p.scale_log2 = d.scale * 1.4426950408889634f;
+        // split plan (see workgroup_cap)
+        const int64_t quantum = mx::kDecodeChunkQuantum;
+        int64_t lmax = 0;
+        for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
+        auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
+        int64_t chunk = std::max<int64_t>(round_up(kMinChunk), round_up((lmax + kMaxSplits - 1) / kMaxSplits));
+        auto launch_wgs = [&](int64_t c) {
+            int64_t n = 0;
+            for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
+            return n * d.n_head_kv * s.n_rowtiles;
+        };
+        const int64_t cap = workgroup_cap();
+        if (launch_wgs(chunk) > cap) {  // smallest chunk within the cap: bisect over multiples of the quantum
+            int64_t lo = chunk / quantum, hi = round_up(lmax) / quantum;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi) / 2;
+                if (launch_wgs(mid * quantum) > cap) lo = mid + 1;
+                else hi = mid;
+            }
+            chunk = lo * quantum;
+        }
+        p.chunk = (int32_t)std::min<int64_t>(chunk, INT32_MAX / 2);
+        p.max_split = 1;
+        for (int i = 0; i < n_seq; i++) {
+            const int32_t n = kv_len[b0 + i];
+            p.seq[i].k = static_cast<const mx::half_t *>(k_caches[b0 + i]);
+            p.seq[i].v = static_cast<const mx::half_t *>(v_caches[b0 + i]);
+            p.seq[i].len = n;
+            p.seq[i].n_split = (int32_t)((n + p.chunk - 1) / p.chunk);
+            p.max_split = std::max(p.max_split, p.seq[i].n_split);
+        }
+        for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
+        if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, st), "decode launch")) return rc;
+    }
+    return MX_ATTN_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 MX_ATTN_API int32_t mx_attn_abi_version(void) { return MX_ATTN_ABI_VERSION; }
@@ -176,88 +274,33 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
                                    const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out, float * lse,
                                    void * workspace, size_t ws_bytes, mx_attn_stream stream) {
     if (int32_t rc = check_desc(desc)) return rc;
-    const mx_attn_desc & d = *desc;
     if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
-    if (d.n_q == 0) return MX_ATTN_OK;
-    if (!kv_len || !k_caches || !v_caches) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len, k_caches and v_caches must not be null");
-    if (!q || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must not be null");
-    if (!aligned16(q) || !aligned16(out)) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
-    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
-    int32_t max_len = 0;
-    for (int32_t b = 0; b < batch; b++) {
-        const int32_t n = kv_len[b];
-        if (n < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d: every sequence needs at least one key", b, n);
-        if (d.causal && n < d.n_q)
-            return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d < n_q = %d: causal rows must all be in the cache", b, n, d.n_q);
-        if (!k_caches[b] || !v_caches[b]) return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d are null", b);
-        if (!aligned16(k_caches[b]) || !aligned16(v_caches[b]))
-            return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d must be 16-byte aligned", b);
-        max_len = std::max(max_len, n);
-    }
-    const size_t need = decode_ws_bytes(desc, batch, max_len);
-    if (need > 0 && !workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null but %zu bytes are needed", need);
-    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
-    if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
-    const WsLayout wl = decode_ws_layout(desc, batch, max_len);
+    if (desc->n_q == 0) return MX_ATTN_OK;
+    return decode_impl(desc, batch, kv_len, q, reinterpret_cast<const void * const *>(k_caches),
+                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, nullptr);
+}
 
-    const DecodeShape s = decode_shape(desc);
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    for (int32_t b0 = 0; b0 < batch; b0 += mx::kMaxSeqPerLaunch) {
-        const int n_seq = std::min<int32_t>(mx::kMaxSeqPerLaunch, batch - b0);
-        mx::DecodeParams p;
-        p.q = reinterpret_cast<const mx::half_t *>(q);
-        p.out = reinterpret_cast<mx::half_t *>(out);
-        p.lse = lse;
-        p.counters = static_cast<uint32_t *>(workspace);
-        p.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + wl.counter_bytes);
-        p.q_stride = d.q_stride;
-        p.kv_stride = d.kv_stride;
-        p.out_stride = d.out_stride;
-        p.n_head = d.n_head;
-        p.n_head_kv = d.n_head_kv;
-        p.group = d.n_head / d.n_head_kv;
-        p.n_q = d.n_q;
-        p.causal = d.causal;
-        p.rows = s.rows;
-        p.n_rowtiles = s.n_rowtiles;
-        p.seq0 = b0;
-        p.scale_log2 = d.scale * 1.4426950408889634f;
-        // split plan (see workgroup_cap)
-        const int64_t quantum = mx::kDecodeChunkQuantum;
-        int64_t lmax = 0;
-        for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
-        auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
-        int64_t chunk = std::max<int64_t>(round_up(kMinChunk), round_up((lmax + kMaxSplits - 1) / kMaxSplits));
-        auto launch_wgs = [&](int64_t c) {
-            int64_t n = 0;
-            for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
-            return n * d.n_head_kv * s.n_rowtiles;
-        };
-        const int64_t cap = workgroup_cap();
-        if (launch_wgs(chunk) > cap) {  // smallest chunk within the cap: bisect over multiples of the quantum
-            int64_t lo = chunk / quantum, hi = round_up(lmax) / quantum;
-            while (lo < hi) {
-                const int64_t mid = (lo + hi) / 2;
-                if (launch_wgs(mid * quantum) > cap) lo = mid + 1;
-                else hi = mid;
-            }
-            chunk = lo * quantum;
-        }
-        p.chunk = (int32_t)std::min<int64_t>(chunk, INT32_MAX / 2);
-        p.max_split = 1;
-        for (int i = 0; i < n_seq; i++) {
-            const int32_t n = kv_len[b0 + i];
-            p.seq[i].k = reinterpret_cast<const mx::half_t *>(k_caches[b0 + i]);
-            p.seq[i].v = reinterpret_cast<const mx::half_t *>(v_caches[b0 + i]);
-            p.seq[i].len = n;
-            p.seq[i].n_split = (int32_t)((n + p.chunk - 1) / p.chunk);
-            p.max_split = std::max(p.max_split, p.seq[i].n_split);
-        }
-        for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
-        if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, st), "decode launch")) return rc;
-    }
-    return MX_ATTN_OK;
+MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, int32_t batch, const int32_t * kv_len,
+                                        const float * qkv, uint16_t * const * k_caches, uint16_t * const * v_caches, float * out,
+                                        float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    const mx_attn_desc & d = *desc;
+    if (!rope) return fail(MX_ATTN_INVALID_ARGUMENT, "rope is null");
+    if (rope->mode < 0 || rope->mode > 2) return fail(MX_ATTN_INVALID_ARGUMENT, "rope->mode (%d) must be 0, 1 or 2", rope->mode);
+    if (rope->mode != 2 && !(std::isfinite(rope->base) && rope->base > 0.f))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "rope->base must be finite and > 0");
+    if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
+    if (d.n_q != 1) return fail(MX_ATTN_INVALID_ARGUMENT, "n_q (%d) must be 1: one new token per sequence", d.n_q);
+    const int64_t row = (int64_t)(d.n_head + 2 * d.n_head_kv) * d.head_dim;
+    if (d.q_stride < row)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "q_stride (%lld) < (n_head + 2 n_head_kv) * head_dim (%lld)", (long long)d.q_stride, (long long)row);
+    // the same k/v cache under two sequences would be appended twice at different positions
+    for (int32_t b = 0; b < batch && k_caches && v_caches; b++)
+        for (int32_t c = 0; c < b; c++)
+            if (k_caches[b] == k_caches[c] || v_caches[b] == v_caches[c])
+                return fail(MX_ATTN_INVALID_ARGUMENT, "sequences %d and %d share a cache: each sequence appends to its own", c, b);
+    return decode_impl(desc, batch, kv_len, qkv, reinterpret_cast<const void * const *>(k_caches),
+                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, rope);
 }
 
 }  // extern "C"

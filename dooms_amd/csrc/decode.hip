@@ -62,8 +62,102 @@ struct KvBlock {
     u32x4 v[NLV];
 };
 
+// sin and cos of x in double, for |x| up to ~1e9: Cody-Waite reduction by pi/2 (pi/2 split in two doubles, fma) to
+// |r| <= pi/4, then the Taylor series of sin and cos to degree 17 / 16 (truncation below 1e-19 there). Accurate well
+// past f32, so that the rotation is fixed by the f32 angle alone; no large-argument slow path, no private memory.
+__device__ __forceinline__ void sincos_d(double x, double & s_out, double & c_out) {
+    constexpr double kTwoOverPi = 0.63661977236758134308, kPio2Hi = 1.5707963267948966, kPio2Lo = 6.123233995736766e-17;
+    const double k = __builtin_rint(x * kTwoOverPi);
+    double r = __builtin_fma(-k, kPio2Hi, x);
+    r = __builtin_fma(-k, kPio2Lo, r);
+    const double r2 = r * r;
+    double sp = 1.0 / 355687428096000.0;  // 1/17!
+    sp = __builtin_fma(sp, r2, -1.0 / 1307674368000.0);
+    sp = __builtin_fma(sp, r2, 1.0 / 6227020800.0);
+    sp = __builtin_fma(sp, r2, -1.0 / 39916800.0);
+    sp = __builtin_fma(sp, r2, 1.0 / 362880.0);
+    sp = __builtin_fma(sp, r2, -1.0 / 5040.0);
+    sp = __builtin_fma(sp, r2, 1.0 / 120.0);
+    sp = __builtin_fma(sp, r2, -1.0 / 6.0);
+    const double sn = __builtin_fma(sp * r2, r, r);
+    double cp = 1.0 / 20922789888000.0;  // 1/16!
+    cp = __builtin_fma(cp, r2, -1.0 / 87178291200.0);
+    cp = __builtin_fma(cp, r2, 1.0 / 479001600.0);
+    cp = __builtin_fma(cp, r2, -1.0 / 3628800.0);
+    cp = __builtin_fma(cp, r2, 1.0 / 40320.0);
+    cp = __builtin_fma(cp, r2, -1.0 / 720.0);
+    cp = __builtin_fma(cp, r2, 1.0 / 24.0);
+    cp = __builtin_fma(cp, r2, -0.5);
+    const double cs = __builtin_fma(cp, r2, 1.0);
+    const int q = (int)((long long)k & 3);
+    s_out = q == 0 ? sn : q == 1 ? cs : q == 2 ? -sn : -cs;
+    c_out = q == 0 ? cs : q == 1 ? -sn : q == 2 ? -cs : sn;
+}
+
+// Rotary embedding of the KS 8-element chunks of one head row that a lane holds (chunk ks covers head dims
+// 32 ks + 8 sgrp .. + 8) for position pos: the reference's rotate_pair (llama_kernels.h:513-518). Pair i turns by the
+// f32 angle theta = float(pos) * freq[i], freq[i] = base^(-2i / head_dim) in f32 (computed once on the host); the
+// rotation itself runs in double and is rounded once to f32. mode 0: adjacent pairs (2i, 2i + 1), llama.cpp's
+// "normal"; 1: split halves (i, i + head_dim / 2), "neox" (qwen2) -- the partner of chunk ks is chunk ks + KS / 2 of
+// the same lane; 2: none.
+template <int HD>
+__device__ __forceinline__ void rope_chunks(float (&x)[HD / 32][8], int sgrp, int pos, int mode, const float * freq) {
+    constexpr int KS = HD / 32;
+    if (mode == 2) return;
+    auto rot = [&](float & a, float & b, int i) {
+        const float theta = (float)pos * freq[i];
+        double sn, cs;
+        sincos_d((double)theta, sn, cs);
+        const double ra = (double)a * cs - (double)b * sn, rb = (double)a * sn + (double)b * cs;
+        a = (float)ra;
+        b = (float)rb;
+    };
+    if (mode == 0) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) rot(x[ks][e], x[ks][e + 1], (32 * ks + 8 * sgrp + e) / 2);
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) rot(x[ks][e], x[ks + KS / 2][e], 32 * ks + 8 * sgrp + e);
+    }
+}
+
+__device__ __forceinline__ void load8f(const float * src, float (&x)[8]) {
+    const float4_t a = *reinterpret_cast<const float4_t *>(src), b = *reinterpret_cast<const float4_t *>(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        x[e] = a[e];
+        x[4 + e] = b[e];
+    }
+}
+
+__device__ __forceinline__ u32x4 to_half8(const float (&x)[8]) {
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (half_t)x[e];
+    return __builtin_bit_cast(u32x4, h);
+}
+
+// Two adjacent output elements: half, or f32 for the fused step (the reference's f32 attention output).
+template <bool F32>
+__device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, float a, float b) {
+    if constexpr (F32) {
+        *reinterpret_cast<float2 *>(p.out32 + off) = make_float2(a, b);
+    } else {
+        p.out[off] = (half_t)a;
+        p.out[off + 1] = (half_t)b;
+    }
+}
+
 // HD: head_dim. RT: query rows per tile (4, 8 or 16; the MFMA tile always has 16 rows, the extra ones are zero).
-template <int HD, int RT>
+// ROPE: the fused decode step (one query row per sequence): q, k and v of the new token come unrotated, in f32, from
+// the q|k|v row; q and the new key are rotated for position kv_len - 1 and rounded to half, the new key and value are
+// used from registers for that position and written into the caches by the one workgroup whose split holds it; the
+// output is f32.
+template <int HD, int RT, bool ROPE>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) {
     using B = KvBlock<HD>;
     constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
@@ -116,7 +210,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     const int st = rr / G, sh = g * G + rr % G;
     const int lim = p.causal ? L - p.n_q + st : L - 1;  // last visible key of the row
     half8_t qb[KS];
-    {
+    if constexpr (ROPE) {  // f32 q|k|v row of the sequence's one token: rotate q for position L - 1, round to half
+        float x[KS][8] = {};
+        const float * qrow = p.qkv + seq_row0 * p.q_stride + (int64_t)sh * HD;
+        if (srow_ok) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, x[ks]);
+            rope_chunks<HD>(x, sgrp, L - 1, p.rope_mode, p.rope_freq);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(x[ks]));
+    } else {
         const half_t * qrow = p.q + (seq_row0 + st) * p.q_stride + (int64_t)sh * HD;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
@@ -131,6 +235,36 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     B cur, nxt;
     if (jb < j1) load_block(jb, cur);
 
+    // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
+    const int jb_new = (L - 1) & ~(kBlockKeys - 1);
+    const bool wave_new = ROPE && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % kDecodeWaves == wave;
+    const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
+    const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
+    u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
+    if constexpr (ROPE) {  // the new key (rotated) and value, rounded to half as the cache stores them
+        const float * row = p.qkv + seq_row0 * p.q_stride;
+        if (k_lane_new) {
+            float x[KS][8];
+            const float * kr = row + (int64_t)(p.n_head + g) * HD + 8 * sgrp;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) load8f(kr + 32 * ks, x[ks]);
+            rope_chunks<HD>(x, sgrp, L - 1, p.rope_mode, p.rope_freq);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) kn[ks] = to_half8(x[ks]);
+            if (rt == 0) {
+                half_t * kd = const_cast<half_t *>(kbase) + (int64_t)(L - 1) * p.kv_stride + 8 * sgrp;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) *reinterpret_cast<u32x4 *>(kd + 32 * ks) = kn[ks];
+            }
+        }
+        if (v_lane_new) {
+            float x[8];
+            load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, x);
+            vn = to_half8(x);
+            if (rt == 0) *reinterpret_cast<u32x4 *>(const_cast<half_t *>(vbase) + (int64_t)(L - 1) * p.kv_stride + vcol) = vn;
+        }
+    }
+
     float m_run = kNegInf, l_run = 0.f;  // per score lane (row srow); l is this lane's partial sum
     // O^T accumulators (16 head dims x 16 rows per tile): lane holds O[row srow][16 dtile + 4 sgrp + v], v = 0..3
     float4_t o[HD / 16];
@@ -144,6 +278,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     for (; jb < j1; jb += kBlockKeys * kDecodeWaves) {
         const int jn = jb + kBlockKeys * kDecodeWaves;
         if (jn < j1) load_block(jn, nxt);
+        if constexpr (ROPE) {
+            if (jb == jb_new) {  // the new key and value replace what the cache held at L - 1
+                const int mt_new = ((L - 1) % kBlockKeys) / 16, i_new = ((L - 1) % kBlockKeys) / KPL;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)  // constant register indices: a runtime one would go through memory
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++)
+                        if (k_lane_new && mt == mt_new) cur.k[mt][ks] = kn[ks];
+#pragma unroll
+                for (int i = 0; i < NLV; i++)
+                    if (v_lane_new && i == i_new) cur.v[i] = vn;
+            }
+        }
         // S^T = K Q^T, 2 tiles of 16 keys: lane holds keys 16 mt + 4 sgrp + v of row srow
         float sc[2][4];
 #pragma unroll
@@ -244,9 +391,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
         }
         if (single) {
             const int t = row / G, h = g * G + row % G;
-            half_t * op = p.out + (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d;
-            op[0] = (half_t)(a0 / tot);
-            op[1] = (half_t)(a1 / tot);
+            store_pair<ROPE>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 / tot, a1 / tot);
             if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
         } else {
             float * pe = part_tile + s * SS + (int64_t)r * (HD + 4);
@@ -310,9 +455,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
         }
         const int t = row / G, h = g * G + row % G;
         const float inv = 1.f / tot;
-        half_t * op = p.out + (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d;
-        op[0] = (half_t)(a0 * inv);
-        op[1] = (half_t)(a1 * inv);
+        store_pair<ROPE>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 * inv, a1 * inv);
         if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
     }
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -321,7 +464,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
 template <int HD, int RT>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
     const int tiles = n_seq * p.n_head_kv * p.n_rowtiles;
-    hipLaunchKernelGGL((decode_kernel<HD, RT>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
+    if (p.rope)
+        hipLaunchKernelGGL((decode_kernel<HD, RT, true>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL((decode_kernel<HD, RT, false>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -10,6 +10,7 @@ namespace mx {
 typedef _Float16 half_t;
 
 // Sequences per decode launch: their cache pointers, lengths and split counts ride in the kernel arguments.
+constexpr int kMaxHeadDim = 128;
 constexpr int kMaxSeqPerLaunch = 32;
 // Keys per split are a multiple of this (4 waves x 32-key blocks), and never fewer.
 constexpr int kDecodeChunkQuantum = 128;
@@ -35,6 +36,11 @@ struct DecodeParams {
     int32_t max_split;   // max over the launch's sequences of n_split
     int32_t seq0;        // index of the launch's first sequence in the caller's batch (query/output rows)
     float scale_log2;    // scale * log2(e): scores are kept in base-2 units
+    int32_t rope;        // 1: fused decode step: q|k|v rows in qkv (f32, q_stride floats apart), f32 output in out32
+    const float * qkv;
+    float * out32;
+    int32_t rope_mode;   // 0 adjacent pairs, 1 split halves (neox), 2 none
+    float rope_freq[kMaxHeadDim / 2];  // base^(-2i / head_dim) in f32 for rotary pair i
     DecodeSeq seq[kMaxSeqPerLaunch];
 };
 

@@ -127,6 +127,38 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
                                    const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out,
                                    float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream);
 
+/* Rotary embedding of the fused decode step: the reference's AttnParams.neox / base (llama_kernels.h:501-506). */
+typedef struct mx_attn_rope {
+    int32_t mode; /* 0: adjacent pairs (2i, 2i + 1), llama.cpp's "normal" (llama); 1: split halves (i, i + head_dim / 2),
+                     "neox" (qwen2); 2: none (positions come from a learned table, as in Whisper) */
+    float base;   /* frequency base (rope.freq_base); pair i of position pos turns by pos * base^(-2i / head_dim) */
+} mx_attn_rope;
+
+/*
+ * The fused decode step: rotary embedding of the new token's query and key, append of its key and value to the caches,
+ * and decode attention, in one launch. Replaces the reference's `attention` kernel with fused_rope = 1
+ * (llama_kernels.h:552-630, dispatched by MetalLlamaDecoder::Impl::attention at metal_llama_decoder.mm:298-306), and
+ * rope_store + attention_split + attention_combine for long caches (llama_kernels.h:521-549, 856-929;
+ * metal_llama_decoder.mm:241-271).
+ *
+ *   rope             rotary layout and base (mode 2: no rotation, the Whisper decoder's self-attention step)
+ *   kv_len           HOST array [batch]: keys of sequence b INCLUDING the new token, which goes to position kv_len[b] - 1
+ *   qkv              device, f32, [batch rows][q_stride floats]: the reference's q | k | v projection row of sequence b's
+ *                    new token, unrotated: n_head query heads, then n_head_kv key heads, then n_head_kv value heads
+ *   k_caches         HOST array [batch] of device pointers to distinct key caches, written at row kv_len[b] - 1 with the
+ *                    rotated key rounded to half (as the reference's rope_store / fused attention store it)
+ *   v_caches         the same for the values
+ *   out              device, f32, [batch rows][out_stride floats] (the reference's attention output is f32)
+ *   lse, workspace   as for mx_attn_decode
+ *
+ * desc->n_q must be 1 and desc->causal is irrelevant (one row sees every key). The query is rotated in f32 and then
+ * rounded to half for the matrix cores; positions below kv_len[b] - 1 are read from the caches as they stand.
+ */
+MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, int32_t batch,
+                                        const int32_t * kv_len, const float * qkv, uint16_t * const * k_caches,
+                                        uint16_t * const * v_caches, float * out, float * lse, void * workspace,
+                                        size_t ws_bytes, mx_attn_stream stream);
+
 /*
  * Zero-fills a decode workspace on `stream` (with a kernel, not a memset, so that a caller may capture it in a HIP
  * graph). Call it once after allocating the workspace; mx_attn_decode keeps it ready for the next call. It has no

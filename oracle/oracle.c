@@ -26,7 +26,17 @@
  *    (src/backend/ggml/ggml_backend.cpp:292-312, task = ith; task += nth). Accelerate is absent here, so plain loops stand
  *    in for cblas_sgemv. This is the CPU baseline bench.py times; it is checked against (1) within f32 error.
  *
- * Layout (both functions): q [n_q][q_stride], k/v [n_kv][kv_stride], out [n_q][out_stride], lse [n_q][n_head]; head h
+ * 3. oracle_rope_f32 — the rotary embedding of the reference's rope_store / fused attention (rotate_pair and pair_index,
+ *    src/backend/metal/llama_kernels.h:508-518): pair i of a head (adjacent (2i, 2i+1), or split halves (i, i + hd/2)
+ *    for neox) turns by theta = pos * base^(-2i / hd). As in the reference the angle is an f32 product of the f32
+ *    position and the f32 frequency powf(base, -2i / hd); the rotation itself is evaluated in double from libm's sin
+ *    and cos and rounded once to f32 (the reference rotates in f32; the two differ by a few f32 ulps). Pinned
+ *    (tests/test_oracle.py) against the reference test's own double-precision rope (Reference::rope,
+ *    tests/unit/test_metal_llama_decoder.cpp:180-189) within the f32 rounding of the angle, against pos 0 = identity,
+ *    per-pair norm preservation, the relative-position property <R(m) q, R(n) k> = <R(m - n) q, k>, and neox = adjacent
+ *    conjugated by the half/interleave permutation.
+ *
+ * Layout (attention functions): q [n_q][q_stride], k/v [n_kv][kv_stride], out [n_q][out_stride], lse [n_q][n_head]; head h
  * at column h * head_dim. Inputs are IEEE binary16 bit patterns.
  */
 #include <math.h>
@@ -179,4 +189,24 @@ int oracle_cpu_attend_f32(int32_t n_head, int32_t n_head_kv, int32_t head_dim, i
         if (r) rc = 2;
     }
     return rc;
+}
+
+/* Rotates n_vec head vectors of head_dim floats (x, contiguous, vector r at x + r * head_dim) for position pos into y.
+ * mode 0: adjacent pairs, 1: split halves (neox), 2: copy. */
+void oracle_rope_f32(int32_t mode, float base, int32_t head_dim, int32_t pos, const float * x, float * y, int64_t n_vec) {
+    const int32_t hd = head_dim;
+    for (int64_t r = 0; r < n_vec; r++) {
+        const float * a = x + r * hd;
+        float * b = y + r * hd;
+        memcpy(b, a, sizeof(float) * (size_t)hd);
+        if (mode == 2) continue;
+        for (int32_t i = 0; i < hd / 2; i++) {
+            const float freq = powf(base, -2.f * (float)i / (float)hd);
+            const float theta = (float)pos * freq;
+            const int32_t i0 = mode == 1 ? i : 2 * i, i1 = mode == 1 ? i + hd / 2 : 2 * i + 1;
+            const double c = cos((double)theta), s = sin((double)theta);
+            b[i0] = (float)((double)a[i0] * c - (double)a[i1] * s);
+            b[i1] = (float)((double)a[i0] * s + (double)a[i1] * c);
+        }
+    }
 }

@@ -31,6 +31,8 @@ def lib():
                                             P, i64, i32]
         L.oracle_f16_to_f32.restype = None
         L.oracle_f16_to_f32.argtypes = [P, P, i64]
+        L.oracle_rope_f32.restype = None
+        L.oracle_rope_f32.argtypes = [i32, ctypes.c_float, i32, i32, P, P, i64]
         _lib = L
     return _lib
 
@@ -78,3 +80,11 @@ def f16_to_f32(a):
     out = np.empty(a.shape, np.float32)
     lib().oracle_f16_to_f32(a.ctypes.data, out.ctypes.data, a.size)
     return out
+
+
+def rope_f32(x, mode, base, head_dim, pos):
+    """oracle_rope_f32 on an f32 array whose last axis holds whole heads (size a multiple of head_dim)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().oracle_rope_f32(mode, base, head_dim, pos, x.ctypes.data, y.ctypes.data, x.size // head_dim)
+    return y

@@ -122,6 +122,29 @@ def test_decode_checks():
     assert decode(desc(n_q=0), lens=(5,)) == _lib.OK
 
 
+def rope_decode(d, mode=0, base=500000.0, lens=(100,), kp=None, vp=None, qkv=A, rope=True):
+    n = len(lens)
+    L = (ctypes.c_int32 * n)(*lens)
+    K = (ctypes.c_void_p * n)(*(kp or [A + 4096 * i for i in range(n)]))
+    V = (ctypes.c_void_p * n)(*(vp or [A + 65536 + 4096 * i for i in range(n)]))
+    r = _lib.MxAttnRope(mode=mode, base=base)
+    return _lib.lib().mx_attn_decode_rope(ctypes.byref(d), ctypes.byref(r) if rope else None, n, L, qkv, K, V, A, None,
+                                          A, 1 << 30, None)
+
+
+def test_decode_rope_checks():
+    d = desc(q_stride=6144)  # (32 + 2 * 8) * 128
+    assert rope_decode(d, rope=False) == _lib.INVALID_ARGUMENT and "rope is null" in _lib.last_error()
+    assert rope_decode(d, mode=3) == _lib.INVALID_ARGUMENT and "mode" in _lib.last_error()
+    assert rope_decode(d, base=0.0) == _lib.INVALID_ARGUMENT and "base" in _lib.last_error()
+    assert rope_decode(d, base=float("nan")) == _lib.INVALID_ARGUMENT and "base" in _lib.last_error()
+    assert rope_decode(desc(q_stride=4096)) == _lib.INVALID_ARGUMENT and "q_stride" in _lib.last_error()
+    assert rope_decode(desc(q_stride=6144, n_q=2)) == _lib.INVALID_ARGUMENT and "n_q" in _lib.last_error()
+    assert rope_decode(d, lens=(5, 6), kp=[A, A]) == _lib.INVALID_ARGUMENT and "share a cache" in _lib.last_error()
+    assert rope_decode(d, lens=(5, 0)) == _lib.INVALID_ARGUMENT and "kv_len[1]" in _lib.last_error()
+    assert rope_decode(d, qkv=A + 8) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
+
+
 def test_workspace_init_checks():
     L = _lib.lib()
     assert L.mx_attn_decode_workspace_init(None, 0, None) == _lib.OK

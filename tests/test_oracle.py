@@ -179,3 +179,71 @@ def test_cpu_restatement_within_f32_error(causal):
     got4 = O.cpu_attend_f32(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), n_head, n_kv, hd, scale,
                             p0=L - n_q, causal=bool(causal), n_threads=4)
     np.testing.assert_array_equal(got, got4)
+
+
+# ---- rotary embedding (oracle_rope_f32) ----
+
+def _rope_double(x, mode, base, hd, pos):
+    """The reference test's own rope in double (tests/unit/test_metal_llama_decoder.cpp:180-189)."""
+    y = np.array(x, dtype=np.float64)
+    for i in range(hd // 2):
+        th = pos * (float(base) ** (-2.0 * i / hd))
+        i0, i1 = (i, i + hd // 2) if mode == 1 else (2 * i, 2 * i + 1)
+        a, b = y[..., i0].copy(), y[..., i1].copy()
+        y[..., i0] = a * np.cos(th) - b * np.sin(th)
+        y[..., i1] = a * np.sin(th) + b * np.cos(th)
+    return y
+
+
+@pytest.mark.parametrize("mode,base,hd", [(0, 500000.0, 128), (1, 1000000.0, 64), (0, 10000.0, 64), (1, 10000.0, 128)])
+@pytest.mark.parametrize("pos", [0, 1, 7, 513, 8191, 32767])
+def test_rope_matches_reference_double_rope(mode, base, hd, pos):
+    rng = np.random.default_rng(pos + hd)
+    x = rng.standard_normal((5, hd)).astype(np.float32)
+    got = O.rope_f32(x, mode, base, hd, pos)
+    ref = _rope_double(x, mode, base, hd, pos)
+    # the oracle's angle is an f32 product: off by at most ~1.5 f32 ulps of theta <= pos, which moves a pair of norm r
+    # by r * |d theta|; plus the final f32 rounding
+    r = np.sqrt(x.astype(np.float64) ** 2).max() * np.sqrt(2)
+    tol = r * (pos * 2.0 ** -23 * 1.5 + 1e-12) + 2e-7 * np.abs(ref).max()
+    assert np.abs(got - ref).max() <= tol
+    if pos == 0:
+        assert np.array_equal(got, x)
+
+
+def test_rope_mode2_is_identity_and_pairs_keep_their_norm():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 128)).astype(np.float32)
+    assert np.array_equal(O.rope_f32(x, 2, 10000.0, 128, 999), x)
+    for mode in (0, 1):
+        y = O.rope_f32(x, mode, 10000.0, 128, 4321).astype(np.float64)
+        xd = x.astype(np.float64)
+        if mode == 0:
+            n0, n1 = xd[:, 0::2] ** 2 + xd[:, 1::2] ** 2, y[:, 0::2] ** 2 + y[:, 1::2] ** 2
+        else:
+            n0, n1 = xd[:, :64] ** 2 + xd[:, 64:] ** 2, y[:, :64] ** 2 + y[:, 64:] ** 2
+        np.testing.assert_allclose(n1, n0, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_rope_relative_position_property(mode):
+    # <R(m) q, R(n) k> = <R(m - n) q, k>: what makes rotary embedding positional; a wrong pair, sign or frequency
+    # index between q and k breaks it
+    rng = np.random.default_rng(11)
+    q, k = rng.standard_normal((2, 64)).astype(np.float32)
+    for m, n in [(100, 37), (2000, 1999), (777, 0)]:
+        a = np.dot(O.rope_f32(q, mode, 10000.0, 64, m).astype(np.float64), O.rope_f32(k, mode, 10000.0, 64, n))
+        b = np.dot(O.rope_f32(q, mode, 10000.0, 64, m - n).astype(np.float64), k.astype(np.float64))
+        assert abs(a - b) <= 1e-4 * (1 + abs(b)) + 64 * m * 2.0 ** -23
+
+
+def test_rope_neox_is_adjacent_under_the_half_interleave_permutation():
+    rng = np.random.default_rng(5)
+    hd = 128
+    x = rng.standard_normal((3, hd)).astype(np.float32)
+    perm = np.empty(hd, dtype=np.int64)  # adjacent position 2i <- half position i, 2i+1 <- i + hd/2
+    perm[0::2] = np.arange(hd // 2)
+    perm[1::2] = np.arange(hd // 2) + hd // 2
+    a = O.rope_f32(x[:, perm], 0, 10000.0, hd, 1234)
+    b = O.rope_f32(x, 1, 10000.0, hd, 1234)[:, perm]
+    assert np.array_equal(a, b)
