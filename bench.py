@@ -92,14 +92,19 @@ def prefill_flops(M, p0, n_head, hd):
 class DecodeProblem:
     """Per-layer caches and the raw C-ABI launch of one decode attention call per layer."""
 
-    def __init__(self, torch, gen, n_head, n_kv, hd, lens, layers, n_q=1, causal=False, shared=False):
+    def __init__(self, torch, gen, n_head, n_kv, hd, lens, layers, n_q=1, causal=False, shared=False, rope=None):
         from dooms_amd import _lib
         self.torch, self._lib = torch, _lib
         self.n_head, self.n_kv, self.hd, self.lens, self.layers, self.n_q = n_head, n_kv, hd, list(lens), layers, n_q
+        self.rope = rope  # (mode, base): the fused step mx_attn_decode_rope on f32 q|k|v rows
         B = len(lens)
         dev = "cuda"
-        self.q = torch.randn(B * n_q, n_head * hd, generator=gen, device=dev).half()
-        self.out = torch.empty(B * n_q, n_head * hd, dtype=torch.float16, device=dev)
+        if rope:
+            self.q = torch.randn(B, (n_head + 2 * n_kv) * hd, generator=gen, device=dev)
+            self.out = torch.empty(B, n_head * hd, dtype=torch.float32, device=dev)
+        else:
+            self.q = torch.randn(B * n_q, n_head * hd, generator=gen, device=dev).half()
+            self.out = torch.empty(B * n_q, n_head * hd, dtype=torch.float16, device=dev)
         self.k, self.v = [], []
         for _ in range(layers):
             ks, vs = [], []
@@ -110,8 +115,8 @@ class DecodeProblem:
                 ks.append(torch.randn(L, n_kv * hd, generator=gen, device=dev).half())
                 vs.append(torch.randn(L, n_kv * hd, generator=gen, device=dev).half())
             self.k.append(ks), self.v.append(vs)
-        self.desc = _lib.make_desc(n_head, n_kv, hd, n_q, n_head * hd, n_kv * hd, n_head * hd, 1.0 / math.sqrt(hd),
-                                   causal=1 if causal else 0)
+        self.desc = _lib.make_desc(n_head, n_kv, hd, n_q, self.q.stride(0), n_kv * hd, n_head * hd,
+                                   1.0 / math.sqrt(hd), causal=1 if causal else 0)
         need = _lib.decode_workspace_bytes(self.desc, B, max(lens))
         self.ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
         _lib.check(_lib.decode_workspace_init(self.ws.data_ptr(), self.ws.numel(),
@@ -122,6 +127,12 @@ class DecodeProblem:
 
     def launch(self, layer):
         _lib = self._lib
+        if self.rope:
+            _lib.check(_lib.decode_rope_raw(self.desc, self.rope[0], self.rope[1], self.lens, self.q.data_ptr(),
+                                            self.kp[layer], self.vp[layer], self.out.data_ptr(), 0,
+                                            self.ws.data_ptr(), self.ws.numel(),
+                                            self.torch.cuda.current_stream().cuda_stream))
+            return
         _lib.check(_lib.decode_raw(self.desc, self.lens, self.q.data_ptr(), self.kp[layer], self.vp[layer],
                                    self.out.data_ptr(), 0, self.ws.data_ptr(), self.ws.numel(),
                                    self.torch.cuda.current_stream().cuda_stream))
@@ -315,6 +326,16 @@ def main():
                                      "layers_rotated": layers}
             del bp
             torch.cuda.empty_cache()
+
+        # ---- the fused step (rotary embedding + cache append + attention), cfg3 batch 1, L = 8192, 32 layers ----
+        fp = DecodeProblem(torch, gen, 32, 8, 128, [8192], layers=32, rope=(0, 500000.0))
+        ms_f, _ = time_graph(torch, fp.step, K, W)
+        extra["decode_rope_llama3_8b_b1_L8192"] = {
+            "us_per_layer": round(ms_f * 1e3 / 32, 3),
+            "GBps": round(32 * fp.bytes_per_launch() / (ms_f * 1e-3) / 1e9, 1),
+            "note": "mx_attn_decode_rope: f32 q|k|v row in, q/k rotated, new k/v written at position 8191, f32 out"}
+        del fp
+        torch.cuda.empty_cache()
 
         # ---- cfg1 Qwen2.5-0.5B decode (513 keys, 24 layers) ----
         qp = DecodeProblem(torch, gen, 14, 2, 64, [513], layers=24)

@@ -62,33 +62,27 @@ struct KvBlock {
     u32x4 v[NLV];
 };
 
-// sin and cos of x in double, for |x| up to ~1e9: Cody-Waite reduction by pi/2 (pi/2 split in two doubles, fma) to
-// |r| <= pi/4, then the Taylor series of sin and cos to degree 17 / 16 (truncation below 1e-19 there). Accurate well
-// past f32, so that the rotation is fixed by the f32 angle alone; no large-argument slow path, no private memory.
-__device__ __forceinline__ void sincos_d(double x, double & s_out, double & c_out) {
+// sin and cos of an f32 angle (|x| up to ~1e9): Cody-Waite reduction by pi/2 in double (pi/2 split in two doubles,
+// fma), so the reduced |r| <= pi/4 is exact to f32, then the Taylor series of sin and cos to degree 11 / 12 in f32
+// (truncation below 2e-9 there). Error a few f32 ulps of 1; no large-argument slow path, no private memory.
+__device__ __forceinline__ void sincos_rope(float x, float & s_out, float & c_out) {
     constexpr double kTwoOverPi = 0.63661977236758134308, kPio2Hi = 1.5707963267948966, kPio2Lo = 6.123233995736766e-17;
-    const double k = __builtin_rint(x * kTwoOverPi);
-    double r = __builtin_fma(-k, kPio2Hi, x);
-    r = __builtin_fma(-k, kPio2Lo, r);
-    const double r2 = r * r;
-    double sp = 1.0 / 355687428096000.0;  // 1/17!
-    sp = __builtin_fma(sp, r2, -1.0 / 1307674368000.0);
-    sp = __builtin_fma(sp, r2, 1.0 / 6227020800.0);
-    sp = __builtin_fma(sp, r2, -1.0 / 39916800.0);
-    sp = __builtin_fma(sp, r2, 1.0 / 362880.0);
-    sp = __builtin_fma(sp, r2, -1.0 / 5040.0);
-    sp = __builtin_fma(sp, r2, 1.0 / 120.0);
-    sp = __builtin_fma(sp, r2, -1.0 / 6.0);
-    const double sn = __builtin_fma(sp * r2, r, r);
-    double cp = 1.0 / 20922789888000.0;  // 1/16!
-    cp = __builtin_fma(cp, r2, -1.0 / 87178291200.0);
-    cp = __builtin_fma(cp, r2, 1.0 / 479001600.0);
-    cp = __builtin_fma(cp, r2, -1.0 / 3628800.0);
-    cp = __builtin_fma(cp, r2, 1.0 / 40320.0);
-    cp = __builtin_fma(cp, r2, -1.0 / 720.0);
-    cp = __builtin_fma(cp, r2, 1.0 / 24.0);
-    cp = __builtin_fma(cp, r2, -0.5);
-    const double cs = __builtin_fma(cp, r2, 1.0);
+    const double k = __builtin_rint((double)x * kTwoOverPi);
+    const float r = (float)__builtin_fma(-k, kPio2Lo, __builtin_fma(-k, kPio2Hi, (double)x));
+    const float r2 = r * r;
+    float sp = -1.f / 39916800.f;
+    sp = __builtin_fmaf(sp, r2, 1.f / 362880.f);
+    sp = __builtin_fmaf(sp, r2, -1.f / 5040.f);
+    sp = __builtin_fmaf(sp, r2, 1.f / 120.f);
+    sp = __builtin_fmaf(sp, r2, -1.f / 6.f);
+    const float sn = __builtin_fmaf(sp * r2, r, r);
+    float cp = 1.f / 479001600.f;
+    cp = __builtin_fmaf(cp, r2, -1.f / 3628800.f);
+    cp = __builtin_fmaf(cp, r2, 1.f / 40320.f);
+    cp = __builtin_fmaf(cp, r2, -1.f / 720.f);
+    cp = __builtin_fmaf(cp, r2, 1.f / 24.f);
+    cp = __builtin_fmaf(cp, r2, -0.5f);
+    const float cs = __builtin_fmaf(cp, r2, 1.f);
     const int q = (int)((long long)k & 3);
     s_out = q == 0 ? sn : q == 1 ? cs : q == 2 ? -sn : -cs;
     c_out = q == 0 ? cs : q == 1 ? -sn : q == 2 ? -cs : sn;
@@ -96,21 +90,20 @@ __device__ __forceinline__ void sincos_d(double x, double & s_out, double & c_ou
 
 // Rotary embedding of the KS 8-element chunks of one head row that a lane holds (chunk ks covers head dims
 // 32 ks + 8 sgrp .. + 8) for position pos: the reference's rotate_pair (llama_kernels.h:513-518). Pair i turns by the
-// f32 angle theta = float(pos) * freq[i], freq[i] = base^(-2i / head_dim) in f32 (computed once on the host); the
-// rotation itself runs in double and is rounded once to f32. mode 0: adjacent pairs (2i, 2i + 1), llama.cpp's
+// f32 angle theta = float(pos) * freq[i], freq[i] = base^(-2i / head_dim) in f32 (computed once on the host), and the
+// rotation in f32, as the reference's. mode 0: adjacent pairs (2i, 2i + 1), llama.cpp's
 // "normal"; 1: split halves (i, i + head_dim / 2), "neox" (qwen2) -- the partner of chunk ks is chunk ks + KS / 2 of
 // the same lane; 2: none.
 template <int HD>
-__device__ __forceinline__ void rope_chunks(float (&x)[HD / 32][8], int sgrp, int pos, int mode, const float * freq) {
+__device__ __forceinline__ void rope_chunks(float (&x)[HD / 32][8], int sgrp, int mode, const float2 * cs_tab) {
     constexpr int KS = HD / 32;
     if (mode == 2) return;
     auto rot = [&](float & a, float & b, int i) {
-        const float theta = (float)pos * freq[i];
-        double sn, cs;
-        sincos_d((double)theta, sn, cs);
-        const double ra = (double)a * cs - (double)b * sn, rb = (double)a * sn + (double)b * cs;
-        a = (float)ra;
-        b = (float)rb;
+        const float2 t = cs_tab[i];
+        const float cs = t.x, sn = t.y;
+        const float ra = a * cs - b * sn, rb = a * sn + b * cs;
+        a = ra;
+        b = rb;
     };
     if (mode == 0) {
 #pragma unroll
@@ -167,6 +160,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     __shared__ float s_m[kDecodeWaves][RT], s_l[kDecodeWaves][RT];
     __shared__ float s_o[kDecodeWaves][RT * HD];
     __shared__ int s_last;
+    __shared__ float2 s_cs[ROPE ? HD / 2 : 1];  // fused step: (cos, sin) of each rotary pair's angle
 
     const int s = blockIdx.x;
     int y = blockIdx.y;
@@ -210,16 +204,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     const int st = rr / G, sh = g * G + rr % G;
     const int lim = p.causal ? L - p.n_q + st : L - 1;  // last visible key of the row
     half8_t qb[KS];
-    if constexpr (ROPE) {  // f32 q|k|v row of the sequence's one token: rotate q for position L - 1, round to half
-        float x[KS][8] = {};
+    float xq[ROPE ? KS : 1][8] = {};  // fused step: the f32 query, rotated once the first block's loads are out
+    if constexpr (ROPE) {
         const float * qrow = p.qkv + seq_row0 * p.q_stride + (int64_t)sh * HD;
         if (srow_ok) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, x[ks]);
-            rope_chunks<HD>(x, sgrp, L - 1, p.rope_mode, p.rope_freq);
+            for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, xq[ks]);
         }
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(x[ks]));
     } else {
         const half_t * qrow = p.q + (seq_row0 + st) * p.q_stride + (int64_t)sh * HD;
 #pragma unroll
@@ -241,14 +232,28 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
     const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
     u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
-    if constexpr (ROPE) {  // the new key (rotated) and value, rounded to half as the cache stores them
+    if constexpr (ROPE) {  // the query and the new key rotated, the new key and value rounded to half as cached
         const float * row = p.qkv + seq_row0 * p.q_stride;
+        float x[KS][8], xv[8];
         if (k_lane_new) {
-            float x[KS][8];
             const float * kr = row + (int64_t)(p.n_head + g) * HD + 8 * sgrp;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(kr + 32 * ks, x[ks]);
-            rope_chunks<HD>(x, sgrp, L - 1, p.rope_mode, p.rope_freq);
+        }
+        if (v_lane_new) load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, xv);
+        if (p.rope_mode != 2) {  // the 64 (hd 128) angles of position L - 1, once per workgroup
+            if (threadIdx.x < HD / 2) {
+                float sn, cs;
+                sincos_rope((float)(L - 1) * p.rope_freq[threadIdx.x], sn, cs);
+                s_cs[threadIdx.x] = make_float2(cs, sn);
+            }
+            __syncthreads();
+        }
+        if (srow_ok) rope_chunks<HD>(xq, sgrp, p.rope_mode, s_cs);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(xq[ks]));
+        if (k_lane_new) {
+            rope_chunks<HD>(x, sgrp, p.rope_mode, s_cs);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) kn[ks] = to_half8(x[ks]);
             if (rt == 0) {
@@ -258,9 +263,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
             }
         }
         if (v_lane_new) {
-            float x[8];
-            load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, x);
-            vn = to_half8(x);
+            vn = to_half8(xv);
             if (rt == 0) *reinterpret_cast<u32x4 *>(const_cast<half_t *>(vbase) + (int64_t)(L - 1) * p.kv_stride + vcol) = vn;
         }
     }

@@ -2,7 +2,8 @@
 // reference's call shapes, so that a decoder written against the reference's interface calls this instead.
 //
 //   reference (dooms.cpp 0.6.1)                                               here
-//   MetalLlamaDecoder::Impl::attention(enc, cache_off, M, p0, fused_rope)      LlamaAttention::attention(layer, q, out, M, p0)
+//   MetalLlamaDecoder::Impl::attention(enc, cache_off, M, p0, false)          LlamaAttention::attention(layer, q, out, M, p0)
+//   MetalLlamaDecoder::Impl::attention(enc, cache_off, 1, p, true)            LlamaAttention::decode_step(layer, qkv, out, p)
 //     (src/backend/metal/metal_llama_decoder.mm:238-307)
 //   MetalWhisperDecoder::Impl::self_attention(cache_off, p)                    WhisperAttention::self_attention(layer, q, out, p)
 //   MetalWhisperDecoder::Impl::self_attention_prompt(cache_off, p0, M)         WhisperAttention::self_attention_prompt(...)
@@ -13,8 +14,8 @@
 // The caches keep the reference's layout: per layer [n_ctx][n_head_kv * head_dim] f16, layer l at l * n_ctx rows
 // (metal_llama_decoder.mm:657-667; the Whisper self cache [n_text_ctx][n_state] and cross cache [n_audio_ctx][n_state],
 // metal_whisper_decoder.mm:460-461). The caller owns them. Rotary embedding is the caller's (the reference's
-// rope_store, llama_kernels.h:520-545, with fused_rope for decode): q arrives rotated, and append() copies rotated
-// keys/values into the cache rows. Like the reference's decoders these objects are not thread-safe; all work is
+// rope_store, llama_kernels.h:520-545) for prompt chunks: q arrives rotated, and append() copies rotated keys/values
+// into the cache rows; decode_step() is the reference's fused_rope decode (rotation and cache write in the kernel). Like the reference's decoders these objects are not thread-safe; all work is
 // ordered on the stream given at create, and nothing synchronizes with the host except create/destroy.
 //
 // Header-only: include it, link libmx_attn.so and the HIP runtime.
@@ -89,6 +90,8 @@ struct LlamaAttentionConfig {  // the attention fields of LlamaDecoderConfig (me
     int32_t n_head = 0;
     int32_t n_head_kv = 0;
     int32_t head_dim = 0;    // 64 or 128
+    float rope_base = 10000.f;  // rotary frequency base (rope.freq_base)
+    bool rope_neox = false;     // rotary pairs (i, i + head_dim / 2) (qwen2) instead of (2i, 2i + 1) (llama)
 };
 
 class LlamaAttention {
@@ -151,6 +154,23 @@ public:
         d.p0 = p0;
         d.causal = 1;
         return Status::from(mx_attn_prefill(&d, q, k, v, out, nullptr, stream_));
+    }
+
+    // One decode step of layer l at position p, the reference's attention(enc, cache_off, 1, p, fused_rope = true)
+    // (metal_llama_decoder.mm:298-306): qkv is the new token's f32 q | k | v projection row, unrotated; q and k are
+    // rotated for position p, k and v are written into the layer's cache at p, and out (f32, q_width floats) gets the
+    // attention over positions 0 .. p.   ResourceExhausted  p past n_ctx
+    Status decode_step(int32_t layer, const float * qkv, float * out, int32_t p) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (p < 0) return {Code::InvalidArgument, "position must be >= 0"};
+        if (p >= cfg_.n_ctx) return {Code::ResourceExhausted, "the context would overflow"};
+        mx_attn_desc d = desc(1, q_width() + 2 * kv_width(), q_width());
+        d.causal = 0;
+        const mx_attn_rope rope{cfg_.rope_neox ? 1 : 0, cfg_.rope_base};
+        const int32_t n = p + 1;
+        uint16_t * k = k_layer(layer);
+        uint16_t * v = v_layer(layer);
+        return Status::from(mx_attn_decode_rope(&d, &rope, 1, &n, qkv, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
     }
 
 private:

@@ -30,7 +30,7 @@
  *    src/backend/metal/llama_kernels.h:508-518): pair i of a head (adjacent (2i, 2i+1), or split halves (i, i + hd/2)
  *    for neox) turns by theta = pos * base^(-2i / hd). As in the reference the angle is an f32 product of the f32
  *    position and the f32 frequency powf(base, -2i / hd); the rotation itself is evaluated in double from libm's sin
- *    and cos and rounded once to f32 (the reference rotates in f32; the two differ by a few f32 ulps). Pinned
+ *    and cos and rounded once to f32 (the reference and the GPU kernel rotate in f32: a few f32 ulps apart). Pinned
  *    (tests/test_oracle.py) against the reference test's own double-precision rope (Reference::rope,
  *    tests/unit/test_metal_llama_decoder.cpp:180-189) within the f32 rounding of the angle, against pos 0 = identity,
  *    per-pair norm preservation, the relative-position property <R(m) q, R(n) k> = <R(m - n) q, k>, and neox = adjacent

@@ -24,6 +24,8 @@ extern "C" int oracle_attention_f64(int32_t n_head, int32_t n_head_kv, int32_t h
                                     int32_t causal, double scale, const uint16_t * q, int64_t q_stride, const uint16_t * k,
                                     const uint16_t * v, int64_t kv_stride, double * out, int64_t out_stride, double * lse);
 
+extern "C" void oracle_rope_f32(int32_t mode, float base, int32_t head_dim, int32_t pos, const float * x, float * y, int64_t n_vec);
+
 namespace {
 
 int g_failed = 0, g_checks = 0;
@@ -131,6 +133,77 @@ TEST(llama_prompt_in_chunks_then_decode_steps) {
         for (int l = 0; l < n_layer; l++) EXPECT(run_rows(l, p0, std::min(20, prompt - p0)));
     for (int p = prompt; p < prompt + steps; p++)
         for (int l = 0; l < n_layer; l++) EXPECT(run_rows(l, p, 1));
+}
+
+// Qwen2-style (neox rope, base 1e6): a 37-token prompt appended rotated, then fused decode steps; each step's output and
+// the cache rows it wrote are checked against the oracle's rope and attention.
+TEST(llama_fused_rope_decode_steps) {
+    using namespace dooms_amd;
+    const int n_ctx = 64, nh = 14, nkv = 2, hd = 64, qw = nh * hd, kw = nkv * hd, rw = qw + 2 * kw;
+    const float base = 1e6f;
+    Dev kc((size_t)n_ctx * kw), vc((size_t)n_ctx * kw);
+    std::unique_ptr<LlamaAttention> attn;
+    LlamaAttentionConfig cfg{1, n_ctx, nh, nkv, hd};
+    cfg.rope_base = base;
+    cfg.rope_neox = true;
+    Status st = LlamaAttention::create(cfg, kc.p, vc.p, nullptr, attn);
+    EXPECT(st.is_ok());
+    if (!st.is_ok()) return;
+    Rng rng{23};
+    const int prompt = 37, steps = 6;
+    std::vector<uint16_t> K((size_t)n_ctx * kw), V((size_t)n_ctx * kw);  // host image of the cache
+    for (int p = 0; p < prompt; p++) {
+        std::vector<float> k(kw), kr(kw);
+        for (auto & x : k) x = rng.normal();
+        oracle_rope_f32(1, base, hd, p, k.data(), kr.data(), nkv);
+        for (int i = 0; i < kw; i++) {
+            K[(size_t)p * kw + i] = to_half(kr[i]);
+            V[(size_t)p * kw + i] = to_half(rng.normal());
+        }
+    }
+    HIP_OK(hipMemcpy(kc.p, K.data(), (size_t)prompt * kw * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(vc.p, V.data(), (size_t)prompt * kw * 2, hipMemcpyHostToDevice));
+    float *dqkv = nullptr, *dout = nullptr;
+    HIP_OK(hipMalloc(&dqkv, rw * 4));
+    HIP_OK(hipMalloc(&dout, qw * 4));
+    for (int p = prompt; p < prompt + steps; p++) {
+        std::vector<float> row(rw);
+        for (auto & x : row) x = rng.normal();
+        HIP_OK(hipMemcpy(dqkv, row.data(), rw * 4, hipMemcpyHostToDevice));
+        Status s = attn->decode_step(0, dqkv, dout, p);
+        HIP_OK(hipDeviceSynchronize());
+        EXPECT(s.is_ok());
+        std::vector<float> qr(qw), kr(kw);
+        oracle_rope_f32(1, base, hd, p, row.data(), qr.data(), nh);
+        oracle_rope_f32(1, base, hd, p, row.data() + qw, kr.data(), nkv);
+        std::vector<uint16_t> gk(kw), gv(kw);
+        HIP_OK(hipMemcpy(gk.data(), kc.p + (size_t)p * kw, kw * 2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(gv.data(), vc.p + (size_t)p * kw, kw * 2, hipMemcpyDeviceToHost));
+        int worst_k = 0;
+        bool v_ok = true;
+        for (int i = 0; i < kw; i++) {
+            worst_k = std::max(worst_k, std::abs((int)(int16_t)gk[i] - (int)(int16_t)to_half(kr[i])));
+            v_ok = v_ok && gv[i] == to_half(row[qw + kw + i]);
+        }
+        EXPECT(worst_k <= 1);  // same sign here; one half ulp for a sine/cosine rounding difference
+        EXPECT(v_ok);
+        std::memcpy(&K[(size_t)p * kw], gk.data(), kw * 2);
+        std::memcpy(&V[(size_t)p * kw], gv.data(), kw * 2);
+        std::vector<uint16_t> qh(qw);
+        for (int i = 0; i < qw; i++) qh[i] = to_half(qr[i]);
+        std::vector<double> ref(qw);
+        oracle_attention_f64(nh, nkv, hd, 1, p, p + 1, 1, 1.0 / std::sqrt((double)hd), qh.data(), qw, K.data(), V.data(), kw,
+                             ref.data(), qw, nullptr);
+        std::vector<float> got(qw);
+        HIP_OK(hipMemcpy(got.data(), dout, qw * 4, hipMemcpyDeviceToHost));
+        size_t bad = 0;
+        for (int i = 0; i < qw; i++)
+            if (!(std::fabs(got[i] - ref[i]) <= 2e-3 + 1e-2 * std::fabs(ref[i]))) bad++;
+        EXPECT(bad == 0);
+    }
+    EXPECT(attn->decode_step(0, dqkv, dout, n_ctx).code == Code::ResourceExhausted);
+    (void)hipFree(dqkv);
+    (void)hipFree(dout);
 }
 
 TEST(llama_errors) {
