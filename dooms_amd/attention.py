@@ -118,3 +118,27 @@ def decode_rope(qkv, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim,
                                     out.data_ptr(), lse.data_ptr() if lse is not None else 0, workspace.data_ptr(),
                                     workspace.numel(), _stream()))
     return out, lse
+
+
+def prefill_rope(qkv, k_cache, v_cache, *, n_head, n_head_kv, head_dim, rope_mode, rope_base=10000.0, p0=0,
+                 causal=True, n_kv=None, scale=None, out=None, lse=None, want_lse=False):
+    """mx_attn_prefill_rope: qkv f32 [n_q][>= (n_head + 2 n_head_kv) hd] unrotated rows at positions p0 ..; their keys
+    and values are written (rotated, f16) into rows p0 .. of k_cache / v_cache, then the chunk attends.
+    Returns (out f32 [n_q][n_head hd], lse or None)."""
+    _rows(qkv, "qkv", torch.float32), _rows(k_cache, "k_cache"), _rows(v_cache, "v_cache")
+    if k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("k_cache and v_cache must share a row stride")
+    n_q = qkv.shape[0]
+    if out is None:
+        out = torch.empty(n_q, n_head * head_dim, dtype=torch.float32, device=qkv.device)
+    _rows(out, "out", torch.float32)
+    if want_lse and lse is None:
+        lse = torch.empty(n_q, n_head, dtype=torch.float32, device=qkv.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, qkv.stride(0), k_cache.stride(0), out.stride(0), scale,
+                       p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0)
+    _lib.check(_lib.prefill_rope_raw(d, rope_mode, rope_base, qkv.data_ptr(), k_cache.data_ptr(),
+                                     v_cache.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else 0,
+                                     _stream()))
+    return out, lse

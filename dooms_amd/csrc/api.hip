@@ -114,6 +114,84 @@ size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len
 
 namespace {
 
+// Rotary frequencies base^(-2i / head_dim) in f32 (rotate_pair, llama_kernels.h:513-518), computed once per call
+// on the host with the C library's powf; 0 past head_dim / 2 or without rotation.
+void fill_freq(float (&freq)[mx::kMaxHeadDim / 2], const mx_attn_rope * rope, int head_dim) {
+    for (int i = 0; i < mx::kMaxHeadDim / 2; i++)
+        freq[i] = (rope && rope->mode != 2 && i < head_dim / 2) ? std::pow(rope->base, -2.f * (float)i / (float)head_dim) : 0.f;
+}
+
+int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_cache, const void * v_cache, void * out,
+                     float * lse, mx_attn_stream stream, const mx_attn_rope * rope) {
+    const mx_attn_desc & d = *desc;
+    if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
+    if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
+    if (d.n_q == 0) return MX_ATTN_OK;
+    const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
+    if (n_kv > INT32_MAX) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 + n_q overflows");
+    if ((d.causal || rope) && n_kv < (int64_t)d.p0 + d.n_q)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%lld) must be >= p0 + n_q (%lld): the chunk's own rows are in the cache",
+                    (long long)n_kv, (long long)d.p0 + d.n_q);
+    if (!q || !k_cache || !v_cache || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must not be null");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must be 16-byte aligned");
+    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+
+    mx::PrefillParams p;
+    p.q = static_cast<const mx::half_t *>(q);
+    p.k = static_cast<const mx::half_t *>(k_cache);
+    p.v = static_cast<const mx::half_t *>(v_cache);
+    p.out = static_cast<mx::half_t *>(out);
+    p.lse = lse;
+    p.q_stride = d.q_stride;
+    p.kv_stride = d.kv_stride;
+    p.out_stride = d.out_stride;
+    p.n_head = d.n_head;
+    p.n_head_kv = d.n_head_kv;
+    p.group = d.n_head / d.n_head_kv;
+    p.n_q = d.n_q;
+    p.p0 = d.p0;
+    p.n_kv = (int32_t)n_kv;
+    p.causal = d.causal;
+    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head);
+    p.n_qtiles = (d.n_q + rows - 1) / rows;
+    p.scale_log2 = d.scale * 1.4426950408889634f;
+    p.rope = rope != nullptr;
+    p.qkv = static_cast<const float *>(q);
+    p.out32 = static_cast<float *>(out);
+    p.rope_mode = rope ? rope->mode : 2;
+    fill_freq(p.rope_freq, rope, d.head_dim);
+    if (rope) {  // the chunk's keys and values go into the caches first (stream order)
+        mx::RopeStoreParams r;
+        r.qkv = static_cast<const float *>(q);
+        r.k = static_cast<mx::half_t *>(const_cast<void *>(k_cache));
+        r.v = static_cast<mx::half_t *>(const_cast<void *>(v_cache));
+        r.qkv_stride = d.q_stride;
+        r.kv_stride = d.kv_stride;
+        r.n_head = d.n_head;
+        r.n_head_kv = d.n_head_kv;
+        r.n_rows = d.n_q;
+        r.p0 = d.p0;
+        r.rope_mode = rope->mode;
+        fill_freq(r.rope_freq, rope, d.head_dim);
+        if (int32_t rc = hip_status(mx::launch_rope_store(r, d.head_dim, st), "rope_store launch")) return rc;
+    }
+    return hip_status(mx::launch_prefill(p, d.head_dim, st), "prefill launch");
+}
+
+// Checks of the rotary parameters and the q|k|v row width shared by the two fused entry points.
+int32_t check_rope(const mx_attn_desc & d, const mx_attn_rope * rope) {
+    if (!rope) return fail(MX_ATTN_INVALID_ARGUMENT, "rope is null");
+    if (rope->mode < 0 || rope->mode > 2) return fail(MX_ATTN_INVALID_ARGUMENT, "rope->mode (%d) must be 0, 1 or 2", rope->mode);
+    if (rope->mode != 2 && !(std::isfinite(rope->base) && rope->base > 0.f))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "rope->base must be finite and > 0");
+    const int64_t row = (int64_t)(d.n_head + 2 * d.n_head_kv) * d.head_dim;
+    if (d.q_stride < row)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "q_stride (%lld) < (n_head + 2 n_head_kv) * head_dim (%lld)", (long long)d.q_stride, (long long)row);
+    return MX_ATTN_OK;
+}
+
 // Shared by mx_attn_decode (rope == nullptr: half q rows and output) and mx_attn_decode_rope (f32 q|k|v rows and
 // output, the new token's key and value appended to the caches by the kernel).
 int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const void * q,
@@ -154,8 +232,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         p.qkv = static_cast<const float *>(q);
         p.out32 = static_cast<float *>(out);
         p.rope_mode = rope ? rope->mode : 2;
-        for (int i = 0; i < mx::kMaxHeadDim / 2; i++)
-            p.rope_freq[i] = (rope && rope->mode != 2 && i < d.head_dim / 2) ? std::pow(rope->base, -2.f * (float)i / (float)d.head_dim) : 0.f;
+        fill_freq(p.rope_freq, rope, d.head_dim);
         p.lse = lse;
         p.counters = static_cast<uint32_t *>(workspace);
         p.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + wl.counter_bytes);
@@ -219,39 +296,14 @@ MX_ATTN_API const char * mx_attn_last_error(void) { return g_last_error.c_str();
 MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * q, const uint16_t * k_cache, const uint16_t * v_cache,
                                     uint16_t * out, float * lse, mx_attn_stream stream) {
     if (int32_t rc = check_desc(desc)) return rc;
-    const mx_attn_desc & d = *desc;
-    if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
-    if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
-    if (d.n_q == 0) return MX_ATTN_OK;
-    const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
-    if (n_kv > INT32_MAX) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 + n_q overflows");
-    if (d.causal && n_kv < (int64_t)d.p0 + d.n_q)
-        return fail(MX_ATTN_INVALID_ARGUMENT, "causal prefill needs n_kv (%lld) >= p0 + n_q (%lld)", (long long)n_kv, (long long)d.p0 + d.n_q);
-    if (!q || !k_cache || !v_cache || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must not be null");
-    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must be 16-byte aligned");
-    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
+    return prefill_impl(desc, q, k_cache, v_cache, out, lse, stream, nullptr);
+}
 
-    mx::PrefillParams p;
-    p.q = reinterpret_cast<const mx::half_t *>(q);
-    p.k = reinterpret_cast<const mx::half_t *>(k_cache);
-    p.v = reinterpret_cast<const mx::half_t *>(v_cache);
-    p.out = reinterpret_cast<mx::half_t *>(out);
-    p.lse = lse;
-    p.q_stride = d.q_stride;
-    p.kv_stride = d.kv_stride;
-    p.out_stride = d.out_stride;
-    p.n_head = d.n_head;
-    p.n_head_kv = d.n_head_kv;
-    p.group = d.n_head / d.n_head_kv;
-    p.n_q = d.n_q;
-    p.p0 = d.p0;
-    p.n_kv = (int32_t)n_kv;
-    p.causal = d.causal;
-    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head);
-    p.n_qtiles = (d.n_q + rows - 1) / rows;
-    p.scale_log2 = d.scale * 1.4426950408889634f;
-    return hip_status(mx::launch_prefill(p, d.head_dim, static_cast<hipStream_t>(stream)), "prefill launch");
+MX_ATTN_API int32_t mx_attn_prefill_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, const float * qkv, uint16_t * k_cache,
+                                         uint16_t * v_cache, float * out, float * lse, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    if (int32_t rc = check_rope(*desc, rope)) return rc;
+    return prefill_impl(desc, qkv, k_cache, v_cache, out, lse, stream, rope);
 }
 
 MX_ATTN_API size_t mx_attn_decode_workspace_bytes(const mx_attn_desc * desc, int32_t batch, int32_t max_kv_len) {
@@ -285,15 +337,9 @@ MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn
                                         float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream) {
     if (int32_t rc = check_desc(desc)) return rc;
     const mx_attn_desc & d = *desc;
-    if (!rope) return fail(MX_ATTN_INVALID_ARGUMENT, "rope is null");
-    if (rope->mode < 0 || rope->mode > 2) return fail(MX_ATTN_INVALID_ARGUMENT, "rope->mode (%d) must be 0, 1 or 2", rope->mode);
-    if (rope->mode != 2 && !(std::isfinite(rope->base) && rope->base > 0.f))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "rope->base must be finite and > 0");
+    if (int32_t rc = check_rope(d, rope)) return rc;
     if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
     if (d.n_q != 1) return fail(MX_ATTN_INVALID_ARGUMENT, "n_q (%d) must be 1: one new token per sequence", d.n_q);
-    const int64_t row = (int64_t)(d.n_head + 2 * d.n_head_kv) * d.head_dim;
-    if (d.q_stride < row)
-        return fail(MX_ATTN_INVALID_ARGUMENT, "q_stride (%lld) < (n_head + 2 n_head_kv) * head_dim (%lld)", (long long)d.q_stride, (long long)row);
     // the same k/v cache under two sequences would be appended twice at different positions
     for (int32_t b = 0; b < batch && k_caches && v_caches; b++)
         for (int32_t c = 0; c < b; c++)

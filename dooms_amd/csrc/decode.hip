@@ -62,78 +62,6 @@ struct KvBlock {
     u32x4 v[NLV];
 };
 
-// sin and cos of an f32 angle (|x| up to ~1e9): Cody-Waite reduction by pi/2 in double (pi/2 split in two doubles,
-// fma), so the reduced |r| <= pi/4 is exact to f32, then the Taylor series of sin and cos to degree 11 / 12 in f32
-// (truncation below 2e-9 there). Error a few f32 ulps of 1; no large-argument slow path, no private memory.
-__device__ __forceinline__ void sincos_rope(float x, float & s_out, float & c_out) {
-    constexpr double kTwoOverPi = 0.63661977236758134308, kPio2Hi = 1.5707963267948966, kPio2Lo = 6.123233995736766e-17;
-    const double k = __builtin_rint((double)x * kTwoOverPi);
-    const float r = (float)__builtin_fma(-k, kPio2Lo, __builtin_fma(-k, kPio2Hi, (double)x));
-    const float r2 = r * r;
-    float sp = -1.f / 39916800.f;
-    sp = __builtin_fmaf(sp, r2, 1.f / 362880.f);
-    sp = __builtin_fmaf(sp, r2, -1.f / 5040.f);
-    sp = __builtin_fmaf(sp, r2, 1.f / 120.f);
-    sp = __builtin_fmaf(sp, r2, -1.f / 6.f);
-    const float sn = __builtin_fmaf(sp * r2, r, r);
-    float cp = 1.f / 479001600.f;
-    cp = __builtin_fmaf(cp, r2, -1.f / 3628800.f);
-    cp = __builtin_fmaf(cp, r2, 1.f / 40320.f);
-    cp = __builtin_fmaf(cp, r2, -1.f / 720.f);
-    cp = __builtin_fmaf(cp, r2, 1.f / 24.f);
-    cp = __builtin_fmaf(cp, r2, -0.5f);
-    const float cs = __builtin_fmaf(cp, r2, 1.f);
-    const int q = (int)((long long)k & 3);
-    s_out = q == 0 ? sn : q == 1 ? cs : q == 2 ? -sn : -cs;
-    c_out = q == 0 ? cs : q == 1 ? -sn : q == 2 ? -cs : sn;
-}
-
-// Rotary embedding of the KS 8-element chunks of one head row that a lane holds (chunk ks covers head dims
-// 32 ks + 8 sgrp .. + 8) for position pos: the reference's rotate_pair (llama_kernels.h:513-518). Pair i turns by the
-// f32 angle theta = float(pos) * freq[i], freq[i] = base^(-2i / head_dim) in f32 (computed once on the host), and the
-// rotation in f32, as the reference's. mode 0: adjacent pairs (2i, 2i + 1), llama.cpp's
-// "normal"; 1: split halves (i, i + head_dim / 2), "neox" (qwen2) -- the partner of chunk ks is chunk ks + KS / 2 of
-// the same lane; 2: none.
-template <int HD>
-__device__ __forceinline__ void rope_chunks(float (&x)[HD / 32][8], int sgrp, int mode, const float2 * cs_tab) {
-    constexpr int KS = HD / 32;
-    if (mode == 2) return;
-    auto rot = [&](float & a, float & b, int i) {
-        const float2 t = cs_tab[i];
-        const float cs = t.x, sn = t.y;
-        const float ra = a * cs - b * sn, rb = a * sn + b * cs;
-        a = ra;
-        b = rb;
-    };
-    if (mode == 0) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) rot(x[ks][e], x[ks][e + 1], (32 * ks + 8 * sgrp + e) / 2);
-    } else {
-#pragma unroll
-        for (int ks = 0; ks < KS / 2; ks++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) rot(x[ks][e], x[ks + KS / 2][e], 32 * ks + 8 * sgrp + e);
-    }
-}
-
-__device__ __forceinline__ void load8f(const float * src, float (&x)[8]) {
-    const float4_t a = *reinterpret_cast<const float4_t *>(src), b = *reinterpret_cast<const float4_t *>(src + 4);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        x[e] = a[e];
-        x[4 + e] = b[e];
-    }
-}
-
-__device__ __forceinline__ u32x4 to_half8(const float (&x)[8]) {
-    half8_t h;
-#pragma unroll
-    for (int e = 0; e < 8; e++) h[e] = (half_t)x[e];
-    return __builtin_bit_cast(u32x4, h);
-}
-
 // Two adjacent output elements: half, or f32 for the fused step (the reference's f32 attention output).
 template <bool F32>
 __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, float a, float b) {
@@ -249,11 +177,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
             }
             __syncthreads();
         }
-        if (srow_ok) rope_chunks<HD>(xq, sgrp, p.rope_mode, s_cs);
+        if (srow_ok) rope_rotate<KS, 32>(xq, 8 * sgrp, p.rope_mode, [&](int i) { return s_cs[i]; });
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(xq[ks]));
         if (k_lane_new) {
-            rope_chunks<HD>(x, sgrp, p.rope_mode, s_cs);
+            rope_rotate<KS, 32>(x, 8 * sgrp, p.rope_mode, [&](int i) { return s_cs[i]; });
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) kn[ks] = to_half8(x[ks]);
             if (rt == 0) {

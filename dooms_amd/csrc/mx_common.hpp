@@ -59,4 +59,74 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
     return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i;
 }
 
+// ---- rotary embedding (the reference's rotate_pair / pair_index, src/backend/metal/llama_kernels.h:508-518) ----
+
+// sin and cos of an f32 angle (|x| up to ~1e9): Cody-Waite reduction by pi/2 in double (pi/2 split in two doubles,
+// fma), so the reduced |r| <= pi/4 is exact to f32, then the Taylor series of sin and cos to degree 11 / 12 in f32
+// (truncation below 2e-9 there). Error a few f32 ulps of 1; no large-argument slow path, no private memory.
+__device__ __forceinline__ void sincos_rope(float x, float & s_out, float & c_out) {
+    constexpr double kTwoOverPi = 0.63661977236758134308, kPio2Hi = 1.5707963267948966, kPio2Lo = 6.123233995736766e-17;
+    const double k = __builtin_rint((double)x * kTwoOverPi);
+    const float r = (float)__builtin_fma(-k, kPio2Lo, __builtin_fma(-k, kPio2Hi, (double)x));
+    const float r2 = r * r;
+    float sp = -1.f / 39916800.f;
+    sp = __builtin_fmaf(sp, r2, 1.f / 362880.f);
+    sp = __builtin_fmaf(sp, r2, -1.f / 5040.f);
+    sp = __builtin_fmaf(sp, r2, 1.f / 120.f);
+    sp = __builtin_fmaf(sp, r2, -1.f / 6.f);
+    const float sn = __builtin_fmaf(sp * r2, r, r);
+    float cp = 1.f / 479001600.f;
+    cp = __builtin_fmaf(cp, r2, -1.f / 3628800.f);
+    cp = __builtin_fmaf(cp, r2, 1.f / 40320.f);
+    cp = __builtin_fmaf(cp, r2, -1.f / 720.f);
+    cp = __builtin_fmaf(cp, r2, 1.f / 24.f);
+    cp = __builtin_fmaf(cp, r2, -0.5f);
+    const float cs = __builtin_fmaf(cp, r2, 1.f);
+    const int q = (int)((long long)k & 3);
+    s_out = q == 0 ? sn : q == 1 ? cs : q == 2 ? -sn : -cs;
+    c_out = q == 0 ? cs : q == 1 ? -sn : q == 2 ? -cs : sn;
+}
+
+// Rotates the N 8-element chunks of one head row that a lane holds, chunk c covering head dims STRIDE c + off .. + 8
+// (off a multiple of 8 below STRIDE, N * STRIDE = head_dim), in f32. Pair i turns by the angle whose (cos, sin)
+// cs_of(i) returns (a float2): theta = pos * base^(-2i / head_dim). mode 0: adjacent pairs (2i, 2i + 1), llama.cpp's
+// "normal"; 1: split halves (i, i + head_dim / 2), "neox" (qwen2) -- the partner of chunk c is chunk c + N / 2 of the
+// same lane; 2: none.
+template <int N, int STRIDE, class CsOf>
+__device__ __forceinline__ void rope_rotate(float (&x)[N][8], int off, int mode, CsOf cs_of) {
+    auto rot = [&](float & a, float & b, int i) {
+        const float2 t = cs_of(i);
+        const float ra = a * t.x - b * t.y, rb = a * t.y + b * t.x;
+        a = ra;
+        b = rb;
+    };
+    if (mode == 0) {
+#pragma unroll
+        for (int c = 0; c < N; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) rot(x[c][e], x[c][e + 1], (STRIDE * c + off + e) / 2);
+    } else if (mode == 1) {
+#pragma unroll
+        for (int c = 0; c < N / 2; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) rot(x[c][e], x[c + N / 2][e], STRIDE * c + off + e);
+    }
+}
+
+__device__ __forceinline__ void load8f(const float * src, float (&x)[8]) {
+    const float4_t a = *reinterpret_cast<const float4_t *>(src), b = *reinterpret_cast<const float4_t *>(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        x[e] = a[e];
+        x[4 + e] = b[e];
+    }
+}
+
+__device__ __forceinline__ u32x4 to_half8(const float (&x)[8]) {
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (half_t)x[e];
+    return __builtin_bit_cast(u32x4, h);
+}
+
 }  // namespace mx

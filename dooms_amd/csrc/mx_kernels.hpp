@@ -53,6 +53,23 @@ struct PrefillParams {
     int64_t q_stride, kv_stride, out_stride;
     int32_t n_head, n_head_kv, group, n_q, p0, n_kv, causal, n_qtiles;
     float scale_log2;
+    int32_t rope;       // 1: query rows come unrotated in f32 from qkv (q_stride floats apart), rotated for position
+                        // p0 + t in the kernel and rounded to half; the output is f32 (out32)
+    const float * qkv;
+    float * out32;
+    int32_t rope_mode;  // 0 adjacent pairs, 1 split halves (neox), 2 none
+    float rope_freq[kMaxHeadDim / 2];
+};
+
+// rope_store (llama_kernels.h:520-545) for the keys and values of n_rows new tokens: key head g of row t rotated for
+// position p0 + t and, like value head g, rounded to half into row p0 + t of the caches.
+struct RopeStoreParams {
+    const float * qkv;  // [n_rows][qkv_stride] f32: q | k | v
+    half_t * k;
+    half_t * v;
+    int64_t qkv_stride, kv_stride;
+    int32_t n_head, n_head_kv, n_rows, p0, rope_mode;
+    float rope_freq[kMaxHeadDim / 2];
 };
 
 int decode_rows_per_tile(int rows);
@@ -61,5 +78,6 @@ hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 
 int prefill_rows_per_workgroup(int n_q, int n_head);  // query rows one prefill workgroup covers
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
+hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
 
 }  // namespace mx

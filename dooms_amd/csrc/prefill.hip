@@ -49,7 +49,9 @@ struct PrefillSmem {
 
 // POS: the scale is > 0, so the block maximum can be taken on raw scores and the scale folded into the exponent's FMA.
 // W: waves per workgroup (32 query rows each); all W waves share each K/V tile in LDS.
-template <int HD, bool POS, int W>
+// ROPE: the reference's prompt path (rope_store, then attention_prefill on f32 q rows, llama_kernels.h:520-545, 660):
+// query rows are read in f32 from the q|k|v rows, rotated for their position and rounded to half; the output is f32.
+template <int HD, bool POS, int W, bool ROPE>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PrefillParams p) {
     constexpr int kWaves = W, kPrefillRows = 32 * W;
@@ -114,7 +116,21 @@ void prefill_kernel(PrefillParams p) {
 
     // Q^T operand: lane holds Q[qrow][16 ks + 8 hgrp .. + 8]
     half8_t qb[KS];
-    {
+    if constexpr (ROPE) {
+        float x[KS][8] = {};
+        if (qrow < p.n_q) {
+            const float * qp = p.qkv + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) load8f(qp + 16 * ks, x[ks]);
+            rope_rotate<KS, 16>(x, 8 * hgrp, p.rope_mode, [&](int i) {
+                float sn, cs;
+                sincos_rope((float)qpos * p.rope_freq[i], sn, cs);
+                return make_float2(cs, sn);
+            });
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(x[ks]));
+    } else {
         const half_t * qp = p.q + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
@@ -262,15 +278,22 @@ void prefill_kernel(PrefillParams p) {
     l_run += shfl_xor(l_run, 32);
     if (qrow < p.n_q) {
         const float inv = 1.f / l_run;
-        half_t * op = p.out + (int64_t)qrow * p.out_stride + (int64_t)h * HD + 4 * hgrp;
+        const int64_t off = (int64_t)qrow * p.out_stride + (int64_t)h * HD + 4 * hgrp;
 #pragma unroll
         for (int dt = 0; dt < DT; dt++)
 #pragma unroll
             for (int gq = 0; gq < 4; gq++) {
-                half4_t r;
+                if constexpr (ROPE) {
+                    float4_t r;
 #pragma unroll
-                for (int e = 0; e < 4; e++) r[e] = (half_t)(o[dt][4 * gq + e] * inv);
-                *reinterpret_cast<half4_t *>(op + 32 * dt + 8 * gq) = r;
+                    for (int e = 0; e < 4; e++) r[e] = o[dt][4 * gq + e] * inv;
+                    *reinterpret_cast<float4_t *>(p.out32 + off + 32 * dt + 8 * gq) = r;
+                } else {
+                    half4_t r;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) r[e] = (half_t)(o[dt][4 * gq + e] * inv);
+                    *reinterpret_cast<half4_t *>(p.out + off + 32 * dt + 8 * gq) = r;
+                }
             }
         if (p.lse && hgrp == 0) p.lse[(int64_t)qrow * p.n_head + h] = (m_run + log2_fast(l_run)) * kLn2;
     }
@@ -289,11 +312,17 @@ int prefill_waves(int n_q, int n_head) {
 
 int prefill_rows_per_workgroup(int n_q, int n_head) { return 32 * prefill_waves(n_q, n_head); }
 
+template <int HD, bool POS, bool ROPE>
+void launch_prefill_r(const PrefillParams & p, int waves, hipStream_t stream) {
+    const dim3 grid((uint32_t)p.n_qtiles * p.n_head);
+    if (waves == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE>), grid, dim3(8 * kWave), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE>), grid, dim3(4 * kWave), 0, stream, p);
+}
+
 template <int HD, bool POS>
 void launch_prefill_t(const PrefillParams & p, int waves, hipStream_t stream) {
-    const dim3 grid((uint32_t)p.n_qtiles * p.n_head);
-    if (waves == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8>), grid, dim3(8 * kWave), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4>), grid, dim3(4 * kWave), 0, stream, p);
+    if (p.rope) launch_prefill_r<HD, POS, true>(p, waves, stream);
+    else launch_prefill_r<HD, POS, false>(p, waves, stream);
 }
 
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream) {

@@ -160,6 +160,26 @@ MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn
                                         size_t ws_bytes, mx_attn_stream stream);
 
 /*
+ * The reference's prompt path on its own buffers: rope_store of the chunk's keys and values into the caches, then
+ * flash attention of its query rows read from the f32 q|k|v rows (rotated and rounded to half in the kernel, as the
+ * reference rounds q at llama_kernels.h:660). Replaces rope_store + attention_prefill<64|128> (llama_kernels.h:520-545,
+ * 632-769) as dispatched by MetalLlamaDecoder::Impl::attention(enc, cache_off, M, p0, fused_rope = false)
+ * (metal_llama_decoder.mm:276-296), and with rope->mode = 2 the Whisper prompt (metal_whisper_decoder.mm:182-203).
+ *
+ *   qkv     device, f32, [n_q rows][q_stride floats]: token t (position p0 + t) as q | k | v, unrotated
+ *   k_cache [n_kv rows][kv_stride] f16: rows p0 .. p0 + n_q - 1 are written (rotated keys), then all rows visible to a
+ *           query are read; n_kv (0: p0 + n_q) must cover the chunk
+ *   v_cache the same for the values
+ *   out     device, f32, [n_q rows][out_stride floats]
+ *   lse     as for mx_attn_prefill
+ *
+ * Two launches on `stream` (the cache write, then the attention); no workspace.
+ */
+MX_ATTN_API int32_t mx_attn_prefill_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, const float * qkv,
+                                         uint16_t * k_cache, uint16_t * v_cache, float * out, float * lse,
+                                         mx_attn_stream stream);
+
+/*
  * Zero-fills a decode workspace on `stream` (with a kernel, not a memset, so that a caller may capture it in a HIP
  * graph). Call it once after allocating the workspace; mx_attn_decode keeps it ready for the next call. It has no
  * counterpart in the reference, whose split partials need no counters (attention_combine runs as a second dispatch,

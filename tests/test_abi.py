@@ -145,6 +145,21 @@ def test_decode_rope_checks():
     assert rope_decode(d, qkv=A + 8) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
 
 
+def test_prefill_rope_checks():
+    L = _lib.lib()
+    r = _lib.MxAttnRope(mode=1, base=1e6)
+    call = lambda d, rope=r, qkv=A: L.mx_attn_prefill_rope(ctypes.byref(d), ctypes.byref(rope) if rope else None, qkv,
+                                                           A, A, A, None, None)
+    d = desc(q_stride=6144, n_q=16, p0=4)
+    assert call(d, rope=None) == _lib.INVALID_ARGUMENT and "rope is null" in _lib.last_error()
+    assert call(d, rope=_lib.MxAttnRope(mode=-1, base=1.0)) == _lib.INVALID_ARGUMENT
+    assert call(desc(q_stride=4096, n_q=16)) == _lib.INVALID_ARGUMENT and "q_stride" in _lib.last_error()
+    assert call(desc(q_stride=6144, n_q=16, p0=4, n_kv=10, causal=0)) == _lib.INVALID_ARGUMENT
+    assert "cache" in _lib.last_error()
+    assert call(d, qkv=A + 4) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
+    assert call(desc(q_stride=6144, n_q=0)) == _lib.OK
+
+
 def test_workspace_init_checks():
     L = _lib.lib()
     assert L.mx_attn_decode_workspace_init(None, 0, None) == _lib.OK
