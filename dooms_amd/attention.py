@@ -60,20 +60,22 @@ def new_workspace(nbytes: int, device) -> torch.Tensor:
 
 def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1, causal=False, scale=None,
            out=None, lse=None, want_lse=False, workspace=None):
-    """mx_attn_decode: q [batch*n_q][>= n_head*hd]; k_caches/v_caches lists of [>= kv_len[b]][>= n_head_kv*hd]
-    tensors (entries may repeat); kv_len list of ints. Returns (out, lse or None)."""
+    """mx_attn_decode (float16 q) or mx_attn_decode_f32 (float32 q and output): q [batch*n_q][>= n_head*hd];
+    k_caches/v_caches lists of [>= kv_len[b]][>= n_head_kv*hd] float16 tensors (entries may repeat); kv_len list of
+    ints. Returns (out, lse or None)."""
     batch = len(kv_len)
     if len(k_caches) != batch or len(v_caches) != batch:
         raise ValueError("k_caches, v_caches and kv_len must have one entry per sequence")
-    _rows(q, "q")
+    f32 = q.dtype == torch.float32
+    _rows(q, "q", q.dtype if f32 else torch.float16)
     kv_stride = k_caches[0].stride(0)
     for t in list(k_caches) + list(v_caches):
         _rows(t, "cache")
         if t.stride(0) != kv_stride:
             raise ValueError("every cache must share one row stride")
     if out is None:
-        out = torch.empty(q.shape[0], n_head * head_dim, dtype=torch.float16, device=q.device)
-    _rows(out, "out")
+        out = torch.empty(q.shape[0], n_head * head_dim, dtype=q.dtype, device=q.device)
+    _rows(out, "out", q.dtype)
     if want_lse and lse is None:
         lse = torch.empty(q.shape[0], n_head, dtype=torch.float32, device=q.device)
     if scale is None:
@@ -82,7 +84,7 @@ def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1,
                        causal=1 if causal else 0)
     if workspace is None:
         workspace = new_workspace(_lib.decode_workspace_bytes(d, batch, max(kv_len)), q.device)
-    _lib.check(_lib.decode_raw(d, list(kv_len), q.data_ptr(), [t.data_ptr() for t in k_caches],
+    _lib.check((_lib.decode_f32_raw if f32 else _lib.decode_raw)(d, list(kv_len), q.data_ptr(), [t.data_ptr() for t in k_caches],
                                [t.data_ptr() for t in v_caches], out.data_ptr(),
                                lse.data_ptr() if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
                                _stream()))

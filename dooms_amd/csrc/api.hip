@@ -192,11 +192,11 @@ int32_t check_rope(const mx_attn_desc & d, const mx_attn_rope * rope) {
     return MX_ATTN_OK;
 }
 
-// Shared by mx_attn_decode (rope == nullptr: half q rows and output) and mx_attn_decode_rope (f32 q|k|v rows and
-// output, the new token's key and value appended to the caches by the kernel).
+// Shared by mx_attn_decode (half q rows and output), mx_attn_decode_f32 (f32 q rows and output) and
+// mx_attn_decode_rope (f32 q|k|v rows and output, the new token's key and value appended to the caches by the kernel).
 int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const void * q,
                     const void * const * k_caches, const void * const * v_caches, void * out, float * lse,
-                    void * workspace, size_t ws_bytes, mx_attn_stream stream, const mx_attn_rope * rope) {
+                    void * workspace, size_t ws_bytes, mx_attn_stream stream, const mx_attn_rope * rope, bool f32) {
     const mx_attn_desc & d = *desc;
 
     if (!kv_len || !k_caches || !v_caches) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len, k_caches and v_caches must not be null");
@@ -228,7 +228,8 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         mx::DecodeParams p;
         p.q = static_cast<const mx::half_t *>(q);
         p.out = static_cast<mx::half_t *>(out);
-        p.rope = rope != nullptr;
+        p.f32 = f32 ? 1 : 0;
+        p.append = rope != nullptr;
         p.qkv = static_cast<const float *>(q);
         p.out32 = static_cast<float *>(out);
         p.rope_mode = rope ? rope->mode : 2;
@@ -329,7 +330,17 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
     if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
     if (desc->n_q == 0) return MX_ATTN_OK;
     return decode_impl(desc, batch, kv_len, q, reinterpret_cast<const void * const *>(k_caches),
-                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, nullptr);
+                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, nullptr, false);
+}
+
+MX_ATTN_API int32_t mx_attn_decode_f32(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const float * q,
+                                       const uint16_t * const * k_caches, const uint16_t * const * v_caches, float * out,
+                                       float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
+    if (desc->n_q == 0) return MX_ATTN_OK;
+    return decode_impl(desc, batch, kv_len, q, reinterpret_cast<const void * const *>(k_caches),
+                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, nullptr, true);
 }
 
 MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, int32_t batch, const int32_t * kv_len,
@@ -346,7 +357,7 @@ MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn
             if (k_caches[b] == k_caches[c] || v_caches[b] == v_caches[c])
                 return fail(MX_ATTN_INVALID_ARGUMENT, "sequences %d and %d share a cache: each sequence appends to its own", c, b);
     return decode_impl(desc, batch, kv_len, qkv, reinterpret_cast<const void * const *>(k_caches),
-                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, rope);
+                       reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, rope, true);
 }
 
 }  // extern "C"

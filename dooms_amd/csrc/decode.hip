@@ -74,11 +74,11 @@ __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, 
 }
 
 // HD: head_dim. RT: query rows per tile (4, 8 or 16; the MFMA tile always has 16 rows, the extra ones are zero).
-// ROPE: the fused decode step (one query row per sequence): q, k and v of the new token come unrotated, in f32, from
-// the q|k|v row; q and the new key are rotated for position kv_len - 1 and rounded to half, the new key and value are
-// used from registers for that position and written into the caches by the one workgroup whose split holds it; the
-// output is f32.
-template <int HD, int RT, bool ROPE>
+// F32: the query rows and the output are f32, as in the reference's buffers (the query is rounded to half here).
+// With p.append it is the fused decode step (one query row per sequence): q, k and v of the new token come unrotated
+// from the q|k|v row; q and the new key are rotated for position kv_len - 1 and rounded to half, the new key and value
+// are used from registers for that position and written into the caches by the one workgroup whose split holds it.
+template <int HD, int RT, bool F32>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) {
     using B = KvBlock<HD>;
     constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     __shared__ float s_m[kDecodeWaves][RT], s_l[kDecodeWaves][RT];
     __shared__ float s_o[kDecodeWaves][RT * HD];
     __shared__ int s_last;
-    __shared__ float2 s_cs[ROPE ? HD / 2 : 1];  // fused step: (cos, sin) of each rotary pair's angle
+    __shared__ float2 s_cs[F32 ? HD / 2 : 1];  // fused step: (cos, sin) of each rotary pair's angle
 
     const int s = blockIdx.x;
     int y = blockIdx.y;
@@ -132,9 +132,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     const int st = rr / G, sh = g * G + rr % G;
     const int lim = p.causal ? L - p.n_q + st : L - 1;  // last visible key of the row
     half8_t qb[KS];
-    float xq[ROPE ? KS : 1][8] = {};  // fused step: the f32 query, rotated once the first block's loads are out
-    if constexpr (ROPE) {
-        const float * qrow = p.qkv + seq_row0 * p.q_stride + (int64_t)sh * HD;
+    float xq[F32 ? KS : 1][8] = {};  // the f32 query (fused step: rotated once the first block's loads are out)
+    if constexpr (F32) {
+        const float * qrow = p.qkv + (seq_row0 + st) * p.q_stride + (int64_t)sh * HD;
         if (srow_ok) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, xq[ks]);
@@ -156,11 +156,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
 
     // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
     const int jb_new = (L - 1) & ~(kBlockKeys - 1);
-    const bool wave_new = ROPE && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % kDecodeWaves == wave;
+    const bool wave_new = F32 && p.append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % kDecodeWaves == wave;
     const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
     const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
     u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
-    if constexpr (ROPE) {  // the query and the new key rotated, the new key and value rounded to half as cached
+    if constexpr (F32) {  // fused step: the query and the new key rotated, the new key and value rounded to half
         const float * row = p.qkv + seq_row0 * p.q_stride;
         float x[KS][8], xv[8];
         if (k_lane_new) {
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
             for (int ks = 0; ks < KS; ks++) load8f(kr + 32 * ks, x[ks]);
         }
         if (v_lane_new) load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, xv);
-        if (p.rope_mode != 2) {  // the 64 (hd 128) angles of position L - 1, once per workgroup
+        if (p.append && p.rope_mode != 2) {  // the 64 (hd 128) angles of position L - 1, once per workgroup
             if (threadIdx.x < HD / 2) {
                 float sn, cs;
                 sincos_rope((float)(L - 1) * p.rope_freq[threadIdx.x], sn, cs);
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
             }
             __syncthreads();
         }
-        if (srow_ok) rope_rotate<KS, 32>(xq, 8 * sgrp, p.rope_mode, [&](int i) { return s_cs[i]; });
+        if (srow_ok && p.append) rope_rotate<KS, 32>(xq, 8 * sgrp, p.rope_mode, [&](int i) { return s_cs[i]; });
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(xq[ks]));
         if (k_lane_new) {
@@ -209,8 +209,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     for (; jb < j1; jb += kBlockKeys * kDecodeWaves) {
         const int jn = jb + kBlockKeys * kDecodeWaves;
         if (jn < j1) load_block(jn, nxt);
-        if constexpr (ROPE) {
-            if (jb == jb_new) {  // the new key and value replace what the cache held at L - 1
+        if constexpr (F32) {
+            if (wave_new && jb == jb_new) {  // the new key and value replace what the cache held at L - 1
                 const int mt_new = ((L - 1) % kBlockKeys) / 16, i_new = ((L - 1) % kBlockKeys) / KPL;
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++)  // constant register indices: a runtime one would go through memory
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
         }
         if (single) {
             const int t = row / G, h = g * G + row % G;
-            store_pair<ROPE>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 / tot, a1 / tot);
+            store_pair<F32>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 / tot, a1 / tot);
             if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
         } else {
             float * pe = part_tile + s * SS + (int64_t)r * (HD + 4);
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
         }
         const int t = row / G, h = g * G + row % G;
         const float inv = 1.f / tot;
-        store_pair<ROPE>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 * inv, a1 * inv);
+        store_pair<F32>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 * inv, a1 * inv);
         if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
     }
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
 template <int HD, int RT>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
     const int tiles = n_seq * p.n_head_kv * p.n_rowtiles;
-    if (p.rope)
+    if (p.f32)
         hipLaunchKernelGGL((decode_kernel<HD, RT, true>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
     else
         hipLaunchKernelGGL((decode_kernel<HD, RT, false>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);

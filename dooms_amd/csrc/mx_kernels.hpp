@@ -36,7 +36,8 @@ struct DecodeParams {
     int32_t max_split;   // max over the launch's sequences of n_split
     int32_t seq0;        // index of the launch's first sequence in the caller's batch (query/output rows)
     float scale_log2;    // scale * log2(e): scores are kept in base-2 units
-    int32_t rope;        // 1: fused decode step: q|k|v rows in qkv (f32, q_stride floats apart), f32 output in out32
+    int32_t f32;         // 1: f32 query rows in qkv (q_stride floats apart) and f32 output in out32
+    int32_t append;      // 1 (with f32): fused decode step, the rows are q|k|v of each sequence's new token
     const float * qkv;
     float * out32;
     int32_t rope_mode;   // 0 adjacent pairs, 1 split halves (neox), 2 none

@@ -4,11 +4,13 @@
 //   reference (dooms.cpp 0.6.1)                                               here
 //   MetalLlamaDecoder::Impl::attention(enc, cache_off, M, p0, false)          LlamaAttention::attention(layer, q, out, M, p0)
 //   MetalLlamaDecoder::Impl::attention(enc, cache_off, 1, p, true)            LlamaAttention::decode_step(layer, qkv, out, p)
+//     (and with rope_store for a prompt chunk, f32 q|k|v rows)               LlamaAttention::prompt(layer, qkv, out, M, p0)
 //     (src/backend/metal/metal_llama_decoder.mm:238-307)
 //   MetalWhisperDecoder::Impl::self_attention(cache_off, p)                    WhisperAttention::self_attention(layer, q, out, p)
 //   MetalWhisperDecoder::Impl::self_attention_prompt(cache_off, p0, M)         WhisperAttention::self_attention_prompt(...)
 //   MetalWhisperDecoder::Impl::cross_attention(cache_off, M)                   WhisperAttention::cross_attention(layer, q, out, M)
-//     (src/backend/metal/metal_whisper_decoder.mm:167-225)
+//     (src/backend/metal/metal_whisper_decoder.mm:167-225); each also on the reference's own f32 buffers (overloads
+//     taking float q|k|v rows and float output: the cache write of the step / prompt happens in the library)
 //   Status / Code (src/core/status.h:13-81)                                     Status / Code below (same numbering)
 //
 // The caches keep the reference's layout: per layer [n_ctx][n_head_kv * head_dim] f16, layer l at l * n_ctx rows
@@ -156,6 +158,20 @@ public:
         return Status::from(mx_attn_prefill(&d, q, k, v, out, nullptr, stream_));
     }
 
+    // A prompt chunk of M tokens at positions p0 .. p0 + M - 1 on the reference's buffers (rope_store + attention with
+    // fused_rope = false, metal_llama_decoder.mm:276-296): qkv holds the chunk's f32 q | k | v rows, unrotated; their
+    // keys and values are rotated and written into the layer's cache, and out (f32) gets the causal attention.
+    Status prompt(int32_t layer, const float * qkv, float * out, int32_t M, int32_t p0) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (M < 1 || p0 < 0) return {Code::InvalidArgument, "need M >= 1 rows at a position p0 >= 0"};
+        if ((int64_t)p0 + M > cfg_.n_ctx) return {Code::ResourceExhausted, "the context would overflow"};
+        mx_attn_desc d = desc(M, q_width() + 2 * kv_width(), q_width());
+        d.p0 = p0;
+        d.causal = 1;
+        const mx_attn_rope rope{cfg_.rope_neox ? 1 : 0, cfg_.rope_base};
+        return Status::from(mx_attn_prefill_rope(&d, &rope, qkv, k_layer(layer), v_layer(layer), out, nullptr, stream_));
+    }
+
     // One decode step of layer l at position p, the reference's attention(enc, cache_off, 1, p, fused_rope = true)
     // (metal_llama_decoder.mm:298-306): qkv is the new token's f32 q | k | v projection row, unrotated; q and k are
     // rotated for position p, k and v are written into the layer's cache at p, and out (f32, q_width floats) gets the
@@ -247,6 +263,39 @@ public:
     // M query rows (greedy 1, or one per beam) over the layer's n_audio_ctx encoder keys/values.
     Status cross_attention(int32_t layer, const uint16_t * q, uint16_t * out, int32_t M) {
         return run(layer, q, out, M, cfg_.n_audio_ctx, 0, cross_k(layer), cross_v(layer));
+    }
+
+    // The same three calls on the reference's f32 buffers (metal_whisper_decoder.mm:167-225): qkv rows are
+    // q | k | v (3 n_state floats), unrotated (Whisper's positions are learned); the step and the prompt write their
+    // keys/values into the self cache themselves; out is f32.
+    Status self_attention(int32_t layer, const float * qkv, float * out, int32_t p) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (p < 0 || p >= cfg_.n_text_ctx) return {Code::ResourceExhausted, "text position out of the context"};
+        mx_attn_desc d = desc(1, 0);
+        d.q_stride = 3 * cfg_.n_state;
+        const mx_attn_rope none{2, 0.f};
+        const int32_t n = p + 1;
+        uint16_t * k = self_k(layer);
+        uint16_t * v = self_v(layer);
+        return Status::from(mx_attn_decode_rope(&d, &none, 1, &n, qkv, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+    }
+    Status self_attention_prompt(int32_t layer, const float * qkv, float * out, int32_t p0, int32_t M) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (p0 < 0 || M < 1 || (int64_t)p0 + M > cfg_.n_text_ctx) return {Code::ResourceExhausted, "prompt out of the context"};
+        mx_attn_desc d = desc(M, 1);
+        d.q_stride = 3 * cfg_.n_state;
+        d.p0 = p0;
+        const mx_attn_rope none{2, 0.f};
+        return Status::from(mx_attn_prefill_rope(&d, &none, qkv, self_k(layer), self_v(layer), out, nullptr, stream_));
+    }
+    Status cross_attention(int32_t layer, const float * q, float * out, int32_t M) {
+        if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
+        if (M < 1 || M > cfg_.max_rows) return {Code::InvalidArgument, "rows must be in [1, max_rows]"};
+        mx_attn_desc d = desc(M, 0);
+        const int32_t n = cfg_.n_audio_ctx;
+        const uint16_t * k = cross_k(layer);
+        const uint16_t * v = cross_v(layer);
+        return Status::from(mx_attn_decode_f32(&d, 1, &n, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
     }
 
 private:

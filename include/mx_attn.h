@@ -127,6 +127,16 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
                                    const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out,
                                    float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream);
 
+/*
+ * mx_attn_decode on the reference's f32 buffers: q rows and the output are f32 (q_stride / out_stride in floats), the
+ * caches f16; the query is rounded to half in the kernel. Replaces attention_split + attention_combine on the Whisper
+ * decoder's f32 q / attn buffers (metal_whisper_decoder.mm:205-225, llama_kernels.h:856-929) and the per-query
+ * `attention` kernel without fused_rope (llama_kernels.h:552-630). Everything else as mx_attn_decode.
+ */
+MX_ATTN_API int32_t mx_attn_decode_f32(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const float * q,
+                                       const uint16_t * const * k_caches, const uint16_t * const * v_caches, float * out,
+                                       float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream);
+
 /* Rotary embedding of the fused decode step: the reference's AttnParams.neox / base (llama_kernels.h:501-506). */
 typedef struct mx_attn_rope {
     int32_t mode; /* 0: adjacent pairs (2i, 2i + 1), llama.cpp's "normal" (llama); 1: split halves (i, i + head_dim / 2),

@@ -135,9 +135,10 @@ TEST(llama_prompt_in_chunks_then_decode_steps) {
         for (int l = 0; l < n_layer; l++) EXPECT(run_rows(l, p, 1));
 }
 
-// Qwen2-style (neox rope, base 1e6): a 37-token prompt appended rotated, then fused decode steps; each step's output and
-// the cache rows it wrote are checked against the oracle's rope and attention.
-TEST(llama_fused_rope_decode_steps) {
+// Qwen2-style (neox rope, base 1e6) on the reference's f32 buffers: a 37-token prompt in chunks of 16 through prompt()
+// (rope_store + flash attention), then fused decode steps; every output and every cache row written is checked against
+// the oracle's rope and attention.
+TEST(llama_f32_prompt_then_fused_decode_steps) {
     using namespace dooms_amd;
     const int n_ctx = 64, nh = 14, nkv = 2, hd = 64, qw = nh * hd, kw = nkv * hd, rw = qw + 2 * kw;
     const float base = 1e6f;
@@ -150,58 +151,54 @@ TEST(llama_fused_rope_decode_steps) {
     EXPECT(st.is_ok());
     if (!st.is_ok()) return;
     Rng rng{23};
-    const int prompt = 37, steps = 6;
+    const int prompt = 37, steps = 6, chunk = 16;
     std::vector<uint16_t> K((size_t)n_ctx * kw), V((size_t)n_ctx * kw);  // host image of the cache
-    for (int p = 0; p < prompt; p++) {
-        std::vector<float> k(kw), kr(kw);
-        for (auto & x : k) x = rng.normal();
-        oracle_rope_f32(1, base, hd, p, k.data(), kr.data(), nkv);
-        for (int i = 0; i < kw; i++) {
-            K[(size_t)p * kw + i] = to_half(kr[i]);
-            V[(size_t)p * kw + i] = to_half(rng.normal());
-        }
-    }
-    HIP_OK(hipMemcpy(kc.p, K.data(), (size_t)prompt * kw * 2, hipMemcpyHostToDevice));
-    HIP_OK(hipMemcpy(vc.p, V.data(), (size_t)prompt * kw * 2, hipMemcpyHostToDevice));
     float *dqkv = nullptr, *dout = nullptr;
-    HIP_OK(hipMalloc(&dqkv, rw * 4));
-    HIP_OK(hipMalloc(&dout, qw * 4));
-    for (int p = prompt; p < prompt + steps; p++) {
-        std::vector<float> row(rw);
-        for (auto & x : row) x = rng.normal();
-        HIP_OK(hipMemcpy(dqkv, row.data(), rw * 4, hipMemcpyHostToDevice));
-        Status s = attn->decode_step(0, dqkv, dout, p);
+    HIP_OK(hipMalloc(&dqkv, (size_t)chunk * rw * 4));
+    HIP_OK(hipMalloc(&dout, (size_t)chunk * qw * 4));
+    // runs M rows at p0 (prompt chunk, or one fused step) and checks cache rows and outputs
+    auto run = [&](int p0, int M) {
+        std::vector<float> rows((size_t)M * rw);
+        for (auto & x : rows) x = rng.normal();
+        HIP_OK(hipMemcpy(dqkv, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+        Status s = M == 1 && p0 >= prompt ? attn->decode_step(0, dqkv, dout, p0) : attn->prompt(0, dqkv, dout, M, p0);
         HIP_OK(hipDeviceSynchronize());
         EXPECT(s.is_ok());
-        std::vector<float> qr(qw), kr(kw);
-        oracle_rope_f32(1, base, hd, p, row.data(), qr.data(), nh);
-        oracle_rope_f32(1, base, hd, p, row.data() + qw, kr.data(), nkv);
-        std::vector<uint16_t> gk(kw), gv(kw);
-        HIP_OK(hipMemcpy(gk.data(), kc.p + (size_t)p * kw, kw * 2, hipMemcpyDeviceToHost));
-        HIP_OK(hipMemcpy(gv.data(), vc.p + (size_t)p * kw, kw * 2, hipMemcpyDeviceToHost));
+        std::vector<uint16_t> qh((size_t)M * qw);
         int worst_k = 0;
         bool v_ok = true;
-        for (int i = 0; i < kw; i++) {
-            worst_k = std::max(worst_k, std::abs((int)(int16_t)gk[i] - (int)(int16_t)to_half(kr[i])));
-            v_ok = v_ok && gv[i] == to_half(row[qw + kw + i]);
+        std::vector<uint16_t> gk((size_t)M * kw), gv((size_t)M * kw);
+        HIP_OK(hipMemcpy(gk.data(), kc.p + (size_t)p0 * kw, gk.size() * 2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(gv.data(), vc.p + (size_t)p0 * kw, gv.size() * 2, hipMemcpyDeviceToHost));
+        for (int t = 0; t < M; t++) {
+            const float * row = rows.data() + (size_t)t * rw;
+            std::vector<float> qr(qw), kr(kw);
+            oracle_rope_f32(1, base, hd, p0 + t, row, qr.data(), nh);
+            oracle_rope_f32(1, base, hd, p0 + t, row + qw, kr.data(), nkv);
+            for (int i = 0; i < qw; i++) qh[(size_t)t * qw + i] = to_half(qr[i]);
+            for (int i = 0; i < kw; i++) {
+                worst_k = std::max(worst_k, std::abs((int)(int16_t)gk[(size_t)t * kw + i] - (int)(int16_t)to_half(kr[i])));
+                v_ok = v_ok && gv[(size_t)t * kw + i] == to_half(row[qw + kw + i]);
+            }
         }
-        EXPECT(worst_k <= 1);  // same sign here; one half ulp for a sine/cosine rounding difference
+        EXPECT(worst_k <= 1);  // one half ulp for a sine/cosine rounding difference
         EXPECT(v_ok);
-        std::memcpy(&K[(size_t)p * kw], gk.data(), kw * 2);
-        std::memcpy(&V[(size_t)p * kw], gv.data(), kw * 2);
-        std::vector<uint16_t> qh(qw);
-        for (int i = 0; i < qw; i++) qh[i] = to_half(qr[i]);
-        std::vector<double> ref(qw);
-        oracle_attention_f64(nh, nkv, hd, 1, p, p + 1, 1, 1.0 / std::sqrt((double)hd), qh.data(), qw, K.data(), V.data(), kw,
+        std::memcpy(&K[(size_t)p0 * kw], gk.data(), gk.size() * 2);
+        std::memcpy(&V[(size_t)p0 * kw], gv.data(), gv.size() * 2);
+        std::vector<double> ref((size_t)M * qw);
+        oracle_attention_f64(nh, nkv, hd, M, p0, p0 + M, 1, 1.0 / std::sqrt((double)hd), qh.data(), qw, K.data(), V.data(), kw,
                              ref.data(), qw, nullptr);
-        std::vector<float> got(qw);
-        HIP_OK(hipMemcpy(got.data(), dout, qw * 4, hipMemcpyDeviceToHost));
+        std::vector<float> got((size_t)M * qw);
+        HIP_OK(hipMemcpy(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost));
         size_t bad = 0;
-        for (int i = 0; i < qw; i++)
+        for (size_t i = 0; i < got.size(); i++)
             if (!(std::fabs(got[i] - ref[i]) <= 2e-3 + 1e-2 * std::fabs(ref[i]))) bad++;
         EXPECT(bad == 0);
-    }
+    };
+    for (int p0 = 0; p0 < prompt; p0 += chunk) run(p0, std::min(chunk, prompt - p0));
+    for (int p = prompt; p < prompt + steps; p++) run(p, 1);
     EXPECT(attn->decode_step(0, dqkv, dout, n_ctx).code == Code::ResourceExhausted);
+    EXPECT(attn->prompt(0, dqkv, dout, 2, n_ctx - 1).code == Code::ResourceExhausted);
     (void)hipFree(dqkv);
     (void)hipFree(dout);
 }
@@ -261,6 +258,80 @@ TEST(whisper_prompt_steps_and_cross_attention) {
     EXPECT(w->cross_attention(0, dq.p, dout.p, 9).code == Code::InvalidArgument);  // more rows than max_rows
     std::unique_ptr<WhisperAttention> w80;
     EXPECT(WhisperAttention::create({1, 320, 4, 8, 8, 1}, sk.p, sv.p, ck.p, cv.p, nullptr, w80).code == Code::Unsupported);
+}
+
+// The Whisper calls on the reference's f32 buffers: prompt rows and single steps write the self cache themselves (no
+// rotation), cross-attention reads f32 query rows; f32 outputs against the oracle with the query rounded to half.
+TEST(whisper_f32_buffers) {
+    using namespace dooms_amd;
+    const int n_state = 256, nh = 4, hd = 64, n_text = 32, n_audio = 150, rw = 3 * n_state;
+    Dev sk((size_t)n_text * n_state), sv((size_t)n_text * n_state), ck((size_t)n_audio * n_state), cv((size_t)n_audio * n_state);
+    std::unique_ptr<WhisperAttention> w;
+    Status st = WhisperAttention::create({1, n_state, nh, n_text, n_audio, 8}, sk.p, sv.p, ck.p, cv.p, nullptr, w);
+    EXPECT(st.is_ok());
+    if (!st.is_ok()) return;
+    Rng rng{31};
+    const std::vector<uint16_t> CK = random_half(rng, (size_t)n_audio * n_state), CV = random_half(rng, (size_t)n_audio * n_state);
+    HIP_OK(hipMemcpy(ck.p, CK.data(), CK.size() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(cv.p, CV.data(), CV.size() * 2, hipMemcpyHostToDevice));
+    std::vector<uint16_t> SK((size_t)n_text * n_state), SV((size_t)n_text * n_state);
+    float *dq = nullptr, *dout = nullptr;
+    HIP_OK(hipMalloc(&dq, (size_t)8 * rw * 4));
+    HIP_OK(hipMalloc(&dout, (size_t)8 * n_state * 4));
+    const double scale = 1.0 / 8.0;
+    auto compare = [&](const std::vector<uint16_t> & qh, int M, const std::vector<uint16_t> & Kh, const std::vector<uint16_t> & Vh,
+                       int n_kv, int p0, int causal) {
+        std::vector<double> ref((size_t)M * n_state);
+        oracle_attention_f64(nh, nh, hd, M, p0, n_kv, causal, scale, qh.data(), n_state, Kh.data(), Vh.data(), n_state, ref.data(),
+                             n_state, nullptr);
+        std::vector<float> got((size_t)M * n_state);
+        HIP_OK(hipMemcpy(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost));
+        size_t bad = 0;
+        for (size_t i = 0; i < got.size(); i++)
+            if (!(std::fabs(got[i] - ref[i]) <= 2e-3 + 1e-2 * std::fabs(ref[i]))) bad++;
+        return bad == 0;
+    };
+    // self: M rows of q | k | v at p0 (prompt when M > 1), checked after the library wrote the cache
+    auto self_rows = [&](int p0, int M) {
+        std::vector<float> rows((size_t)M * rw);
+        for (auto & x : rows) x = rng.normal();
+        HIP_OK(hipMemcpy(dq, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+        Status s = M == 1 ? w->self_attention(0, dq, dout, p0) : w->self_attention_prompt(0, dq, dout, p0, M);
+        HIP_OK(hipDeviceSynchronize());
+        EXPECT(s.is_ok());
+        std::vector<uint16_t> qh((size_t)M * n_state);
+        bool cache_ok = true;
+        std::vector<uint16_t> gk((size_t)M * n_state), gv((size_t)M * n_state);
+        HIP_OK(hipMemcpy(gk.data(), sk.p + (size_t)p0 * n_state, gk.size() * 2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(gv.data(), sv.p + (size_t)p0 * n_state, gv.size() * 2, hipMemcpyDeviceToHost));
+        for (int t = 0; t < M; t++)
+            for (int i = 0; i < n_state; i++) {
+                const float * row = rows.data() + (size_t)t * rw;
+                qh[(size_t)t * n_state + i] = to_half(row[i]);
+                cache_ok = cache_ok && gk[(size_t)t * n_state + i] == to_half(row[n_state + i]) &&
+                           gv[(size_t)t * n_state + i] == to_half(row[2 * n_state + i]);
+                SK[(size_t)(p0 + t) * n_state + i] = to_half(row[n_state + i]);
+                SV[(size_t)(p0 + t) * n_state + i] = to_half(row[2 * n_state + i]);
+            }
+        EXPECT(cache_ok);
+        EXPECT(compare(qh, M, SK, SV, p0 + M, p0, 1));
+    };
+    self_rows(0, 5);
+    for (int p = 5; p < 9; p++) self_rows(p, 1);
+    for (int M : {1, 5}) {  // cross: greedy and 5 beams over the shared encoder cache
+        std::vector<float> q((size_t)M * n_state);
+        for (auto & x : q) x = rng.normal();
+        HIP_OK(hipMemcpy(dq, q.data(), q.size() * 4, hipMemcpyHostToDevice));
+        Status s = w->cross_attention(0, dq, dout, M);
+        HIP_OK(hipDeviceSynchronize());
+        EXPECT(s.is_ok());
+        std::vector<uint16_t> qh(q.size());
+        for (size_t i = 0; i < q.size(); i++) qh[i] = to_half(q[i]);
+        EXPECT(compare(qh, M, CK, CV, n_audio, 0, 0));
+    }
+    EXPECT(w->self_attention(0, dq, dout, n_text).code == Code::ResourceExhausted);
+    (void)hipFree(dq);
+    (void)hipFree(dout);
 }
 
 int main() {

@@ -176,3 +176,49 @@ def test_decode_matches_prefill_kernel(device):
     b = do[0].cpu().numpy().astype(np.float64)
     assert np.abs(a - b).max() <= 2e-3
     assert np.abs(pl[L - 1].cpu().numpy() - dl[0].cpu().numpy()).max() <= 1e-3
+
+
+# ---- mx_attn_decode_f32: the reference's f32 query rows and f32 output (query rounded to half in the kernel) ----
+
+def run_decode_f32(device, seed, n_head, n_head_kv, hd, kv_lens, n_q=1, causal=False, shared_cache=False,
+                   check_heads=None):
+    rng = np.random.default_rng(seed)
+    batch = len(kv_lens)
+    kvw = n_head_kv * hd
+    q = rng.standard_normal((batch * n_q, n_head * hd), dtype=np.float32)
+    caches = []
+    for b in range(batch):
+        if shared_cache and b > 0:
+            caches.append(caches[0])
+            continue
+        caches.append((normal_f16(rng, (kv_lens[b], kvw)), normal_f16(rng, (kv_lens[b], kvw))))
+    scale = 1.0 / np.sqrt(hd)
+    out, lse = A.decode(torch.from_numpy(q).to(device), [torch.from_numpy(k).to(device) for k, _ in caches],
+                        [torch.from_numpy(v).to(device) for _, v in caches], list(kv_lens), n_head=n_head,
+                        n_head_kv=n_head_kv, head_dim=hd, n_q=n_q, causal=causal, want_lse=True)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    out = out.cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy()
+    qh = q.astype(np.float16)
+    heads = np.arange(n_head) if check_heads is None else np.asarray(check_heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    for b in range(batch):
+        k, v = caches[b]
+        L = kv_lens[b]
+        ro, rl = ref_attention(qh[b * n_q:(b + 1) * n_q], k, v, n_head, n_head_kv, hd, scale, p0=L - n_q,
+                               causal=causal, heads=check_heads)
+        assert_close(out[b * n_q:(b + 1) * n_q][:, cols], ro, hd, f"f32 seq {b} L={L}",
+                     lse[b * n_q:(b + 1) * n_q][:, heads], rl)
+
+
+def test_f32_whisper_cross_beam5(device):
+    run_decode_f32(device, 41, 20, 20, 64, [1500], n_q=5)
+
+
+def test_f32_whisper_prompt_rows(device):
+    run_decode_f32(device, 42, 20, 20, 64, [9], n_q=4, causal=True)
+
+
+def test_f32_llama3_8b_batch3(device):
+    run_decode_f32(device, 43, 32, 8, 128, [1, 700, 5000], check_heads=[0, 13, 31])
