@@ -21,7 +21,7 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
 
 # Every symbol include/mx_attn.h declares.
 EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_prefill_rope", "mx_attn_decode",
-           "mx_attn_decode_f32", "mx_attn_decode_rope",
+           "mx_attn_decode_f32", "mx_attn_decode_rope", "mx_linear", "mx_linear_workspace_bytes",
            "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init")
 
 ROPE_NORMAL = 0  # adjacent pairs (2i, 2i + 1): llama
@@ -42,6 +42,16 @@ class MxAttnDesc(ctypes.Structure):
 class MxAttnRope(ctypes.Structure):
     """mx_attn_rope (include/mx_attn.h)."""
     _fields_ = [("mode", ctypes.c_int32), ("base", ctypes.c_float)]
+
+
+class MxLinearDesc(ctypes.Structure):
+    """mx_linear_desc (include/mx_linear.h)."""
+    _fields_ = [("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("flags", ctypes.c_uint32),
+                ("x_stride", ctypes.c_int64), ("y_stride", ctypes.c_int64), ("eps", ctypes.c_float),
+                ("reserved", ctypes.c_int32)]
+
+
+LINEAR_RMS_NORM, LINEAR_ACCUMULATE, LINEAR_BIAS, LINEAR_OUT_F16 = 1, 2, 4, 8
 
 
 class MxAttnError(RuntimeError):
@@ -79,6 +89,11 @@ def lib() -> ctypes.CDLL:
         L.mx_attn_decode_rope.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.POINTER(MxAttnRope), ctypes.c_int32,
                                           ctypes.POINTER(ctypes.c_int32), P, ctypes.POINTER(P), ctypes.POINTER(P), P,
                                           P, P, ctypes.c_size_t, P]
+        L.mx_linear_workspace_bytes.restype = ctypes.c_size_t
+        L.mx_linear_workspace_bytes.argtypes = [ctypes.POINTER(MxLinearDesc)]
+        L.mx_linear.restype = ctypes.c_int32
+        L.mx_linear.argtypes = [ctypes.POINTER(MxLinearDesc), ctypes.c_int32, ctypes.POINTER(P), P, ctypes.POINTER(P),
+                                P, ctypes.POINTER(P), P, ctypes.c_size_t, P]
         L.mx_attn_decode_workspace_bytes.restype = ctypes.c_size_t
         L.mx_attn_decode_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.c_int32]
         L.mx_attn_decode_workspace_init.restype = ctypes.c_int32
@@ -156,3 +171,17 @@ def decode_workspace_init(ws: int, ws_bytes: int, stream: int) -> int:
 
 def decode_workspace_bytes(desc: MxAttnDesc, batch: int, max_kv_len: int) -> int:
     return lib().mx_attn_decode_workspace_bytes(ctypes.byref(desc), batch, max_kv_len)
+
+
+def linear_raw(desc: MxLinearDesc, w_ptrs, x: int, y_ptrs, gamma: int, bias_ptrs, ws: int, ws_bytes: int,
+               stream: int) -> int:
+    """mx_linear on raw device addresses (w_ptrs / y_ptrs / bias_ptrs: Python sequences, bias_ptrs may be None)."""
+    n = len(w_ptrs)
+    wp = (ctypes.c_void_p * n)(*w_ptrs)
+    yp = (ctypes.c_void_p * n)(*y_ptrs)
+    bp = None if bias_ptrs is None else (ctypes.c_void_p * n)(*[b or None for b in bias_ptrs])
+    return lib().mx_linear(ctypes.byref(desc), n, wp, x, yp, gamma or None, bp, ws or None, ws_bytes, stream or None)
+
+
+def linear_workspace_bytes(desc: MxLinearDesc) -> int:
+    return lib().mx_linear_workspace_bytes(ctypes.byref(desc))

@@ -144,3 +144,41 @@ def prefill_rope(qkv, k_cache, v_cache, *, n_head, n_head_kv, head_dim, rope_mod
                                      v_cache.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else 0,
                                      _stream()))
     return out, lse
+
+
+def linear(x, weights, *, out=None, gamma=None, bias=None, eps=1e-5, accumulate=False, out_f16=False):
+    """mx_linear: x f32 [M][>= K]; weights: one f16 [N][K] tensor or a list of them (same shape, one launch);
+    out: matching output tensor(s) (f32, or f16 with out_f16), created if None; gamma f32 [K] turns on the RMS norm;
+    bias: f32 [N] tensor or list (None entries allowed). Returns the output tensor or list."""
+    single = isinstance(weights, torch.Tensor)
+    ws_list = [weights] if single else list(weights)
+    _rows(x, "x", torch.float32)
+    N, K = ws_list[0].shape
+    for w in ws_list:
+        _rows(w, "weight")
+        if tuple(w.shape) != (N, K) or w.stride(0) != K:
+            raise ValueError("weights must be contiguous [N][K] tensors of one shape")
+    odt = torch.float16 if out_f16 else torch.float32
+    if out is None:
+        outs = [torch.empty(x.shape[0], N, dtype=odt, device=x.device) for _ in ws_list]
+    else:
+        outs = [out] if single else list(out)
+    for o in outs:
+        _rows(o, "out", odt)
+    if len({o.stride(0) for o in outs}) != 1:
+        raise ValueError("outputs must share one row stride")
+    bl = None
+    if bias is not None:
+        bl = [bias] if isinstance(bias, torch.Tensor) else list(bias)
+    flags = ((_lib.LINEAR_RMS_NORM if gamma is not None else 0) | (_lib.LINEAR_ACCUMULATE if accumulate else 0) |
+             (_lib.LINEAR_BIAS if bl is not None else 0) | (_lib.LINEAR_OUT_F16 if out_f16 else 0))
+    d = _lib.MxLinearDesc(M=x.shape[0], N=N, K=K, flags=flags, x_stride=x.stride(0), y_stride=outs[0].stride(0),
+                          eps=eps, reserved=0)
+    need = _lib.linear_workspace_bytes(d)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device) if need else None
+    _lib.check(_lib.linear_raw(d, [w.data_ptr() for w in ws_list], x.data_ptr(), [o.data_ptr() for o in outs],
+                               gamma.data_ptr() if gamma is not None else 0,
+                               None if bl is None else [b.data_ptr() if b is not None else 0 for b in bl],
+                               ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
+                               _stream()))
+    return outs[0] if single else outs

@@ -4,6 +4,7 @@
 // dooms_code's numbering, never an abort, and a thread-local message for the last failure. Every check runs on the host
 // before anything is enqueued, so a rejected call leaves the stream untouched.
 #include "mx_attn.h"
+#include "mx_linear.h"
 
 #include <hip/hip_runtime.h>
 
@@ -113,6 +114,12 @@ size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len
 }  // namespace
 
 namespace {
+
+// Row scales of the GEMM path's RMS norm: M floats, 256-byte rounded.
+size_t linear_ws_bytes(const mx_linear_desc & d) {
+    if (!(d.flags & MX_LINEAR_RMS_NORM) || d.M <= mx::kLinearGemvMaxRows) return 0;
+    return ((size_t)d.M * sizeof(float) + 255) / 256 * 256;
+}
 
 // Rotary frequencies base^(-2i / head_dim) in f32 (rotate_pair, llama_kernels.h:513-518), computed once per call
 // on the host with the C library's powf; 0 past head_dim / 2 or without rotation.
@@ -358,6 +365,60 @@ MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn
                 return fail(MX_ATTN_INVALID_ARGUMENT, "sequences %d and %d share a cache: each sequence appends to its own", c, b);
     return decode_impl(desc, batch, kv_len, qkv, reinterpret_cast<const void * const *>(k_caches),
                        reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, rope, true);
+}
+
+MX_ATTN_API size_t mx_linear_workspace_bytes(const mx_linear_desc * desc) {
+    if (!desc) {
+        fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
+        return 0;
+    }
+    return linear_ws_bytes(*desc);
+}
+
+MX_ATTN_API int32_t mx_linear(const mx_linear_desc * desc, int32_t count, const uint16_t * const * W, const float * X,
+                              void * const * Y, const float * gamma, const float * const * bias, void * workspace,
+                              size_t ws_bytes, mx_attn_stream stream) {
+    if (!desc) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
+    const mx_linear_desc & d = *desc;
+    if (d.reserved != 0) return fail(MX_ATTN_INVALID_ARGUMENT, "desc->reserved must be 0");
+    if (d.M < 0 || d.N < 1 || d.K < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "need M >= 0, N >= 1, K >= 1 (M %d, N %d, K %d)", d.M, d.N, d.K);
+    if (d.K % 32) return fail(MX_ATTN_UNSUPPORTED, "K (%d) must be a multiple of 32", d.K);
+    if (d.flags & ~15u) return fail(MX_ATTN_INVALID_ARGUMENT, "unknown flags 0x%x", d.flags);
+    const bool out16 = d.flags & MX_LINEAR_OUT_F16;
+    if (d.x_stride < d.K || d.x_stride % 4) return fail(MX_ATTN_INVALID_ARGUMENT, "x_stride (%lld) must be >= K and a multiple of 4", (long long)d.x_stride);
+    if (d.y_stride < d.N || d.y_stride % (out16 ? 8 : 4))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "y_stride (%lld) must be >= N and a multiple of %d", (long long)d.y_stride, out16 ? 8 : 4);
+    if ((d.flags & MX_LINEAR_RMS_NORM) && !(std::isfinite(d.eps) && d.eps >= 0.f)) return fail(MX_ATTN_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    if (count < 1 || count > mx::kLinearMaxMats) return fail(MX_ATTN_INVALID_ARGUMENT, "count (%d) must be in [1, %d]", count, mx::kLinearMaxMats);
+    if (d.M == 0) return MX_ATTN_OK;
+    if (!W || !Y || !X) return fail(MX_ATTN_INVALID_ARGUMENT, "W, X and Y must not be null");
+    if (!aligned16(X)) return fail(MX_ATTN_INVALID_ARGUMENT, "X must be 16-byte aligned");
+    if ((d.flags & MX_LINEAR_RMS_NORM) && (!gamma || !aligned16(gamma))) return fail(MX_ATTN_INVALID_ARGUMENT, "gamma must be a 16-byte aligned pointer with MX_LINEAR_RMS_NORM");
+    if ((d.flags & MX_LINEAR_BIAS) && !bias) return fail(MX_ATTN_INVALID_ARGUMENT, "bias is null with MX_LINEAR_BIAS");
+    mx::LinearParams p;
+    for (int32_t i = 0; i < count; i++) {
+        if (!W[i] || !Y[i]) return fail(MX_ATTN_INVALID_ARGUMENT, "W[%d] or Y[%d] is null", i, i);
+        if (!aligned16(W[i]) || !aligned16(Y[i])) return fail(MX_ATTN_INVALID_ARGUMENT, "W[%d] and Y[%d] must be 16-byte aligned", i, i);
+        p.w[i] = reinterpret_cast<const mx::half_t *>(W[i]);
+        p.y[i] = Y[i];
+        p.bias[i] = (d.flags & MX_LINEAR_BIAS) ? bias[i] : nullptr;
+    }
+    const size_t need = linear_ws_bytes(d);
+    if (need && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u)))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "a 256-byte aligned workspace of %zu bytes is needed", need);
+    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+    p.x = X;
+    p.gamma = gamma;
+    p.scale = static_cast<float *>(workspace);
+    p.x_stride = d.x_stride;
+    p.y_stride = d.y_stride;
+    p.M = d.M;
+    p.N = d.N;
+    p.K = d.K;
+    p.count = count;
+    p.flags = d.flags;
+    p.eps = d.eps;
+    return hip_status(mx::launch_linear(p, static_cast<hipStream_t>(stream)), "linear launch");
 }
 
 }  // extern "C"

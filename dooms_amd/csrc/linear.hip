@@ -1,0 +1,322 @@
+// Projections over f16 weights: Y = X W^T (+ bias), optionally RMS-normalized input, accumulate, f16 output.
+//
+// Reference behaviour (dooms.cpp 0.6.1, src/backend/metal/llama_kernels.h):
+//   * matvec1 (96-126) / matvecm (809-842), one to eight tokens: f32 input rows, y = (W . (x * gamma)) * scale + bias,
+//     scale = 1 / sqrt(sum x^2 / K + eps) reduced over the row (stage_input, 62-80);
+//   * matmul / matmul_big (222-255, 418-450), prompt chunks: the input tile staged as half(x * gamma * scale) with the
+//     row scale from rms_scale (312-328), half x half products accumulated in f32, then + bias, or added into y.
+//   * the Whisper cross-attention cache: matmul_big into an f32 scratch, then to_half (metal_whisper_decoder.mm:295-316);
+//     here the GEMM rounds to half in its epilogue and writes the cache row directly.
+//
+// MI355X design:
+//   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). A workgroup of 4 waves
+//     stages the (normalized) input rows in LDS once; each wave owns 4 weight rows and streams them in 16-byte loads,
+//     two iterations of 4 loads in flight per lane; the dot products stay f32 and are reduced across the wave at the end.
+//   * M > 8 (prompt): gemm_kernel, v_mfma_f32_32x32x16_f16 on 128 x 128 output tiles, K in steps of 32 through LDS
+//     (double buffer, rows padded to 40 halves so that the 16-byte operand reads of 16 consecutive rows hit 16 distinct
+//     4-bank groups), the next step's global loads in flight during the current step's products. Each wave owns a
+//     64 x 64 block (2 x 2 MFMA tiles). The input is converted to half (after the RMS scale) while it is staged.
+//   * Several matrices with the same input and shape (the cross cache's K and V of every layer) run in one launch.
+#include <algorithm>
+
+#include "mx_common.hpp"
+#include "mx_kernels.hpp"
+
+namespace mx {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// ---- RMS scale of each input row (rms_scale, llama_kernels.h:312-328): one workgroup per row ----
+__global__ __launch_bounds__(kThreads) void rms_scale_kernel(LinearParams p) {
+    __shared__ float red[kWaves];
+    const float * row = p.x + (int64_t)blockIdx.x * p.x_stride;
+    float ss = 0.f;
+    for (int k = threadIdx.x * 4; k < p.K; k += kThreads * 4) {
+        const float4_t v = *reinterpret_cast<const float4_t *>(row + k);
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += shfl_xor(ss, o);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) t += red[w];
+        p.scale[blockIdx.x] = 1.f / __builtin_sqrtf(t / (float)p.K + p.eps);
+    }
+}
+
+// y (+)= v (+ bias) into row m, column n of output matrix mi.
+template <bool OUT16>
+__device__ __forceinline__ void store_y(const LinearParams & p, int mi, int m, int n, float v) {
+    if (p.flags & kLinearBias) {
+        const float * b = p.bias[mi];
+        if (b) v += b[n];
+    }
+    const int64_t o = (int64_t)m * p.y_stride + n;
+    if constexpr (OUT16) {
+        half_t * y = static_cast<half_t *>(p.y[mi]);
+        if (p.flags & kLinearAccumulate) v += (float)y[o];
+        y[o] = (half_t)v;
+    } else {
+        float * y = static_cast<float *>(p.y[mi]);
+        if (p.flags & kLinearAccumulate) v += y[o];
+        y[o] = v;
+    }
+}
+
+// ---- M <= 8: f32 input rows in LDS, 4 weight rows per wave ----
+constexpr int kGemvRows = 4;  // weight rows per wave
+
+// STAGE: the input rows (times gamma) fit the LDS budget and are staged once; otherwise every wave reads them from
+// L2 as it goes (the reference's kStageInput = false variant, metal_llama_decoder.mm:45-47).
+template <int MT, bool STAGE, bool OUT16>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(LinearParams p) {
+    extern __shared__ float xs[];  // [MT][K]: x (* gamma) of each input row, when staged
+    __shared__ float red[MT][kWaves];
+    __shared__ float s_scale[MT];
+    const int K = p.K, M = p.M;
+    const bool norm = p.flags & kLinearNorm;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+
+    // stage the rows and, with the norm, reduce their sums of squares (stage_input, llama_kernels.h:62-80)
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        float ss = 0.f;
+        if (m < M) {
+            const float * xr = p.x + (int64_t)m * p.x_stride;
+            for (int k = threadIdx.x * 4; k < K; k += kThreads * 4) {
+                float4_t v = *reinterpret_cast<const float4_t *>(xr + k);
+                ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+                if constexpr (STAGE) {
+                    if (norm) v = v * *reinterpret_cast<const float4_t *>(p.gamma + k);
+                    *reinterpret_cast<float4_t *>(xs + m * K + k) = v;
+                }
+            }
+        }
+        if (norm) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += shfl_xor(ss, o);
+            if (lane == 0) red[m][wave] = ss;
+        }
+    }
+    __syncthreads();
+    if (norm && threadIdx.x < MT) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) t += red[threadIdx.x][w];
+        s_scale[threadIdx.x] = 1.f / __builtin_sqrtf(t / (float)K + p.eps);
+    }
+    __syncthreads();
+
+    // work item: (matrix, group of 4 rows) per wave
+    const int groups = (p.N + kGemvRows - 1) / kGemvRows;
+    const int item = blockIdx.x * kWaves + wave;
+    if (item >= groups * p.count) return;  // after the last barrier
+    const int mi = item / groups;
+    const int r0 = (item % groups) * kGemvRows;
+    const half_t * w = p.w[mi];
+    const half_t * wr[kGemvRows];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; i++) wr[i] = w + (int64_t)min(r0 + i, p.N - 1) * K;
+
+    float acc[kGemvRows][MT];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; i++)
+#pragma unroll
+        for (int m = 0; m < MT; m++) acc[i][m] = 0.f;
+    const int C8 = K / 8;  // 16-byte chunks per row
+#pragma unroll 2
+    for (int c = lane; c < C8; c += kWave) {
+        half8_t wv[kGemvRows];
+#pragma unroll
+        for (int i = 0; i < kGemvRows; i++) wv[i] = as_half8(load16(wr[i] + 8 * c));
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            float4_t x0, x1;
+            if constexpr (STAGE) {
+                x0 = *reinterpret_cast<const float4_t *>(xs + m * K + 8 * c);
+                x1 = *reinterpret_cast<const float4_t *>(xs + m * K + 8 * c + 4);
+            } else {
+                const float * xr = p.x + (int64_t)min(m, M - 1) * p.x_stride + 8 * c;
+                x0 = *reinterpret_cast<const float4_t *>(xr);
+                x1 = *reinterpret_cast<const float4_t *>(xr + 4);
+                if (norm) {
+                    x0 = x0 * *reinterpret_cast<const float4_t *>(p.gamma + 8 * c);
+                    x1 = x1 * *reinterpret_cast<const float4_t *>(p.gamma + 8 * c + 4);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kGemvRows; i++) {
+                float a = acc[i][m];
+#pragma unroll
+                for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[i][e], x0[e], a);
+#pragma unroll
+                for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[i][4 + e], x1[e], a);
+                acc[i][m] = a;
+            }
+        }
+    }
+    // reduce over the wave; lane i * MT + m stores (row r0 + i, input row m)
+    float mine = 0.f;
+#pragma unroll
+    for (int i = 0; i < kGemvRows; i++)
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            float s = acc[i][m];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) s += shfl_xor(s, o);
+            if (lane == i * MT + m) mine = s;
+        }
+    if (lane < kGemvRows * MT) {
+        const int i = lane / MT, m = lane % MT, n = r0 + i;
+        if (m < M && n < p.N) store_y<OUT16>(p, mi, m, n, norm ? mine * s_scale[m] : mine);
+    }
+}
+
+// ---- M > 8: MFMA GEMM, 128 x 128 tiles ----
+constexpr int kTM = 128, kTN = 128, kTK = 32;
+constexpr int kPitch = kTK + 8;  // halves per staged row
+
+template <bool NORM, bool OUT16>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(LinearParams p) {
+    __shared__ half_t xs[2][kTM * kPitch];
+    __shared__ half_t ws[2][kTN * kPitch];
+    const int n_tiles = (p.N + kTN - 1) / kTN, m_tiles = (p.M + kTM - 1) / kTM;
+    // consecutive work items share a weight tile (different token tiles); contiguous ranges per XCD
+    const uint32_t t = xcd_remap(blockIdx.x, (uint32_t)(p.count * n_tiles * m_tiles));
+    const int mt = t % m_tiles, nt = (t / m_tiles) % n_tiles, mi = t / (m_tiles * n_tiles);
+    const int m0 = mt * kTM, n0 = nt * kTN;
+    const half_t * w = p.w[mi];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int l32 = lane % 32, hi = lane / 32;
+
+    // staging map: chunk c = threadIdx.x + 256 j (j = 0, 1) is row c / 4, columns 8 (c % 4) .. + 8 of the step
+    float xr[2][8];
+    u32x4 wr[2];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int c = threadIdx.x + kThreads * j, row = c / 4, kc = c % 4;
+            const int m = min(m0 + row, p.M - 1), n = min(n0 + row, p.N - 1);
+            load8f(p.x + (int64_t)m * p.x_stride + k0 + 8 * kc, xr[j]);
+            if constexpr (NORM) {
+                float g[8];
+                load8f(p.gamma + k0 + 8 * kc, g);
+                const float s = p.scale[m];
+#pragma unroll
+                for (int e = 0; e < 8; e++) xr[j][e] *= g[e] * s;  // x * (gamma * scale), as the reference's staging
+            }
+            wr[j] = load16(w + (int64_t)n * p.K + k0 + 8 * kc);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int c = threadIdx.x + kThreads * j, row = c / 4, kc = c % 4;
+            *reinterpret_cast<u32x4 *>(&xs[buf][row * kPitch + 8 * kc]) = to_half8(xr[j]);
+            *reinterpret_cast<u32x4 *>(&ws[buf][row * kPitch + 8 * kc]) = wr[j];
+        }
+    };
+
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+    const int wm = wave / 2, wn = wave % 2;  // this wave's 64 x 64 block
+    const int a_base = (64 * wm + l32) * kPitch + 8 * hi;
+    const int b_base = (64 * wn + l32) * kPitch + 8 * hi;
+    const int nk = p.K / kTK;
+    load(0);
+    store(0);
+    if (nk > 1) load(kTK);
+    for (int ib = 0; ib < nk; ib++) {
+        const int buf = ib & 1;
+        __syncthreads();  // step ib is in buffer buf; buffer buf ^ 1 is free
+        if (ib + 1 < nk) {
+            store(buf ^ 1);
+            if (ib + 2 < nk) load((ib + 2) * kTK);
+        }
+        const half_t * a_s = xs[buf];
+        const half_t * b_s = ws[buf];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            half8_t a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) a[i] = as_half8(*reinterpret_cast<const u32x4 *>(a_s + a_base + 32 * i * kPitch + 16 * ks));
+#pragma unroll
+            for (int j = 0; j < 2; j++) b[j] = as_half8(*reinterpret_cast<const u32x4 *>(b_s + b_base + 32 * j * kPitch + 16 * ks));
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = mfma32x32x16(a[i], b[j], acc[i][j]);
+        }
+    }
+
+    // lane holds Y[m0 + 64 wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + 64 wn + 32 j + l32]
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + 64 * wn + 32 * j + l32;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + 64 * wm + 32 * i + 8 * (v / 4) + 4 * hi + v % 4;
+                if (m < p.M) store_y<OUT16>(p, mi, m, n, acc[i][j][v]);
+            }
+        }
+}
+
+template <int MT>
+hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
+    const int groups = (p.N + kGemvRows - 1) / kGemvRows;
+    const dim3 grid((uint32_t)((groups * p.count + kWaves - 1) / kWaves));
+    const size_t lds = (size_t)MT * p.K * sizeof(float);
+    const bool out16 = p.flags & kLinearOutF16;
+    if (lds <= kLinearGemvLds) {
+        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, true, true>), grid, dim3(kThreads), lds, stream, p);
+        else hipLaunchKernelGGL((gemv_kernel<MT, true, false>), grid, dim3(kThreads), lds, stream, p);
+    } else {
+        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, false, true>), grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((gemv_kernel<MT, false, false>), grid, dim3(kThreads), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
+    if (p.M <= kLinearGemvMaxRows) {
+        if (p.M <= 1) return launch_gemv_t<1>(p, stream);
+        if (p.M <= 2) return launch_gemv_t<2>(p, stream);
+        if (p.M <= 4) return launch_gemv_t<4>(p, stream);
+        return launch_gemv_t<8>(p, stream);
+    }
+    const bool norm = p.flags & kLinearNorm;
+    if (norm) {
+        hipLaunchKernelGGL(rms_scale_kernel, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
+    const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);
+    const bool out16 = p.flags & kLinearOutF16;
+    const dim3 grid((uint32_t)tiles);
+    if (norm) {
+        if (out16) hipLaunchKernelGGL((gemm_kernel<true, true>), grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((gemm_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        if (out16) hipLaunchKernelGGL((gemm_kernel<false, true>), grid, dim3(kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((gemm_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mx

@@ -73,12 +73,32 @@ struct RopeStoreParams {
     float rope_freq[kMaxHeadDim / 2];
 };
 
+// Projections (linear.hip): Y[i] = X W[i]^T for count matrices sharing X and the shape.
+constexpr uint32_t kLinearNorm = 1, kLinearAccumulate = 2, kLinearBias = 4, kLinearOutF16 = 8;
+constexpr int kLinearMaxMats = 64;
+constexpr int kLinearGemvMaxRows = 8;        // M up to this runs the f32-input GEMV, above it the MFMA GEMM
+constexpr size_t kLinearGemvLds = 64 * 1024;  // staged input rows up to this many bytes per workgroup
+
+struct LinearParams {
+    const float * x;
+    const float * gamma;
+    float * scale;  // [M] row RMS scales (GEMM with the norm): written by rms_scale_kernel, read by the GEMM
+    int64_t x_stride, y_stride;
+    int32_t M, N, K, count;
+    uint32_t flags;
+    float eps;
+    const half_t * w[kLinearMaxMats];
+    void * y[kLinearMaxMats];
+    const float * bias[kLinearMaxMats];
+};
+
 int decode_rows_per_tile(int rows);
 hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, hipStream_t stream);
 hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 
 int prefill_rows_per_workgroup(int n_q, int n_head);  // query rows one prefill workgroup covers
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
+hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
 
 }  // namespace mx

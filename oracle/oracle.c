@@ -36,6 +36,13 @@
  *    per-pair norm preservation, the relative-position property <R(m) q, R(n) k> = <R(m - n) q, k>, and neox = adjacent
  *    conjugated by the half/interleave permutation.
  *
+ * 4. oracle_linear_f64 — the projections around the attention (src/backend/metal/llama_kernels.h): matvec1 / matvecm
+ *    (96-126, 809-842: f32 input, y = (W . (x * gamma)) * scale + bias) and matmul / matmul_big with rms_scale (186-199,
+ *    312-328, 418-450: input staged as half(x * (gamma * scale)), half products summed) — selected by half_input —
+ *    summed here in double; scale = 1 / sqrt(mean(x^2) + eps) (the sum of squares in double, the scale rounded to
+ *    f32 as the kernels keep it). Pinned (tests/test_oracle.py) against numpy's float64 matmul of the same operands,
+ *    W = identity, W = 0 (bias only), the residual accumulate, and the closed-form scale of a constant row.
+ *
  * Layout (attention functions): q [n_q][q_stride], k/v [n_kv][kv_stride], out [n_q][out_stride], lse [n_q][n_head]; head h
  * at column h * head_dim. Inputs are IEEE binary16 bit patterns.
  */
@@ -70,6 +77,32 @@ static float f16_to_f32(uint16_t h) {
 
 void oracle_f16_to_f32(const uint16_t * src, float * dst, int64_t n) {
     for (int64_t i = 0; i < n; i++) dst[i] = f16_to_f32(src[i]);
+}
+
+/* IEEE binary32 -> binary16, round to nearest even (overflow to infinity). */
+static uint16_t f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u)); /* inf, nan */
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);                                   /* rounds past 65504 */
+    if (ax < 0x38800000u) { /* subnormal half (or zero): value = m * 2^-24 */
+        float a;
+        memcpy(&a, &ax, 4);
+        const float m = a * 16777216.0f; /* exact: scaling by a power of two */
+        const uint32_t r = (uint32_t)nearbyintf(m);  /* round half to even (default rounding mode) */
+        return (uint16_t)(sign | r);
+    }
+    const uint32_t e = ((ax >> 23) - 112u) << 10, man = ax & 0x7fffffu;
+    uint32_t h = e | (man >> 13);
+    const uint32_t rest = man & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+void oracle_f32_to_f16(const float * src, uint16_t * dst, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dst[i] = f32_to_f16(src[i]);
 }
 
 /* Last key visible to query row t, plus one. */
@@ -209,4 +242,43 @@ void oracle_rope_f32(int32_t mode, float base, int32_t head_dim, int32_t pos, co
             b[i1] = (float)((double)a[i0] * s + (double)a[i1] * c);
         }
     }
+}
+
+/* Y[m][n] (+)= sum_k a[m][k] W[n][k] (+ bias[n]) in double for m < M, n < N (Y dense [M][N]). flags: 1 RMS norm with
+ * gamma, 2 accumulate into Y, 4 bias. half_input: the matmul staging (a = half(x * (gamma * scale))), else the matvec
+ * form (a = x * gamma in f32, the sum times scale). */
+int oracle_linear_f64(int32_t M, int32_t N, int32_t K, uint32_t flags, int32_t half_input, float eps, const float * X,
+                      int64_t x_stride, const uint16_t * W, const float * gamma, const float * bias, double * Y) {
+    if (M < 0 || N < 1 || K < 1) return 1;
+    float * a = (float *)malloc(sizeof(float) * (size_t)K);
+    if (!a) return 2;
+    const int norm = (flags & 1u) != 0;
+    for (int64_t m = 0; m < M; m++) {
+        const float * x = X + m * x_stride;
+        float scale = 1.f;
+        if (norm) {
+            double ss = 0.0;
+            for (int32_t k = 0; k < K; k++) ss += (double)x[k] * (double)x[k];
+            scale = (float)(1.0 / sqrt(ss / (double)K + (double)eps));
+        }
+        for (int32_t k = 0; k < K; k++) {
+            if (half_input) {
+                const float v = norm ? x[k] * (gamma[k] * scale) : x[k];
+                a[k] = f16_to_f32(f32_to_f16(v));
+            } else {
+                a[k] = norm ? x[k] * gamma[k] : x[k];
+            }
+        }
+        for (int64_t n = 0; n < N; n++) {
+            const uint16_t * wr = W + n * K;
+            double s = 0.0;
+            for (int32_t k = 0; k < K; k++) s += (double)a[k] * (double)f16_to_f32(wr[k]);
+            if (norm && !half_input) s *= (double)scale;
+            if (flags & 4u) s += (double)bias[n];
+            double * y = Y + m * N + n;
+            *y = (flags & 2u) ? *y + s : s;
+        }
+    }
+    free(a);
+    return 0;
 }

@@ -31,6 +31,10 @@ def lib():
                                             P, i64, i32]
         L.oracle_f16_to_f32.restype = None
         L.oracle_f16_to_f32.argtypes = [P, P, i64]
+        L.oracle_f32_to_f16.restype = None
+        L.oracle_f32_to_f16.argtypes = [P, P, i64]
+        L.oracle_linear_f64.restype = ctypes.c_int
+        L.oracle_linear_f64.argtypes = [i32, i32, i32, ctypes.c_uint32, i32, ctypes.c_float, P, i64, P, P, P, P]
         L.oracle_rope_f32.restype = None
         L.oracle_rope_f32.argtypes = [i32, ctypes.c_float, i32, i32, P, P, i64]
         _lib = L
@@ -87,4 +91,28 @@ def rope_f32(x, mode, base, head_dim, pos):
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().oracle_rope_f32(mode, base, head_dim, pos, x.ctypes.data, y.ctypes.data, x.size // head_dim)
+    return y
+
+
+def f32_to_f16(a):
+    """Round-to-nearest-even binary32 -> binary16 (oracle_f32_to_f16), as float16 array."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16(a.ctypes.data, out.ctypes.data, a.size)
+    return out.view(np.float16)
+
+
+def linear_f64(x, w, flags=0, half_input=False, eps=1e-5, gamma=None, bias=None, y0=None):
+    """oracle_linear_f64: x f32 [M][>=K], w f16 [N][K]; returns Y float64 [M][N] (y0: the accumulate input)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float16)
+    M, N, K = x.shape[0], w.shape[0], w.shape[1]
+    y = np.zeros((M, N)) if y0 is None else np.array(y0, dtype=np.float64, order="C")
+    g = None if gamma is None else np.ascontiguousarray(gamma, dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = lib().oracle_linear_f64(M, N, K, flags, 1 if half_input else 0, eps, x.ctypes.data, x.shape[1],
+                                 w.ctypes.data, None if g is None else g.ctypes.data,
+                                 None if b is None else b.ctypes.data, y.ctypes.data)
+    if rc:
+        raise ValueError(f"oracle_linear_f64 failed ({rc})")
     return y

@@ -3,6 +3,7 @@ declares, the descriptor layout agrees between C and the binding, and every argu
 (the dooms_code numbering, include/dooms/dooms_c.h:24-33 in the reference) with a message, before anything touches a GPU.
 """
 import ctypes
+import glob
 import os
 import re
 import subprocess
@@ -17,9 +18,12 @@ HEADER = os.path.join(ROOT, "include", "mx_attn.h")
 A = 256  # a 256-byte aligned fake device address: never dereferenced, every call below fails its checks first
 
 
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+
+
 def declared():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"MX_ATTN_API\s+[\w\s\*]+?\b(mx_attn_\w+)\s*\(", text)))
+    text = "".join(open(h).read() for h in HEADERS)
+    return sorted(set(re.findall(r"MX_ATTN_API\s+[\w\s\*]+?\b(mx_\w+)\s*\(", text)))
 
 
 def exported():
@@ -195,3 +199,45 @@ def test_python_front_end_refuses_host_tensors():
     x = torch.zeros(4, 128, dtype=torch.float16)
     with pytest.raises(ValueError):
         attention.prefill(x, x, x, n_head=1, n_head_kv=1, head_dim=128)
+
+
+def test_linear_desc_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mx_linear.h"\n'
+                   'int main(void){printf("%zu %zu %zu %zu %zu\\n", sizeof(mx_linear_desc), offsetof(mx_linear_desc, flags),'
+                   ' offsetof(mx_linear_desc, x_stride), offsetof(mx_linear_desc, eps), offsetof(mx_linear_desc, reserved));'
+                   'return 0;}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    D = _lib.MxLinearDesc
+    assert got == [ctypes.sizeof(D), D.flags.offset, D.x_stride.offset, D.eps.offset, D.reserved.offset]
+
+
+def test_linear_checks():
+    def ld(**kw):
+        base = dict(M=4, N=64, K=128, flags=0, x_stride=128, y_stride=64, eps=1e-5, reserved=0)
+        base.update(kw)
+        return _lib.MxLinearDesc(**base)
+
+    def call(d, count=1, w=A, x=A, y=A, gamma=0, bias=None, ws=0, ws_bytes=0):
+        return _lib.linear_raw(d, [w] * count, x, [y] * count, gamma, bias, ws, ws_bytes, 0)
+
+    assert call(ld(K=100, x_stride=100)) == _lib.UNSUPPORTED and "multiple of 32" in _lib.last_error()
+    assert call(ld(reserved=1)) == _lib.INVALID_ARGUMENT
+    assert call(ld(flags=16)) == _lib.INVALID_ARGUMENT and "flags" in _lib.last_error()
+    assert call(ld(x_stride=64)) == _lib.INVALID_ARGUMENT and "x_stride" in _lib.last_error()
+    assert call(ld(y_stride=66)) == _lib.INVALID_ARGUMENT and "y_stride" in _lib.last_error()
+    assert call(ld(flags=8, y_stride=68)) == _lib.INVALID_ARGUMENT  # f16 rows need a multiple of 8
+    assert call(ld(), count=0) == _lib.INVALID_ARGUMENT and "count" in _lib.last_error()
+    assert call(ld(), count=65) == _lib.INVALID_ARGUMENT
+    assert call(ld(flags=1)) == _lib.INVALID_ARGUMENT and "gamma" in _lib.last_error()
+    assert call(ld(flags=4)) == _lib.INVALID_ARGUMENT and "bias" in _lib.last_error()
+    assert call(ld(), x=A + 4) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
+    # the GEMM path's RMS norm needs M floats of workspace
+    d = ld(M=100, flags=1)
+    assert _lib.linear_workspace_bytes(d) == 512 and _lib.linear_workspace_bytes(ld(M=8, flags=1)) == 0
+    assert call(d, gamma=A, ws=A, ws_bytes=256) == _lib.RESOURCE_EXHAUSTED
+    assert call(d, gamma=A, ws=A + 16, ws_bytes=512) == _lib.INVALID_ARGUMENT
+    assert call(ld(M=0), w=0, x=0, y=0) == _lib.OK

@@ -1,0 +1,141 @@
+"""Parity of mx_linear (the projections either side of the attention) with the oracle, through the C ABI.
+
+Replaces matvec1 / matvecm (llama_kernels.h:96-126, 809-842) for M <= 8 rows and matmul / matmul_big with rms_scale
+(llama_kernels.h:164-300, 309-450) for prompt chunks, and the Whisper cross-attention cache producer (matmul_big then
+to_half, metal_whisper_decoder.mm:295-316). Shapes are the decoders' own: Llama-3-8B / Qwen2.5 q|k|v and attn_output,
+Whisper large-v3-turbo (n_state 1280) prompt rows and the 1500-frame cross cache.
+
+Tolerance (f32 accumulation against the oracle's double sums of the same operands), per output element with
+S = sum_k |a_k w_k|: the f32-input path |y - ref| <= 1e-5 S + 1e-6; the half-operand path likewise when the inputs are
+not normalized (the GPU and the oracle round x to half identically) and 2^-10 S + 1e-6 with the RMS norm (the row
+scale may differ in its last f32 bit between the two reductions, which can move an operand to the neighbouring half);
+f16 outputs add half an ulp of the result.
+"""
+import numpy as np
+import pytest
+import torch
+
+from dooms_amd import attention as A
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def check(got, x, w, gamma, bias, eps, half_input, accumulate_from=None, out_f16=False, rows=None, what=""):
+    rows = np.arange(x.shape[0]) if rows is None else np.asarray(rows)
+    flags = (1 if gamma is not None else 0) | (4 if bias is not None else 0) | (2 if accumulate_from is not None else 0)
+    xs = x[rows]
+    y0 = None if accumulate_from is None else accumulate_from[rows].astype(np.float64)
+    ref = O.linear_f64(xs, w, flags=flags, half_input=half_input, eps=eps, gamma=gamma, bias=bias, y0=y0)
+    # S = sum_k |a_k w_k| with the oracle's operands (matvec form: x * gamma * scale)
+    if gamma is not None:
+        scale = 1 / np.sqrt((xs.astype(np.float64) ** 2).mean(axis=1) + eps)
+        a = np.abs(xs.astype(np.float64) * gamma[None, :] * scale[:, None])
+    else:
+        a = np.abs(xs.astype(np.float64))
+    S = a @ np.abs(w.astype(np.float64)).T
+    rel = (2.0 ** -10 if (half_input and gamma is not None) else 1e-5)
+    tol = rel * S + 1e-6
+    g = got[rows].astype(np.float64)
+    if out_f16:
+        tol = tol + np.abs(ref) * 2.0 ** -11 + 2.0 ** -25
+    err = np.abs(g - ref)
+    assert np.all(np.isfinite(g)), what
+    bad = err > tol
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} out of tolerance, max err {err.max():.3e}"
+
+
+def run(device, seed, M, N, K, norm=False, bias=False, accumulate=False, out_f16=False, count=1, rows=None,
+        x_pad=0, y_pad=0, eps=1e-5):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((M, K + x_pad), dtype=np.float32) * 2)
+    ws = [(rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float16) for _ in range(count)]
+    gamma = rng.uniform(0.2, 2.0, K).astype(np.float32) if norm else None
+    biases = [rng.standard_normal(N).astype(np.float32) for _ in range(count)] if bias else None
+    odt = np.float16 if out_f16 else np.float32
+    y0 = [rng.standard_normal((M, N + y_pad)).astype(odt) for _ in range(count)]
+    dx = torch.from_numpy(x).to(device)
+    dws = [torch.from_numpy(w).to(device) for w in ws]
+    douts = [torch.from_numpy(y.copy()).to(device) for y in y0]
+    outs = A.linear(dx[:, :K] if x_pad == 0 else dx, dws, out=[o[:, :N] for o in douts],
+                    gamma=None if gamma is None else torch.from_numpy(gamma).to(device),
+                    bias=None if biases is None else [torch.from_numpy(b).to(device) for b in biases],
+                    eps=eps, accumulate=accumulate, out_f16=out_f16)
+    torch.cuda.synchronize()
+    half_input = M > 8
+    for i in range(count):
+        got = douts[i].cpu().numpy()
+        check(got[:, :N], x[:, :K], ws[i], gamma, None if biases is None else biases[i], eps, half_input,
+              accumulate_from=y0[i][:, :N] if accumulate else None, out_f16=out_f16, rows=rows,
+              what=f"M={M} N={N} K={K} matrix {i}")
+        if y_pad:  # padding columns untouched
+            assert np.array_equal(got[:, N:], y0[i][:, N:])
+
+
+# ---- one token (matvec1): q|k|v with the RMS norm, attn_output into the residual ----
+def test_llama3_8b_qkv_decode(device):
+    run(device, 1, 1, 6144, 4096, norm=True)
+
+
+def test_qwen05b_qkv_decode_bias(device):
+    run(device, 2, 1, 1152, 896, norm=True, bias=True)
+
+
+def test_llama3_8b_attn_output_accumulate(device):
+    run(device, 3, 1, 4096, 4096, accumulate=True)
+
+
+# ---- up to 8 rows (matvecm): Whisper prompt rows, staged and unstaged input ----
+@pytest.mark.parametrize("M", [2, 3, 5, 8])
+def test_whisper_rows(device, M):
+    run(device, 10 + M, M, 1280, 1280, bias=True)
+
+
+def test_eight_rows_unstaged_input_with_norm(device):
+    run(device, 4, 8, 1024, 4096, norm=True, bias=True)  # 8 x 4096 f32 exceeds the 64 KB staging budget
+
+
+# ---- prompt chunks (matmul): the MFMA GEMM ----
+def test_qwen05b_prompt_qkv(device):
+    run(device, 5, 512, 1152, 896, norm=True, bias=True, rows=list(range(0, 512, 5)) + [511])
+
+
+def test_gemm_ragged_edges(device):
+    run(device, 6, 131, 200, 96, bias=True, accumulate=True)
+
+
+def test_gemm_llama3_attn_output_chunk(device):
+    run(device, 7, 300, 4096, 4096, accumulate=True, rows=[0, 1, 127, 128, 255, 299])
+
+
+def test_gemm_padded_strides(device):
+    run(device, 8, 40, 72, 64, norm=True, x_pad=12, y_pad=8)
+
+
+def test_gemv_padded_strides_f16(device):
+    run(device, 9, 3, 72, 64, norm=True, out_f16=True, x_pad=4, y_pad=8)
+
+
+# ---- the Whisper cross-attention cache: K and V of 4 layers in one launch, f16 rows ----
+def test_whisper_cross_kv_cache(device):
+    rng = np.random.default_rng(12)
+    A_, d, L = 1500, 1280, 4
+    x = rng.standard_normal((A_, d), dtype=np.float32)
+    ws = [(rng.standard_normal((d, d), dtype=np.float32) / np.sqrt(d)).astype(np.float16) for _ in range(2 * L)]
+    biases = [None if i % 2 == 0 else rng.standard_normal(d).astype(np.float32) for i in range(2 * L)]  # K: no bias
+    dev = lambda a: torch.from_numpy(a).to(device)
+    outs = A.linear(dev(x), [dev(w) for w in ws], bias=[None if b is None else dev(b) for b in biases],
+                    out_f16=True)
+    torch.cuda.synchronize()
+    rows = [0, 1, 63, 64, 127, 128, 700, 1407, 1408, 1499]
+    for i in range(2 * L):
+        got = outs[i].cpu().numpy()
+        assert got.dtype == np.float16
+        check(got, x, ws[i], None, biases[i], 1e-5, True, out_f16=True, rows=rows, what=f"cross matrix {i}")
+
+
+def test_linear_rejects_mismatched_shapes(device):
+    x = torch.zeros(2, 64, device=device)
+    with pytest.raises(ValueError):
+        A.linear(x, [torch.zeros(8, 64, dtype=torch.float16, device=device),
+                     torch.zeros(16, 64, dtype=torch.float16, device=device)])

@@ -247,3 +247,59 @@ def test_rope_neox_is_adjacent_under_the_half_interleave_permutation():
     a = O.rope_f32(x[:, perm], 0, 10000.0, hd, 1234)
     b = O.rope_f32(x, 1, 10000.0, hd, 1234)[:, perm]
     assert np.array_equal(a, b)
+
+
+# ---- binary16 rounding and the projections (oracle_f32_to_f16, oracle_linear_f64) ----
+
+def test_f32_to_f16_matches_numpy_round_to_nearest_even():
+    rng = np.random.default_rng(21)
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32) * np.float32(s) for s in (1e-6, 1e-3, 1, 300, 6e4)])
+    specials = np.array([0.0, -0.0, 65504, 65519.99, 65520, -65520, 1e9, np.inf, -np.inf, 2.0 ** -24, 2.0 ** -25,
+                         3 * 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 - 2.0 ** -25, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11],
+                        dtype=np.float32)
+    x = np.concatenate([x, specials])
+    np.testing.assert_array_equal(O.f32_to_f16(x).view(np.uint16), x.astype(np.float16).view(np.uint16))
+
+
+def _lin_inputs(rng, M, N, K):
+    x = rng.standard_normal((M, K), dtype=np.float32) * 3
+    w = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    return x, w, g, b
+
+
+@pytest.mark.parametrize("half_input", [False, True])
+def test_linear_matches_numpy(half_input):
+    rng = np.random.default_rng(22)
+    x, w, g, b = _lin_inputs(rng, 5, 40, 64)
+    eps = 1e-5
+    scale = (1 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1) + eps)).astype(np.float32)
+    if half_input:
+        a = (x * (g[None, :] * scale[:, None])).astype(np.float16).astype(np.float64)
+        ref = a @ w.astype(np.float64).T + b
+    else:
+        a = (x * g[None, :]).astype(np.float64)
+        ref = (a @ w.astype(np.float64).T) * scale[:, None].astype(np.float64) + b
+    got = O.linear_f64(x, w, flags=1 | 4, half_input=half_input, eps=eps, gamma=g, bias=b)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # plain product (no norm): half_input rounds x to half, the matvec form keeps it
+    got = O.linear_f64(x, w, half_input=half_input)
+    xa = x.astype(np.float16) if half_input else x
+    np.testing.assert_allclose(got, xa.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+
+
+def test_linear_closed_forms():
+    rng = np.random.default_rng(23)
+    K = 32
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    eye = np.eye(K, dtype=np.float16)
+    np.testing.assert_array_equal(O.linear_f64(x, eye), x.astype(np.float64))           # W = I: y = x
+    b = rng.standard_normal(K).astype(np.float32)
+    np.testing.assert_array_equal(O.linear_f64(x, np.zeros((K, K), np.float16), flags=4, bias=b),
+                                  np.broadcast_to(b.astype(np.float64), (3, K)))         # W = 0: y = bias
+    y0 = rng.standard_normal((3, K))
+    np.testing.assert_allclose(O.linear_f64(x, eye, flags=2, y0=y0), y0 + x, rtol=0, atol=1e-15)  # residual add
+    c = np.full((1, K), 2.5, np.float32)  # constant row: scale = 1 / sqrt(c^2 + eps), gamma = 1 -> y = c * scale
+    got = O.linear_f64(c, eye, flags=1, eps=1e-6, gamma=np.ones(K, np.float32))
+    np.testing.assert_allclose(got, np.float32(1 / np.sqrt(2.5 ** 2 + 1e-6)) * 2.5, rtol=1e-7)
