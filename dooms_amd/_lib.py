@@ -22,7 +22,8 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
 # Every symbol include/mx_attn.h declares.
 EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_prefill_rope", "mx_attn_decode",
            "mx_attn_decode_f32", "mx_attn_decode_rope", "mx_linear", "mx_linear_workspace_bytes",
-           "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init")
+           "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init", "mx_self_attention",
+           "mx_self_attention_workspace_bytes")
 
 ROPE_NORMAL = 0  # adjacent pairs (2i, 2i + 1): llama
 ROPE_NEOX = 1    # split halves (i, i + head_dim / 2): qwen2
@@ -50,6 +51,14 @@ class MxLinearDesc(ctypes.Structure):
                 ("x_stride", ctypes.c_int64), ("y_stride", ctypes.c_int64), ("eps", ctypes.c_float),
                 ("reserved", ctypes.c_int32)]
 
+
+class MxSelfAttnDesc(ctypes.Structure):
+    """mx_self_attn_desc (include/mx_attn.h)."""
+    _fields_ = [("batch", ctypes.c_int32), ("n_tok", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("embed", ctypes.c_int32), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float)]
+
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 LINEAR_RMS_NORM, LINEAR_ACCUMULATE, LINEAR_BIAS, LINEAR_OUT_F16 = 1, 2, 4, 8
 
@@ -98,6 +107,10 @@ def lib() -> ctypes.CDLL:
         L.mx_attn_decode_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.c_int32]
         L.mx_attn_decode_workspace_init.restype = ctypes.c_int32
         L.mx_attn_decode_workspace_init.argtypes = [P, ctypes.c_size_t, P]
+        L.mx_self_attention_workspace_bytes.restype = ctypes.c_size_t
+        L.mx_self_attention_workspace_bytes.argtypes = [ctypes.POINTER(MxSelfAttnDesc)]
+        L.mx_self_attention.restype = ctypes.c_int32
+        L.mx_self_attention.argtypes = [ctypes.POINTER(MxSelfAttnDesc), P, P, P, ctypes.c_size_t, P]
         _lib = L
     return _lib
 
@@ -185,3 +198,12 @@ def linear_raw(desc: MxLinearDesc, w_ptrs, x: int, y_ptrs, gamma: int, bias_ptrs
 
 def linear_workspace_bytes(desc: MxLinearDesc) -> int:
     return lib().mx_linear_workspace_bytes(ctypes.byref(desc))
+
+
+def self_attention_workspace_bytes(desc: MxSelfAttnDesc) -> int:
+    return lib().mx_self_attention_workspace_bytes(ctypes.byref(desc))
+
+
+def self_attention_raw(desc: MxSelfAttnDesc, qkv: int, y: int, ws: int, ws_bytes: int, stream: int) -> int:
+    """mx_self_attention on raw device addresses; returns the code."""
+    return lib().mx_self_attention(ctypes.byref(desc), qkv, y, ws or None, ws_bytes, stream or None)

@@ -182,3 +182,29 @@ def linear(x, weights, *, out=None, gamma=None, bias=None, eps=1e-5, accumulate=
                                ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
                                _stream()))
     return outs[0] if single else outs
+
+
+_SA_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def self_attention(qkv, *, heads, scale=None, out=None):
+    """mx_self_attention, the IR's SelfAttention op: qkv [B][N][3E] contiguous (f32, f16 or bf16) -> y [B][N][E] of the
+    same dtype. scale defaults to head_dim^-0.5. The workspace (if the shape needs one) comes from torch's allocator."""
+    if not qkv.is_cuda:
+        raise ValueError("qkv must be a device tensor")
+    if qkv.dim() != 3 or not qkv.is_contiguous() or qkv.dtype not in _SA_DTYPES:
+        raise ValueError("qkv must be a contiguous [B][N][3E] f32/f16/bf16 tensor")
+    B, N, E3 = qkv.shape
+    if E3 % 3:
+        raise ValueError("the last dimension of qkv must be a multiple of 3")
+    E = E3 // 3
+    if scale is None:
+        scale = (E // heads) ** -0.5 if heads >= 1 and E % heads == 0 else 1.0
+    d = _lib.MxSelfAttnDesc(batch=B, n_tok=N, heads=heads, embed=E, dtype=_SA_DTYPES[qkv.dtype], scale=scale)
+    if out is None:
+        out = torch.empty(B, N, E, dtype=qkv.dtype, device=qkv.device)
+    nbytes = _lib.self_attention_workspace_bytes(d)  # 0 also for an invalid descriptor, which the call reports
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=qkv.device) if nbytes else None
+    _lib.check(_lib.self_attention_raw(d, qkv.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else 0,
+                                       nbytes, _stream()))
+    return out

@@ -168,6 +168,7 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.qkv = static_cast<const float *>(q);
     p.out32 = static_cast<float *>(out);
     p.rope_mode = rope ? rope->mode : 2;
+    p.q_batch = p.kv_batch = p.out_batch = p.lse_batch = 0;
     fill_freq(p.rope_freq, rope, d.head_dim);
     if (rope) {  // the chunk's keys and values go into the caches first (stream order)
         mx::RopeStoreParams r;
@@ -293,9 +294,150 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     return MX_ATTN_OK;
 }
 
+// ---- IR SelfAttention (src/ir/op.h:31-32) ----
+
+int32_t check_self_attn(const mx_self_attn_desc * d) {
+    if (!d) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
+    if (d->batch < 1 || d->batch > 65535 || d->n_tok < 0)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be in [1, 65535] and n_tok (%d) >= 0", d->batch, d->n_tok);
+    if (d->heads < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "self_attention: heads must be >= 1, got %d", d->heads);
+    if (d->embed < 1 || d->embed % d->heads)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "self_attention: embedding %d is not divisible by %d heads", d->embed, d->heads);
+    if (d->dtype < MX_ATTN_F32 || d->dtype > MX_ATTN_BF16) return fail(MX_ATTN_INVALID_ARGUMENT, "dtype %d is not f32, f16 or bf16", d->dtype);
+    if (!std::isfinite(d->scale)) return fail(MX_ATTN_INVALID_ARGUMENT, "self_attention: scale must be finite");
+    if (d->embed / d->heads > mx::kMaxHeadDim)
+        return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is above %d", d->embed / d->heads, mx::kMaxHeadDim);
+    if ((int64_t)d->batch * d->n_tok * 3 * d->embed > ((int64_t)1 << 40)) return fail(MX_ATTN_INVALID_ARGUMENT, "qkv is too large");
+    return MX_ATTN_OK;
+}
+
+// How a descriptor runs: in place (f16, head_dim 64/128), with f16 keys/values copied (f32, head_dim 64/128), or padded.
+struct SelfAttnPlan {
+    int mode;       // 0 in place, 1 f16 copy of K/V, 2 padded operands
+    int hd, hdp;    // head_dim and the kernel's head_dim
+    size_t q_off, kv_off, o_off, bytes;  // workspace layout
+};
+
+SelfAttnPlan self_attn_plan(const mx_self_attn_desc & d) {
+    SelfAttnPlan s{};
+    s.hd = d.embed / d.heads;
+    const bool native = s.hd == 64 || s.hd == 128;
+    s.mode = native && d.dtype == MX_ATTN_F16 ? 0 : native && d.dtype == MX_ATTN_F32 ? 1 : 2;
+    s.hdp = s.hd <= 64 ? 64 : 128;
+    const int64_t rows = (int64_t)d.batch * d.n_tok;
+    auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+    if (s.mode == 1) {
+        s.kv_off = 0;
+        s.bytes = up((size_t)rows * 2 * d.embed * 2);
+    } else if (s.mode == 2) {
+        const size_t w = (size_t)rows * d.heads * s.hdp;
+        s.q_off = 0;
+        s.kv_off = up(w * 4);
+        s.o_off = s.kv_off + up(w * 2 * 2);
+        s.bytes = s.o_off + up(w * 4);
+    }
+    return s;
+}
+
 }  // namespace
 
 extern "C" {
+
+MX_ATTN_API size_t mx_self_attention_workspace_bytes(const mx_self_attn_desc * desc) {
+    if (check_self_attn(desc)) return 0;
+    return self_attn_plan(*desc).bytes;
+}
+
+MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void * qkv, void * y, void * workspace,
+                                      size_t ws_bytes, mx_attn_stream stream) {
+    if (int32_t rc = check_self_attn(desc)) return rc;
+    const mx_self_attn_desc & d = *desc;
+    if (d.n_tok == 0) return MX_ATTN_OK;
+    if (!qkv || !y) return fail(MX_ATTN_INVALID_ARGUMENT, "qkv and y must not be null");
+    if (!aligned16(qkv) || !aligned16(y)) return fail(MX_ATTN_INVALID_ARGUMENT, "qkv and y must be 16-byte aligned");
+    const SelfAttnPlan s = self_attn_plan(d);
+    const int64_t rows = (int64_t)d.batch * d.n_tok, E = d.embed;
+    const size_t esz = d.dtype == MX_ATTN_F32 ? 4 : 2;
+    {  // y must not overlap qkv
+        const char * a = static_cast<const char *>(qkv), * b = static_cast<const char *>(y);
+        if (a < b + (size_t)rows * E * esz && b < a + (size_t)rows * 3 * E * esz)
+            return fail(MX_ATTN_INVALID_ARGUMENT, "y overlaps qkv");
+    }
+    if (s.bytes > 0 && !workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null but %zu bytes are needed", s.bytes);
+    if (ws_bytes < s.bytes) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, s.bytes);
+    if (s.bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 255u)) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    char * ws = static_cast<char *>(workspace);
+
+    mx::PrefillParams p{};
+    p.n_head = p.n_head_kv = d.heads;
+    p.group = 1;
+    p.n_q = p.n_kv = d.n_tok;
+    p.p0 = 0;
+    p.causal = 0;
+    const int rpw = mx::prefill_rows_per_workgroup(d.n_tok, d.heads * d.batch);
+    p.n_qtiles = (d.n_tok + rpw - 1) / rpw;
+    p.scale_log2 = d.scale * 1.4426950408889634f;
+    p.rope_mode = 2;
+    p.lse = nullptr;
+    p.lse_batch = 0;
+    fill_freq(p.rope_freq, nullptr, s.hdp);
+    if (s.mode == 0) {  // the packed f16 rows in place: q at column 0, k at E, v at 2E of each 3E row
+        const mx::half_t * x = static_cast<const mx::half_t *>(qkv);
+        p.q = x;
+        p.k = x + E;
+        p.v = x + 2 * E;
+        p.out = static_cast<mx::half_t *>(y);
+        p.q_stride = p.kv_stride = 3 * E;
+        p.out_stride = E;
+        p.q_batch = p.kv_batch = (int64_t)d.n_tok * 3 * E;
+        p.out_batch = (int64_t)d.n_tok * E;
+        p.rope = 0;
+        return hip_status(mx::launch_prefill_batched(p, s.hd, d.batch, st), "self_attention launch");
+    }
+    mx::SelfAttnPackParams pk;
+    pk.qkv = qkv;
+    pk.q = s.mode == 2 ? reinterpret_cast<float *>(ws + s.q_off) : nullptr;
+    pk.kv = reinterpret_cast<mx::half_t *>(ws + s.kv_off);
+    pk.rows = rows;
+    pk.heads = d.heads;
+    pk.hd = s.hd;
+    pk.hdp = s.mode == 2 ? s.hdp : s.hd;
+    pk.dtype = d.dtype;
+    if (int32_t rc = hip_status(mx::launch_self_attn_pack(pk, st), "self_attention pack launch")) return rc;
+    const int64_t W = (int64_t)d.heads * pk.hdp;  // padded row width of one third
+    p.k = pk.kv;
+    p.v = pk.kv + W;
+    p.kv_stride = 2 * W;
+    p.kv_batch = (int64_t)d.n_tok * 2 * W;
+    p.rope = 1;  // f32 query rows (no rotation, rope_mode 2) and f32 output
+    if (s.mode == 1) {  // f32 query rows read in place, f32 output straight into y
+        p.qkv = static_cast<const float *>(qkv);
+        p.q_stride = 3 * E;
+        p.q_batch = (int64_t)d.n_tok * 3 * E;
+        p.out32 = static_cast<float *>(y);
+        p.out_stride = E;
+        p.out_batch = (int64_t)d.n_tok * E;
+        return hip_status(mx::launch_prefill_batched(p, s.hd, d.batch, st), "self_attention launch");
+    }
+    p.qkv = pk.q;
+    p.q_stride = W;
+    p.q_batch = (int64_t)d.n_tok * W;
+    float * o = reinterpret_cast<float *>(ws + s.o_off);
+    p.out32 = o;
+    p.out_stride = W;
+    p.out_batch = (int64_t)d.n_tok * W;
+    if (int32_t rc = hip_status(mx::launch_prefill_batched(p, s.hdp, d.batch, st), "self_attention launch")) return rc;
+    mx::SelfAttnUnpackParams u;
+    u.o = o;
+    u.y = y;
+    u.rows = rows;
+    u.heads = d.heads;
+    u.hd = s.hd;
+    u.hdp = s.hdp;
+    u.dtype = d.dtype;
+    return hip_status(mx::launch_self_attn_unpack(u, st), "self_attention unpack launch");
+}
 
 MX_ATTN_API int32_t mx_attn_abi_version(void) { return MX_ATTN_ABI_VERSION; }
 

@@ -59,7 +59,26 @@ struct PrefillParams {
     const float * qkv;
     float * out32;
     int32_t rope_mode;  // 0 adjacent pairs, 1 split halves (neox), 2 none
+    // independent problems along blockIdx.y (the IR self-attention's batch): elements between the q (or qkv), cache,
+    // output and lse blocks of consecutive problems; 0 for one problem
+    int64_t q_batch, kv_batch, out_batch, lse_batch;
     float rope_freq[kMaxHeadDim / 2];
+};
+
+// Packing of the IR self-attention's [B][N][3E] q|k|v rows (f32 or f16) into the attention kernel's operands when the
+// rows cannot be read in place: f32 query rows and f16 key|value rows with head_dim padded to hdp (zeros), and back.
+struct SelfAttnPackParams {
+    const void * qkv;     // [rows][3 E], of dtype (0 f32, 1 f16, 2 bf16)
+    float * q;            // [rows][H hdp] f32, or null (the query is read in place)
+    half_t * kv;          // [rows][2 H hdp] f16: keys at column 0, values at column H hdp
+    int64_t rows;         // B N
+    int32_t heads, hd, hdp, dtype;
+};
+struct SelfAttnUnpackParams {
+    const float * o;      // [rows][H hdp] f32
+    void * y;             // [rows][E], of dtype (0 f32, 1 f16, 2 bf16)
+    int64_t rows;
+    int32_t heads, hd, hdp, dtype;
 };
 
 // rope_store (llama_kernels.h:520-545) for the keys and values of n_rows new tokens: key head g of row t rotated for
@@ -100,5 +119,9 @@ int prefill_rows_per_workgroup(int n_q, int n_head);  // query rows one prefill 
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
+// n_batch problems of the prefill kernel along blockIdx.y, offsets from p.*_batch
+hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, hipStream_t stream);
+hipError_t launch_self_attn_pack(const SelfAttnPackParams & p, hipStream_t stream);
+hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t stream);
 
 }  // namespace mx

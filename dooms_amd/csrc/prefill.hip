@@ -73,6 +73,9 @@ void prefill_kernel(PrefillParams p) {
     const int qt = p.causal ? p.n_qtiles - 1 - qt_order : qt_order;
     const int h = kvh * G + gi;
     const int q0 = qt * kPrefillRows;
+    // problem blockIdx.y of a batch: its own query, cache, output and lse blocks
+    const int64_t bq = blockIdx.y * p.q_batch, bkv = blockIdx.y * p.kv_batch, bo = blockIdx.y * p.out_batch;
+    float * const lse_g = p.lse ? p.lse + blockIdx.y * p.lse_batch : nullptr;
 
     const int wave = threadIdx.x / kWave;  // wave-uniform, in a scalar register
     const int lane = threadIdx.x % kWave;
@@ -86,8 +89,8 @@ void prefill_kernel(PrefillParams p) {
     const int kend = p.causal ? min(p.n_kv, p.p0 + last_row + 1) : p.n_kv;
     const int nblk = (kend + kBK - 1) / kBK;
 
-    const half_t * kg = p.k + (int64_t)kvh * HD;
-    const half_t * vg = p.v + (int64_t)kvh * HD;
+    const half_t * kg = p.k + bkv + (int64_t)kvh * HD;
+    const half_t * vg = p.v + bkv + (int64_t)kvh * HD;
     // tile-load mapping, block b = i * W + wave of 16 rows x 4 chunks (64 contiguous bytes per row):
     //   K: row 16 (b % 4) + lane % 16, chunk 4 (b / 4) + lane / 16 (16 lanes of one LDS write phase: 16 rows, one chunk)
     //   V: row 16 (b % 4) + 4 (lane / 16) + (lane % 16) / 4, chunk 4 (b / 4) + lane % 4 (16 lanes: 4 rows x 4 chunks)
@@ -119,7 +122,7 @@ void prefill_kernel(PrefillParams p) {
     if constexpr (ROPE) {
         float x[KS][8] = {};
         if (qrow < p.n_q) {
-            const float * qp = p.qkv + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
+            const float * qp = p.qkv + bq + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(qp + 16 * ks, x[ks]);
             rope_rotate<KS, 16>(x, 8 * hgrp, p.rope_mode, [&](int i) {
@@ -131,7 +134,7 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(x[ks]));
     } else {
-        const half_t * qp = p.q + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
+        const half_t * qp = p.q + bq + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             u32x4 v = {0u, 0u, 0u, 0u};
@@ -287,15 +290,15 @@ void prefill_kernel(PrefillParams p) {
                     float4_t r;
 #pragma unroll
                     for (int e = 0; e < 4; e++) r[e] = o[dt][4 * gq + e] * inv;
-                    *reinterpret_cast<float4_t *>(p.out32 + off + 32 * dt + 8 * gq) = r;
+                    *reinterpret_cast<float4_t *>(p.out32 + bo + off + 32 * dt + 8 * gq) = r;
                 } else {
                     half4_t r;
 #pragma unroll
                     for (int e = 0; e < 4; e++) r[e] = (half_t)(o[dt][4 * gq + e] * inv);
-                    *reinterpret_cast<half4_t *>(p.out + off + 32 * dt + 8 * gq) = r;
+                    *reinterpret_cast<half4_t *>(p.out + bo + off + 32 * dt + 8 * gq) = r;
                 }
             }
-        if (p.lse && hgrp == 0) p.lse[(int64_t)qrow * p.n_head + h] = (m_run + log2_fast(l_run)) * kLn2;
+        if (lse_g && hgrp == 0) lse_g[(int64_t)qrow * p.n_head + h] = (m_run + log2_fast(l_run)) * kLn2;
     }
 }
 
@@ -312,30 +315,98 @@ int prefill_waves(int n_q, int n_head) {
 
 int prefill_rows_per_workgroup(int n_q, int n_head) { return 32 * prefill_waves(n_q, n_head); }
 
+// ---- the IR self-attention's operand packing (row f4): one thread per 8 consecutive padded head dims ----
+__global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams p) {
+    const int H = p.heads, hd = p.hd, hdp = p.hdp, E = H * hd;
+    const int64_t per_row = (int64_t)3 * H * (hdp / 8);  // 8-wide groups of q, k and v per row
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= p.rows * per_row) return;
+    const int64_t row = i / per_row;
+    int r = (int)(i % per_row);
+    const int part = r / (H * (hdp / 8));  // 0 q, 1 k, 2 v
+    r %= H * (hdp / 8);
+    const int h = r / (hdp / 8), d0 = 8 * (r % (hdp / 8));
+    if (part == 0 && !p.q) return;
+    float x[8];
+    const int64_t src = row * 3 * E + (int64_t)part * E + (int64_t)h * hd;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int d = d0 + e;
+        x[e] = 0.f;
+        if (d < hd) {
+            if (p.dtype == 1) x[e] = (float)static_cast<const half_t *>(p.qkv)[src + d];
+            else if (p.dtype == 2) x[e] = __uint_as_float((uint32_t)static_cast<const uint16_t *>(p.qkv)[src + d] << 16);
+            else x[e] = static_cast<const float *>(p.qkv)[src + d];
+        }
+    }
+    if (part == 0) {
+        float * dst = p.q + row * H * hdp + (int64_t)h * hdp + d0;
+        *reinterpret_cast<float4_t *>(dst) = float4_t{x[0], x[1], x[2], x[3]};
+        *reinterpret_cast<float4_t *>(dst + 4) = float4_t{x[4], x[5], x[6], x[7]};
+    } else {
+        *reinterpret_cast<u32x4 *>(p.kv + row * 2 * H * hdp + (int64_t)(part - 1) * H * hdp + (int64_t)h * hdp + d0) = to_half8(x);
+    }
+}
+
+__global__ __launch_bounds__(256) void self_attn_unpack_kernel(SelfAttnUnpackParams p) {
+    const int H = p.heads, hd = p.hd, E = H * hd;
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= p.rows * E) return;
+    const int64_t row = i / E;
+    const int c = (int)(i % E), h = c / hd, d = c % hd;
+    const float v = p.o[row * H * p.hdp + (int64_t)h * p.hdp + d];
+    if (p.dtype == 1) {
+        static_cast<half_t *>(p.y)[i] = (half_t)v;
+    } else if (p.dtype == 2) {  // bf16, round to nearest even; NaN stays a (quiet) NaN
+        const uint32_t b = __float_as_uint(v);
+        static_cast<uint16_t *>(p.y)[i] = v != v ? (uint16_t)0x7FC0u : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+    } else {
+        static_cast<float *>(p.y)[i] = v;
+    }
+}
+
+hipError_t launch_self_attn_pack(const SelfAttnPackParams & p, hipStream_t stream) {
+    const int64_t n = p.rows * 3 * p.heads * (p.hdp / 8);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(self_attn_pack_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t stream) {
+    const int64_t n = p.rows * p.heads * p.hd;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(self_attn_unpack_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
 template <int HD, bool POS, bool ROPE>
-void launch_prefill_r(const PrefillParams & p, int waves, hipStream_t stream) {
-    const dim3 grid((uint32_t)p.n_qtiles * p.n_head);
+void launch_prefill_r(const PrefillParams & p, int waves, int n_batch, hipStream_t stream) {
+    const dim3 grid((uint32_t)p.n_qtiles * p.n_head, (uint32_t)n_batch);
     if (waves == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE>), grid, dim3(8 * kWave), 0, stream, p);
     else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE>), grid, dim3(4 * kWave), 0, stream, p);
 }
 
 template <int HD, bool POS>
-void launch_prefill_t(const PrefillParams & p, int waves, hipStream_t stream) {
-    if (p.rope) launch_prefill_r<HD, POS, true>(p, waves, stream);
-    else launch_prefill_r<HD, POS, false>(p, waves, stream);
+void launch_prefill_t(const PrefillParams & p, int waves, int n_batch, hipStream_t stream) {
+    if (p.rope) launch_prefill_r<HD, POS, true>(p, waves, n_batch, stream);
+    else launch_prefill_r<HD, POS, false>(p, waves, n_batch, stream);
+}
+
+hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, hipStream_t stream) {
+    const bool pos = p.scale_log2 > 0.f;
+    const int waves = prefill_waves(p.n_q, p.n_head * n_batch);
+    if (head_dim == 64) {
+        if (pos) launch_prefill_t<64, true>(p, waves, n_batch, stream);
+        else launch_prefill_t<64, false>(p, waves, n_batch, stream);
+    } else {
+        if (pos) launch_prefill_t<128, true>(p, waves, n_batch, stream);
+        else launch_prefill_t<128, false>(p, waves, n_batch, stream);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream) {
-    const bool pos = p.scale_log2 > 0.f;
-    const int waves = prefill_waves(p.n_q, p.n_head);
-    if (head_dim == 64) {
-        if (pos) launch_prefill_t<64, true>(p, waves, stream);
-        else launch_prefill_t<64, false>(p, waves, stream);
-    } else {
-        if (pos) launch_prefill_t<128, true>(p, waves, stream);
-        else launch_prefill_t<128, false>(p, waves, stream);
-    }
-    return hipGetLastError();
+    return launch_prefill_batched(p, head_dim, 1, stream);
 }
 
 }  // namespace mx

@@ -17,6 +17,8 @@
  *   partial buffer split_part  metal_llama_decoder.mm:672-677                          mx_attn_decode_workspace_bytes
  *   dooms_last_error / dooms_code  include/dooms/dooms_c.h:24-36                       mx_attn_last_error / MX_ATTN_*
  *   AttnParams / SplitParams  llama_kernels.h:496-507, 844-854                         mx_attn_desc
+ *   IR SelfAttention (packed [B,N,3E], no mask)  src/ir/op.h:31-32, lowered at          mx_self_attention
+ *       src/backend/ggml/ggml_backend.cpp:398-412
  *
  * What the boundary takes over from the reference and what it leaves to the caller:
  *   - Q, K, V and the output are IEEE binary16 (passed as uint16_t bit patterns, so the header needs no half type);
@@ -203,6 +205,46 @@ MX_ATTN_API int32_t mx_attn_decode_workspace_init(void * workspace, size_t ws_by
  * invalid descriptor.
  */
 MX_ATTN_API size_t mx_attn_decode_workspace_bytes(const mx_attn_desc * desc, int32_t batch, int32_t max_kv_len);
+
+/* Element types of mx_self_attention's tensors: the order of the reference's DType (src/core/dtype.h:13). */
+#define MX_ATTN_F32 0
+#define MX_ATTN_F16 1
+#define MX_ATTN_BF16 2
+
+/*
+ * The IR's SelfAttention op (src/ir/op.h:31-32, 64-71): packed q|k|v rows [batch][n_tok][3 embed] -> [batch][n_tok][embed],
+ * per head softmax(scale * q k^T) v, no mask, head h the h-th run of head_dim = embed / heads values of each third.
+ */
+typedef struct mx_self_attn_desc {
+    int32_t batch;   /* B, 1 .. 65535 */
+    int32_t n_tok;   /* N >= 0 (0: nothing to do) */
+    int32_t heads;   /* >= 1 (self_attention_params, src/ir/op.cpp:69-76) */
+    int32_t embed;   /* E, a multiple of heads (infer_self_attention, src/ir/shape_infer.cpp:156-171); head_dim <= 128 */
+    int32_t dtype;   /* MX_ATTN_F32, MX_ATTN_F16 or MX_ATTN_BF16: of qkv and of y (the op keeps the input's dtype) */
+    float scale;     /* finite; multiplies q k^T before the softmax (0: uniform attention) */
+} mx_self_attn_desc;
+
+/*
+ * Device workspace bytes mx_self_attention needs: 0 for f16 input with head_dim 64 or 128 (the kernel reads the packed
+ * rows in place); for f32 input with head_dim 64 or 128 the keys and values as f16 (2 B N E halves; the reference's GPU
+ * path makes the same f16 copy, ggml_backend.cpp:332-335); for any other head_dim or bf16 the operands padded to
+ * head_dim 64 or 128. Returns 0 and sets the last error for an invalid descriptor.
+ */
+MX_ATTN_API size_t mx_self_attention_workspace_bytes(const mx_self_attn_desc * desc);
+
+/*
+ * SelfAttention on the GPU. Replaces the reference's lowering of the op (ggml_backend.cpp:398-412: the fused
+ * ggml_flash_attn_ext of lower_attention_fused, :325-340, the unfused chain of :342-356 for head dims flash attention does
+ * not take, and the CPU op attention_cpu_op, :292-312). One prefill-kernel launch (non-causal, every batch element along
+ * the grid) on the packed rows, plus a packing launch before and an unpacking launch after it when the head_dim or dtype
+ * needs them. Scores and accumulation are f32 over half operands (as the reference's GPU path, which rounds Q/K/V to half).
+ *
+ *   qkv        device, [batch][n_tok][3 embed] of desc->dtype, contiguous, 16-byte aligned
+ *   y          device, [batch][n_tok][embed] of desc->dtype, contiguous, 16-byte aligned, not overlapping qkv
+ *   workspace  device, 256-byte aligned, at least mx_self_attention_workspace_bytes(desc) bytes (NULL when that is 0)
+ */
+MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void * qkv, void * y, void * workspace,
+                                      size_t ws_bytes, mx_attn_stream stream);
 
 #ifdef __cplusplus
 }

@@ -116,3 +116,26 @@ def linear_f64(x, w, flags=0, half_input=False, eps=1e-5, gamma=None, bias=None,
     if rc:
         raise ValueError(f"oracle_linear_f64 failed ({rc})")
     return y
+
+
+def self_attention_f64(qkv, heads, scale):
+    """The IR SelfAttention op in f64 on packed rows qkv [B][N][3E] (any float dtype; f16 is exact in f64): per batch
+    element and head softmax(scale q k^T) v without a mask -- the reference's test oracle attention_ref
+    (tests/unit/test_backend_ggml.cpp:650-675): scores in double, max subtracted, exponentials normalized by their sum.
+    Returns y [B][N][E] f64."""
+    qkv = np.asarray(qkv)
+    B, N, E3 = qkv.shape
+    E = E3 // 3
+    hd = E // heads
+    y = np.zeros((B, N, E), np.float64)
+    for b in range(B):
+        x = qkv[b].astype(np.float64)
+        for h in range(heads):
+            q = x[:, h * hd:(h + 1) * hd]
+            k = x[:, E + h * hd:E + (h + 1) * hd]
+            v = x[:, 2 * E + h * hd:2 * E + (h + 1) * hd]
+            s = scale * (q @ k.T)
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            y[b, :, h * hd:(h + 1) * hd] = (p / p.sum(axis=1, keepdims=True)) @ v
+    return y

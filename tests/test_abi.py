@@ -241,3 +241,48 @@ def test_linear_checks():
     assert call(d, gamma=A, ws=A, ws_bytes=256) == _lib.RESOURCE_EXHAUSTED
     assert call(d, gamma=A, ws=A + 16, ws_bytes=512) == _lib.INVALID_ARGUMENT
     assert call(ld(M=0), w=0, x=0, y=0) == _lib.OK
+
+
+def test_self_attn_desc_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mx_attn.h"\n'
+                   'int main(void){printf("%zu %zu %zu\\n", sizeof(mx_self_attn_desc), offsetof(mx_self_attn_desc, dtype),'
+                   ' offsetof(mx_self_attn_desc, scale));return 0;}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    D = _lib.MxSelfAttnDesc
+    assert got == [ctypes.sizeof(D), D.dtype.offset, D.scale.offset]
+
+
+def test_self_attention_checks():
+    """Argument checks of mx_self_attention, with the reference's own messages where it has them
+    (self_attention_params, src/ir/op.cpp:69-76; infer_self_attention, src/ir/shape_infer.cpp:156-171)."""
+    def sd(**kw):
+        base = dict(batch=1, n_tok=210, heads=16, embed=1280, dtype=_lib.DTYPE_F32, scale=80 ** -0.5)
+        base.update(kw)
+        return _lib.MxSelfAttnDesc(**base)
+
+    def call(d, qkv=A, y=1 << 40, ws=A, ws_bytes=1 << 30):
+        return _lib.self_attention_raw(d, qkv, y, ws, ws_bytes, 0)
+
+    assert call(sd(heads=0)) == _lib.INVALID_ARGUMENT and "heads must be >= 1" in _lib.last_error()
+    assert call(sd(heads=3)) == _lib.INVALID_ARGUMENT and "not divisible by 3 heads" in _lib.last_error()
+    assert call(sd(scale=float("inf"))) == _lib.INVALID_ARGUMENT and "scale must be finite" in _lib.last_error()
+    assert call(sd(dtype=3)) == _lib.INVALID_ARGUMENT and "dtype" in _lib.last_error()
+    assert call(sd(batch=0)) == _lib.INVALID_ARGUMENT
+    assert call(sd(heads=4, embed=4 * 160)) == _lib.UNSUPPORTED and "head_dim 160" in _lib.last_error()
+    assert call(sd(), qkv=0) == _lib.INVALID_ARGUMENT and "null" in _lib.last_error()
+    assert call(sd(), qkv=A + 4) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
+    assert call(sd(), y=A) == _lib.INVALID_ARGUMENT and "overlaps" in _lib.last_error()
+    assert call(sd(n_tok=0), qkv=0, y=0) == _lib.OK
+    # workspace: none for f16 at head_dim 64/128, the f16 K/V copy for f32 there, padded operands otherwise
+    assert _lib.self_attention_workspace_bytes(sd(heads=20, dtype=_lib.DTYPE_F16)) == 0
+    assert _lib.self_attention_workspace_bytes(sd(heads=20)) == 210 * 2 * 1280 * 2
+    w = 210 * 16 * 128  # ViT-H: head_dim 80 padded to 128
+    assert _lib.self_attention_workspace_bytes(sd()) == w * 4 + w * 4 + w * 4
+    n = _lib.self_attention_workspace_bytes(sd())
+    assert call(sd(), ws_bytes=n - 1) == _lib.RESOURCE_EXHAUSTED
+    assert call(sd(), ws=0, ws_bytes=n) == _lib.INVALID_ARGUMENT
+    assert call(sd(), ws=A + 16, ws_bytes=n) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()

@@ -303,3 +303,40 @@ def test_linear_closed_forms():
     c = np.full((1, K), 2.5, np.float32)  # constant row: scale = 1 / sqrt(c^2 + eps), gamma = 1 -> y = c * scale
     got = O.linear_f64(c, eye, flags=1, eps=1e-6, gamma=np.ones(K, np.float32))
     np.testing.assert_allclose(got, np.float32(1 / np.sqrt(2.5 ** 2 + 1e-6)) * 2.5, rtol=1e-7)
+
+
+# ---- the IR SelfAttention oracle (packed [B, N, 3E] rows, no mask) ----
+
+@pytest.mark.parametrize("B,N,H,D", [(1, 5, 2, 4), (2, 7, 3, 8), (1, 1, 1, 16), (1, 17, 4, 64), (1, 9, 2, 6),
+                                     (1, 40, 4, 80)])
+def test_self_attention_oracle_matches_torch_and_the_c_oracle(B, N, H, D):
+    """The reference's own test shapes (kAttnCases, test_backend_ggml.cpp:679-681, ViT-H reduced to 40 tokens): the
+    numpy restatement against torch SDPA in float64 and against oracle_attention_f64 (C) on f16-representable inputs."""
+    rng = np.random.default_rng(700 + N)
+    E = H * D
+    qkv = rand_f16(rng, (B, N, 3 * E))
+    scale = D ** -0.5
+    y = O.self_attention_f64(qkv, H, scale)
+    x = torch.from_numpy(qkv.astype(np.float64))
+    q, k, v = (x[..., i * E:(i + 1) * E].reshape(B, N, H, D).transpose(1, 2) for i in range(3))
+    t = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale).transpose(1, 2).reshape(B, N, E)
+    np.testing.assert_allclose(y, t.numpy(), rtol=0, atol=1e-12)
+    for b in range(B):
+        o, _ = O.attention_f64(qkv[b, :, :E], np.ascontiguousarray(qkv[b, :, E:2 * E]),
+                               np.ascontiguousarray(qkv[b, :, 2 * E:]), H, H, D, scale, causal=False)
+        np.testing.assert_allclose(y[b], o, rtol=0, atol=1e-12)
+
+
+def test_self_attention_oracle_closed_forms():
+    """scale 0 -> every row is the mean of v over the tokens (test_backend_ggml.cpp:715-735); one token -> its v;
+    batch elements are independent (swapping them swaps the outputs)."""
+    rng = np.random.default_rng(710)
+    B, N, H, D = 2, 6, 2, 8
+    E = H * D
+    qkv = rng.standard_normal((B, N, 3 * E))
+    y = O.self_attention_f64(qkv, H, 0.0)
+    np.testing.assert_allclose(y, np.broadcast_to(qkv[:, :, 2 * E:].mean(axis=1, keepdims=True), y.shape), atol=1e-14)
+    one = O.self_attention_f64(qkv[:, :1], H, 0.7)
+    np.testing.assert_allclose(one[:, 0], qkv[:, 0, 2 * E:], atol=1e-14)
+    np.testing.assert_allclose(O.self_attention_f64(qkv[::-1], H, 0.3), O.self_attention_f64(qkv, H, 0.3)[::-1],
+                               atol=1e-14)
