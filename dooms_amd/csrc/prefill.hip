@@ -225,7 +225,10 @@ void prefill_kernel(PrefillParams p) {
                 }
         }
         bmax = fmaxf(bmax, shfl_xor(bmax, 32));
-        const float m_new = fmaxf(m_run, POS ? bmax * c : bmax);
+        // lazy rescale: the reference maximum moves only when the block's maximum exceeds it by more than 8 (base 2);
+        // the probabilities then stay below 2^8, well inside f16, and the O rescale below is rare
+        const float m_cand = fmaxf(m_run, POS ? bmax * c : bmax);
+        const float m_new = m_cand > m_run + 8.f ? m_cand : m_run;
         const bool none = m_new == kNegInf;       // no visible key yet in this row
         const float m_use = none ? 0.f : m_new;   // then every exponent below is 2^-inf = 0
         const float corr = none ? 1.f : exp2_fast(m_run - m_new);
@@ -301,6 +304,7 @@ void prefill_kernel(PrefillParams p) {
         if (lse_g && hgrp == 0) lse_g[(int64_t)qrow * p.n_head + h] = (m_run + log2_fast(l_run)) * kLn2;
     }
 }
+
 
 }  // namespace
 
