@@ -43,7 +43,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget per leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "all", "decode-headline", "prefill-headline"], default="all",
+    ap.add_argument("--only", choices=["decode", "prefill", "all", "decode-headline", "prefill-headline", "linear",
+                                       "self-attention"], default="all",
                     help="*-headline: only the headline workload of that path (for profiling one kernel)")
     return ap.parse_args()
 
@@ -178,6 +179,65 @@ class PrefillProblem:
         return sum(prefill_flops(M, p0, self.n_head, self.hd) for p0, M in self.chunks)
 
 
+class LinearProblem:
+    """mx_linear launches over `layers` distinct weight sets (so that weights stream from HBM), one input."""
+
+    def __init__(self, torch, gen, M, N, K, flags, layers, count=1):
+        from dooms_amd import _lib
+        self.torch, self._lib = torch, _lib
+        self.M, self.N, self.K, self.flags, self.layers, self.count = M, N, K, flags, layers, count
+        dev = "cuda"
+        self.x = torch.randn(M, K, generator=gen, device=dev)
+        self.w = [[(torch.randn(N, K, generator=gen, device=dev) / math.sqrt(K)).half() for _ in range(count)]
+                  for _ in range(layers)]
+        out16 = bool(flags & _lib.LINEAR_OUT_F16)
+        self.y = [torch.zeros(M, N, dtype=torch.float16 if out16 else torch.float32, device=dev) for _ in range(count)]
+        self.gamma = torch.rand(K, generator=gen, device=dev) + 0.5
+        self.bias = [torch.randn(N, generator=gen, device=dev) for _ in range(count)]
+        self.desc = _lib.MxLinearDesc(M=M, N=N, K=K, flags=flags, x_stride=K, y_stride=N, eps=1e-5, reserved=0)
+        nb = _lib.linear_workspace_bytes(self.desc)
+        self.ws = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
+        self.nb = nb
+
+    def step(self):
+        _lib = self._lib
+        for l in range(self.layers):
+            _lib.check(_lib.linear_raw(self.desc, [w.data_ptr() for w in self.w[l]], self.x.data_ptr(),
+                                       [y.data_ptr() for y in self.y], self.gamma.data_ptr(),
+                                       [b.data_ptr() for b in self.bias] if self.flags & _lib.LINEAR_BIAS else None,
+                                       self.ws.data_ptr(), self.nb, self.torch.cuda.current_stream().cuda_stream))
+
+    def weight_bytes(self):
+        return 2 * self.N * self.K * self.count
+
+    def flops(self):
+        return 2 * self.M * self.N * self.K * self.count
+
+
+class SelfAttentionProblem:
+    """mx_self_attention (the IR SelfAttention op) on packed [B, N, 3E] rows."""
+
+    def __init__(self, torch, gen, B, N, H, D, dtype):
+        from dooms_amd import _lib
+        self.torch, self._lib = torch, _lib
+        codes = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+        E = H * D
+        self.B, self.N, self.E = B, N, E
+        self.qkv = (torch.rand(B, N, 3 * E, generator=gen, device="cuda") * 2 - 1).to(dtype)
+        self.y = torch.empty(B, N, E, dtype=dtype, device="cuda")
+        self.desc = _lib.MxSelfAttnDesc(batch=B, n_tok=N, heads=H, embed=E, dtype=codes[dtype], scale=D ** -0.5)
+        self.nb = _lib.self_attention_workspace_bytes(self.desc)
+        self.ws = torch.empty(max(self.nb, 256), dtype=torch.uint8, device="cuda")
+
+    def step(self):
+        self._lib.check(self._lib.self_attention_raw(self.desc, self.qkv.data_ptr(), self.y.data_ptr(),
+                                                     self.ws.data_ptr(), self.nb,
+                                                     self.torch.cuda.current_stream().cuda_stream))
+
+    def flops(self):
+        return 4 * self.B * self.N * self.N * self.E  # the reference's cost model (src/ir/cost.cpp:30-34)
+
+
 def cpu_info():
     model = ""
     try:
@@ -215,6 +275,42 @@ def cpu_decode_baseline(torch, prob, budget_s, threads):
         nbytes += prob.bytes_per_launch()
         done += 1
     return nbytes / t_total / 1e9, done, t_total
+
+
+def cpu_self_attention_baseline(sp, H, D, budget_s, threads):
+    """The reference's CPU SelfAttention (attention_cpu_op, src/backend/ggml/ggml_backend.cpp:292-312: per (batch, head)
+    scores, row softmax, weighted values in f32) through the restated CPU attention on the packed rows, timed per call."""
+    from oracle import oracle as O
+    x = sp.qkv.float().cpu().numpy()
+    E = sp.E
+    done, t = 0, 0.0
+    while t < budget_s or done == 0:
+        t0 = time.perf_counter()
+        for b in range(sp.B):
+            O.cpu_attend_f32(x[b, :, :E], x[b, :, E:2 * E], x[b, :, 2 * E:], H, H, D, D ** -0.5, causal=False,
+                             n_threads=threads)
+        t += time.perf_counter() - t0
+        done += 1
+    us = t / done * 1e6
+    return {"us_per_call": round(us, 1), "TFLOPs": round(sp.flops() / (us * 1e-6) / 1e12, 4), "cores": threads,
+            "kind": "port", "sample": f"{done} calls of the same shape through the restated CPU attention, {t:.1f} s"}
+
+
+def cpu_gemv_baseline(lp, budget_s):
+    """An f32 GEMV on the host (numpy's BLAS, all its threads) for the same weights: the reference's CPU matvec is
+    llama.cpp/ggml, which is not buildable here, so this is a stand-in port, timed per launch."""
+    import numpy as np
+    w = lp.w[0][0].float().cpu().numpy()
+    x = lp.x.cpu().numpy()
+    done, t = 0, 0.0
+    while t < budget_s or done == 0:
+        t0 = time.perf_counter()
+        _ = x @ w.T
+        t += time.perf_counter() - t0
+        done += 1
+    us = t / done * 1e6
+    return {"us_per_launch": round(us, 1), "GBps_weights_f32": round(4 * lp.N * lp.K / (us * 1e-6) / 1e9, 1),
+            "kind": "port", "sample": f"{done} numpy f32 GEMVs (BLAS threads), {t:.1f} s"}
 
 
 def cpu_prefill_baseline(torch, prob, budget_s, threads):
@@ -398,6 +494,62 @@ def main():
                               "a different metric and machine, so vs_baseline stays null"}
         del p2
 
+    if args.only in ("linear", "all"):
+        # ---- the projections either side of the attention (mx_linear): Llama-3-8B shapes, Whisper cross cache ----
+        from dooms_amd import _lib as L
+        lin = {}
+        for name, M, N, Kd, flags, layers, count in [
+                ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1),
+                ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1),
+                ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1),
+                ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8)]:
+            lp = LinearProblem(torch, gen, M, N, Kd, flags, layers, count)
+            ms_l, _ = time_graph(torch, lp.step, max(5, K), max(1, W))
+            us = ms_l * 1e3 / layers
+            e = {"M": M, "N": N, "K": Kd, "count": count, "us_per_launch": round(us, 2)}
+            if M <= 8:
+                e["GBps_weights"] = round(lp.weight_bytes() / (us * 1e-6) / 1e9, 1)
+                e["roofline"] = {"bound": "hbm", "frac": round(e["GBps_weights"] / HBM_PEAK_GBS, 4)}
+            else:
+                e["TFLOPs"] = round(lp.flops() / (us * 1e-6) / 1e12, 1)
+                e["roofline"] = {"bound": "mfma", "frac": round(e["TFLOPs"] / F16_PEAK_TFLOPS, 4)}
+            if not args.no_cpu and M == 1 and name.startswith("gemv_qkv"):
+                e["cpu_baseline"] = cpu_gemv_baseline(lp, min(5.0, args.cpu_seconds))
+            lin[name] = e
+            del lp
+            torch.cuda.empty_cache()
+        extra["linear"] = lin
+
+    if args.only in ("self-attention", "all"):
+        # ---- the IR SelfAttention op (mx_self_attention): ViT shapes ----
+        sa = {}
+        for name, B, N, H, D, dt in [("vit_h_210x16x80_f32", 1, 210, 16, 80, torch.float32),
+                                     ("vit_b16_384px_b8_f16", 8, 577, 12, 64, torch.float16),
+                                     ("vit_l_1024tok_b4_bf16", 4, 1024, 16, 64, torch.bfloat16)]:
+            sp = SelfAttentionProblem(torch, gen, B, N, H, D, dt)
+            reps = 16
+
+            def step(sp=sp):
+                for _ in range(reps):
+                    sp.step()
+            ms_s, _ = time_graph(torch, step, max(5, K), max(1, W))
+            us = ms_s * 1e3 / reps
+            sa[name] = {"us_per_call": round(us, 2), "TFLOPs": round(sp.flops() / (us * 1e-6) / 1e12, 2),
+                        "flops_per_call": sp.flops()}
+            if not args.no_cpu and name.startswith("vit_h"):
+                sa[name]["cpu_baseline"] = cpu_self_attention_baseline(sp, H, D, min(5.0, args.cpu_seconds), threads)
+            del sp
+        extra["self_attention"] = sa
+
+    if "value" not in result and "prefill" not in result:  # --only linear / self-attention: their first figure
+        if "linear" in extra:
+            e = extra["linear"]["gemv_qkv_llama3_8b"]
+            result.update({"value": e["GBps_weights"], "unit": "GB/s",
+                           "config": {"workload": "mx_linear q|k|v GEMV, Llama-3-8B (M 1, N 6144, K 4096)"}})
+        else:
+            e = extra["self_attention"]["vit_b16_384px_b8_f16"]
+            result.update({"value": e["TFLOPs"], "unit": "TFLOP/s",
+                           "config": {"workload": "mx_self_attention, ViT-B/16 384 px, batch 8 (577 tokens, 12 x 64)"}})
     if "value" not in result:  # --only prefill*: the prefill figure is the line's value
         pre = result["prefill"]
         result.update({"value": pre["value"], "unit": pre["unit"], "ms_per_step": pre["ms_per_step"],
