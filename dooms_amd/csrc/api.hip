@@ -115,10 +115,10 @@ size_t decode_ws_bytes(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len
 
 namespace {
 
-// Row scales of the GEMM path's RMS norm: M floats, 256-byte rounded.
+// The GEMM path (M > 8) stages the input rows as half, zero-padded to a multiple of 64 columns, 256-byte rounded.
 size_t linear_ws_bytes(const mx_linear_desc & d) {
-    if (!(d.flags & MX_LINEAR_RMS_NORM) || d.M <= mx::kLinearGemvMaxRows) return 0;
-    return ((size_t)d.M * sizeof(float) + 255) / 256 * 256;
+    if (d.M <= mx::kLinearGemvMaxRows) return 0;
+    return ((size_t)d.M * (size_t)((d.K + 63) / 64 * 64) * 2 + 255) / 256 * 256;
 }
 
 // Rotary frequencies base^(-2i / head_dim) in f32 (rotate_pair, llama_kernels.h:513-518), computed once per call
@@ -551,7 +551,7 @@ MX_ATTN_API int32_t mx_linear(const mx_linear_desc * desc, int32_t count, const 
     if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
     p.x = X;
     p.gamma = gamma;
-    p.scale = static_cast<float *>(workspace);
+    p.xh = static_cast<mx::half_t *>(workspace);
     p.x_stride = d.x_stride;
     p.y_stride = d.y_stride;
     p.M = d.M;

@@ -12,12 +12,14 @@
 //   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). A workgroup of 4 waves
 //     stages the (normalized) input rows in LDS once; each wave owns 4 weight rows and streams them in 16-byte loads,
 //     two iterations of 4 loads in flight per lane; the dot products stay f32 and are reduced across the wave at the end.
-//   * M > 8 (prompt): gemm_kernel, v_mfma_f32_32x32x16_f16 on 128 x 128 output tiles, K in steps of 32 through LDS
-//     (double buffer, rows padded to 40 halves so that the 16-byte operand reads of 16 consecutive rows hit 16 distinct
-//     4-bank groups), the next step's global loads in flight during the current step's products. Each wave owns a
-//     64 x 64 block (2 x 2 MFMA tiles). The input is converted to half (after the RMS scale) while it is staged.
+//   * M > 8 (prompt): stage_kernel writes each input row once as half(x * gamma * scale) into the workspace (the
+//     reference stages the same values per tile); gemm_kernel, v_mfma_f32_32x32x16_f16 on 128 x 128 output tiles, K in
+//     steps of 64 through LDS (double buffer, rows padded to 72 halves so that the 16-byte operand reads of 16
+//     consecutive rows hit 16 distinct 4-bank groups), the step after next loading while the current step multiplies.
+//     Each wave owns a 64 x 64 block (2 x 2 MFMA tiles); two workgroups per CU.
 //   * Several matrices with the same input and shape (the cross cache's K and V of every layer) run in one launch.
 #include <algorithm>
+#include <type_traits>
 
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
@@ -29,25 +31,43 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
-// ---- RMS scale of each input row (rms_scale, llama_kernels.h:312-328): one workgroup per row ----
-__global__ __launch_bounds__(kThreads) void rms_scale_kernel(LinearParams p) {
+// ---- M > 8: the input rows staged once as half, as the reference's matmul staging does per tile
+// (half(x * gamma * rms_scale), llama_kernels.h:186-199, with rms_scale from llama_kernels.h:312-328): one workgroup
+// per row; the GEMM then multiplies half operands only ----
+template <bool NORM>
+__global__ __launch_bounds__(kThreads) void stage_kernel(LinearParams p) {
     __shared__ float red[kWaves];
     const float * row = p.x + (int64_t)blockIdx.x * p.x_stride;
-    float ss = 0.f;
-    for (int k = threadIdx.x * 4; k < p.K; k += kThreads * 4) {
-        const float4_t v = *reinterpret_cast<const float4_t *>(row + k);
-        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-    }
+    const int kp = (p.K + 63) / 64 * 64;  // staged rows are zero-padded to a multiple of 64 columns
+    half_t * dst = p.xh + (int64_t)blockIdx.x * kp;
+    float s = 1.f;
+    if constexpr (NORM) {
+        float ss = 0.f;
+        for (int k = threadIdx.x * 4; k < p.K; k += kThreads * 4) {
+            const float4_t v = *reinterpret_cast<const float4_t *>(row + k);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += shfl_xor(ss, o);
-    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
-    __syncthreads();
-    if (threadIdx.x == 0) {
+        for (int o = 32; o > 0; o >>= 1) ss += shfl_xor(ss, o);
+        if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+        __syncthreads();
         float t = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) t += red[w];
-        p.scale[blockIdx.x] = 1.f / __builtin_sqrtf(t / (float)p.K + p.eps);
+        s = 1.f / __builtin_sqrtf(t / (float)p.K + p.eps);
     }
+    for (int k = threadIdx.x * 8; k < p.K; k += kThreads * 8) {
+        float x[8];
+        load8f(row + k, x);
+        if constexpr (NORM) {
+            float g[8];
+            load8f(p.gamma + k, g);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] *= g[e] * s;  // x * (gamma * scale), as the reference's staging
+        }
+        *reinterpret_cast<u32x4 *>(dst + k) = to_half8(x);
+    }
+    for (int k = p.K + threadIdx.x * 8; k < kp; k += kThreads * 8) *reinterpret_cast<u32x4 *>(dst + k) = u32x4{0u, 0u, 0u, 0u};
 }
 
 // y (+)= v (+ bias) into row m, column n of output matrix mi.
@@ -178,12 +198,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(LinearParams p) {
     }
 }
 
-// ---- M > 8: MFMA GEMM, 128 x 128 tiles ----
-constexpr int kTM = 128, kTN = 128, kTK = 32;
-constexpr int kPitch = kTK + 8;  // halves per staged row
+// ---- M > 8: MFMA GEMM on the staged half rows, 128 x 128 tiles, K in steps of 64 ----
+constexpr int kTM = 128, kTN = 128, kTK = 64;
+constexpr int kPitch = kTK + 8;  // halves per staged row: the 16-byte reads of 16 consecutive rows hit distinct banks
+constexpr int kChunks = kTM * (kTK / 8) / kThreads;  // 16-byte chunks per thread per tile and step (4)
 
-template <bool NORM, bool OUT16>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(LinearParams p) {
+template <bool OUT16>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
     __shared__ half_t xs[2][kTM * kPitch];
     __shared__ half_t ws[2][kTN * kPitch];
     const int n_tiles = (p.N + kTN - 1) / kTN, m_tiles = (p.M + kTM - 1) / kTM;
@@ -195,31 +216,36 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(LinearParams p) {
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int l32 = lane % 32, hi = lane / 32;
 
-    // staging map: chunk c = threadIdx.x + 256 j (j = 0, 1) is row c / 4, columns 8 (c % 4) .. + 8 of the step
-    float xr[2][8];
-    u32x4 wr[2];
-    auto load = [&](int k0) {
+    // staging map: chunk c = threadIdx.x + 256 j is row c / 8, columns 8 (c % 8) .. + 8 of the step. The staged rows are
+    // zero-padded to a multiple of 64 columns (kp); a weight column past K (K an odd multiple of 32) is read from the
+    // row's last 8 columns instead, finite values that meet the zero padding
+    const int kp = (p.K + kTK - 1) / kTK * kTK;
+    const int kc = threadIdx.x % 8;  // the same for every j: 256 is a multiple of 8
+    const half_t * a0 = p.xh + (int64_t)min(m0 + (int)threadIdx.x / 8, p.M - 1) * kp + 8 * kc;
+    const half_t * b0 = w + (int64_t)min(n0 + (int)threadIdx.x / 8, p.N - 1) * p.K;
+    const int64_t a_step = (int64_t)(kThreads / 8) * kp, b_step = (int64_t)(kThreads / 8) * p.K;  // 32 rows per j
+    const int brow_max = p.N - 1 - n0, arow_max = p.M - 1 - m0;  // rows past N (M) repeat the last row
+    // two register sets: step i's tiles travel in set i % 2, loaded two steps before they are stored into LDS
+    u32x4 ar[2][kChunks], br[2][kChunks];
+    auto load = [&](int step, auto S) __attribute__((always_inline)) {
+        constexpr int st = decltype(S)::value;
+        const int k0 = step * kTK;
+        const int bcol = min(k0 + 8 * kc, p.K - 8);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int c = threadIdx.x + kThreads * j, row = c / 4, kc = c % 4;
-            const int m = min(m0 + row, p.M - 1), n = min(n0 + row, p.N - 1);
-            load8f(p.x + (int64_t)m * p.x_stride + k0 + 8 * kc, xr[j]);
-            if constexpr (NORM) {
-                float g[8];
-                load8f(p.gamma + k0 + 8 * kc, g);
-                const float s = p.scale[m];
-#pragma unroll
-                for (int e = 0; e < 8; e++) xr[j][e] *= g[e] * s;  // x * (gamma * scale), as the reference's staging
-            }
-            wr[j] = load16(w + (int64_t)n * p.K + k0 + 8 * kc);
+        for (int j = 0; j < kChunks; j++) {
+            const int64_t aoff = (int)threadIdx.x / 8 + 32 * j <= arow_max ? j * a_step : (int64_t)(arow_max - (int)threadIdx.x / 8) * kp;
+            ar[st][j] = load16(a0 + aoff + k0);
+            const int64_t boff = (int)threadIdx.x / 8 + 32 * j <= brow_max ? j * b_step : (int64_t)(brow_max - (int)threadIdx.x / 8) * p.K;
+            br[st][j] = load16(b0 + boff + bcol);
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, auto S) __attribute__((always_inline)) {
+        constexpr int st = decltype(S)::value;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int c = threadIdx.x + kThreads * j, row = c / 4, kc = c % 4;
-            *reinterpret_cast<u32x4 *>(&xs[buf][row * kPitch + 8 * kc]) = to_half8(xr[j]);
-            *reinterpret_cast<u32x4 *>(&ws[buf][row * kPitch + 8 * kc]) = wr[j];
+        for (int j = 0; j < kChunks; j++) {
+            const int c = threadIdx.x + kThreads * j, row = c / 8, kc = c % 8;
+            *reinterpret_cast<u32x4 *>(&xs[buf][row * kPitch + 8 * kc]) = ar[st][j];
+            *reinterpret_cast<u32x4 *>(&ws[buf][row * kPitch + 8 * kc]) = br[st][j];
         }
     };
 
@@ -234,21 +260,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(LinearParams p) {
     const int wm = wave / 2, wn = wave % 2;  // this wave's 64 x 64 block
     const int a_base = (64 * wm + l32) * kPitch + 8 * hi;
     const int b_base = (64 * wn + l32) * kPitch + 8 * hi;
-    const int nk = p.K / kTK;
-    load(0);
-    store(0);
-    if (nk > 1) load(kTK);
-    for (int ib = 0; ib < nk; ib++) {
+    const int nk = kp / kTK;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    load(0, S0{});
+    store(0, S0{});
+    load(min(1, nk - 1), S1{});
+    load(min(2, nk - 1), S0{});
+    // step ib: its tiles are in LDS buffer ib % 2; step ib + 1's go from register set (ib + 1) % 2 into the other
+    // buffer, and that set is refilled with step ib + 3's
+    // The loads and stores are unconditional (past the last step the last step's tiles are loaded again and go into a
+    // buffer nobody reads), so the loop has one path and the waits for one register set leave the other set in flight.
+    auto step = [&](int ib, auto S) __attribute__((always_inline)) {
         const int buf = ib & 1;
         __syncthreads();  // step ib is in buffer buf; buffer buf ^ 1 is free
-        if (ib + 1 < nk) {
-            store(buf ^ 1);
-            if (ib + 2 < nk) load((ib + 2) * kTK);
-        }
+        store(buf ^ 1, S);
+        load(min(ib + 3, nk - 1), S);
         const half_t * a_s = xs[buf];
         const half_t * b_s = ws[buf];
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
+        for (int ks = 0; ks < kTK / 16; ks++) {
             half8_t a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) a[i] = as_half8(*reinterpret_cast<const u32x4 *>(a_s + a_base + 32 * i * kPitch + 16 * ks));
@@ -259,7 +290,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(LinearParams p) {
 #pragma unroll
                 for (int j = 0; j < 2; j++) acc[i][j] = mfma32x32x16(a[i], b[j], acc[i][j]);
         }
+    };
+    int ib = 0;
+    for (; ib + 1 < nk; ib += 2) {
+        step(ib, S1{});
+        step(ib + 1, S0{});
     }
+    if (ib < nk) step(ib, S1{});
 
     // lane holds Y[m0 + 64 wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + 64 wn + 32 j + l32]
 #pragma unroll
@@ -302,20 +339,13 @@ hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
         return launch_gemv_t<8>(p, stream);
     }
     const bool norm = p.flags & kLinearNorm;
-    if (norm) {
-        hipLaunchKernelGGL(rms_scale_kernel, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
-        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    }
+    if (norm) hipLaunchKernelGGL(stage_kernel<true>, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(stage_kernel<false>, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);
-    const bool out16 = p.flags & kLinearOutF16;
     const dim3 grid((uint32_t)tiles);
-    if (norm) {
-        if (out16) hipLaunchKernelGGL((gemm_kernel<true, true>), grid, dim3(kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((gemm_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
-    } else {
-        if (out16) hipLaunchKernelGGL((gemm_kernel<false, true>), grid, dim3(kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((gemm_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
-    }
+    if (p.flags & kLinearOutF16) hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -101,7 +101,7 @@ constexpr size_t kLinearGemvLds = 64 * 1024;  // staged input rows up to this ma
 struct LinearParams {
     const float * x;
     const float * gamma;
-    float * scale;  // [M] row RMS scales (GEMM with the norm): written by rms_scale_kernel, read by the GEMM
+    half_t * xh;    // [M][K] the staged input rows (M > 8): written by stage_kernel, read by the GEMM
     int64_t x_stride, y_stride;
     int32_t M, N, K, count;
     uint32_t flags;

@@ -51,8 +51,9 @@ typedef struct mx_linear_desc {
 } mx_linear_desc;
 
 /*
- * Bytes of device workspace mx_linear needs for this descriptor: M floats (256-byte rounded) for the per-row RMS
- * scales when MX_LINEAR_RMS_NORM is set and M > 8 (the reference's rms_scale buffer), else 0.
+ * Bytes of device workspace mx_linear needs for this descriptor: for M > 8, M * round_up(K, 64) halves (256-byte
+ * rounded) for the input rows staged once as half(x * gamma * rms_scale) (the values the reference's matmul stages
+ * per tile, with its rms_scale buffer folded in); 0 for M <= 8.
  */
 MX_ATTN_API size_t mx_linear_workspace_bytes(const mx_linear_desc * desc);
 

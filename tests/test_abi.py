@@ -235,11 +235,13 @@ def test_linear_checks():
     assert call(ld(flags=1)) == _lib.INVALID_ARGUMENT and "gamma" in _lib.last_error()
     assert call(ld(flags=4)) == _lib.INVALID_ARGUMENT and "bias" in _lib.last_error()
     assert call(ld(), x=A + 4) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
-    # the GEMM path's RMS norm needs M floats of workspace
+    # the GEMM path (M > 8) stages the input rows as half: M * K halves of workspace
     d = ld(M=100, flags=1)
-    assert _lib.linear_workspace_bytes(d) == 512 and _lib.linear_workspace_bytes(ld(M=8, flags=1)) == 0
+    assert _lib.linear_workspace_bytes(d) == 100 * 128 * 2 and _lib.linear_workspace_bytes(ld(M=8, flags=1)) == 0
+    assert _lib.linear_workspace_bytes(ld(M=9, K=96, x_stride=96)) == 2304  # 9 rows x 128 padded columns x 2 bytes
     assert call(d, gamma=A, ws=A, ws_bytes=256) == _lib.RESOURCE_EXHAUSTED
-    assert call(d, gamma=A, ws=A + 16, ws_bytes=512) == _lib.INVALID_ARGUMENT
+    assert call(d, gamma=A, ws=A + 16, ws_bytes=1 << 20) == _lib.INVALID_ARGUMENT
+    assert call(ld(M=100)) == _lib.INVALID_ARGUMENT and "workspace" in _lib.last_error()
     assert call(ld(M=0), w=0, x=0, y=0) == _lib.OK
 
 

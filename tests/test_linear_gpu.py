@@ -104,6 +104,13 @@ def test_gemm_ragged_edges(device):
     run(device, 6, 131, 200, 96, bias=True, accumulate=True)
 
 
+@pytest.mark.parametrize("M,N,K", [(9, 64, 32), (33, 132, 160), (200, 256, 192), (129, 96, 320)])
+def test_gemm_step_counts(device, M, N, K):
+    """K steps of 64 (the last one half zero-padded when K is an odd multiple of 32), odd and even step counts
+    (the GEMM's main loop runs steps in pairs and finishes an odd count alone), the smallest GEMM row count."""
+    run(device, 20 + K, M, N, K, norm=True, bias=True)
+
+
 def test_gemm_llama3_attn_output_chunk(device):
     run(device, 7, 300, 4096, 4096, accumulate=True, rows=[0, 1, 127, 128, 255, 299])
 
