@@ -7,6 +7,7 @@
 // (test_metal_llama_decoder.cpp:497-532 evaluates the same prompt in chunks of 20), two layers, GQA 4/2, head_dim 64.
 // Whisper: prompt rows, single-token self-attention steps, greedy and 5-beam cross-attention over 150 encoder rows.
 // Error paths: unsupported head_dim, context overflow, bad layer.
+// The two rows beside the attention (ops_host.hpp): the IR SelfAttention op and a q|k|v projection.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -19,10 +20,14 @@
 #include <vector>
 
 #include "attention_host.hpp"
+#include "ops_host.hpp"
 
 extern "C" int oracle_attention_f64(int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t n_q, int32_t p0, int32_t n_kv,
                                     int32_t causal, double scale, const uint16_t * q, int64_t q_stride, const uint16_t * k,
                                     const uint16_t * v, int64_t kv_stride, double * out, int64_t out_stride, double * lse);
+
+extern "C" int oracle_linear_f64(int32_t M, int32_t N, int32_t K, uint32_t flags, int32_t half_input, float eps, const float * X,
+                                 int64_t x_stride, const uint16_t * W, const float * gamma, const float * bias, double * Y);
 
 extern "C" void oracle_rope_f32(int32_t mode, float base, int32_t head_dim, int32_t pos, const float * x, float * y, int64_t n_vec);
 
@@ -332,6 +337,107 @@ TEST(whisper_f32_buffers) {
     EXPECT(w->self_attention(0, dq, dout, n_text).code == Code::ResourceExhausted);
     (void)hipFree(dq);
     (void)hipFree(dout);
+}
+
+// The IR SelfAttention op through SelfAttentionOp: f16 rows read in place (head_dim 64), f32 rows with padded head_dim
+// 80 (the ViT-H shape's head size), batch 2; oracle_attention_f64 per batch element on the half-rounded operands.
+TEST(ir_self_attention_op) {
+    using namespace dooms_amd;
+    struct Case { int B, N, H, D; DType dt; };
+    for (const Case c : {Case{2, 37, 3, 64, DType::F16}, Case{2, 29, 2, 80, DType::F32}}) {
+        const int E = c.H * c.D;
+        const size_t n_in = (size_t)c.B * c.N * 3 * E, n_out = (size_t)c.B * c.N * E;
+        Rng rng{(uint64_t)(900 + c.D)};
+        std::vector<float> x(n_in);
+        for (auto & v : x) v = (float)(2 * rng.uniform() - 1);
+        std::vector<uint16_t> xh(n_in);
+        for (size_t i = 0; i < n_in; i++) xh[i] = to_half(x[i]);
+        const bool f32 = c.dt == DType::F32;
+        void * dx = nullptr, * dy = nullptr;
+        HIP_OK(hipMalloc(&dx, n_in * (f32 ? 4 : 2)));
+        HIP_OK(hipMalloc(&dy, n_out * (f32 ? 4 : 2)));
+        HIP_OK(hipMemcpy(dx, f32 ? (const void *)x.data() : (const void *)xh.data(), n_in * (f32 ? 4 : 2), hipMemcpyHostToDevice));
+        std::unique_ptr<SelfAttentionOp> op;
+        const float scale = 1.f / std::sqrt((float)c.D);
+        EXPECT(SelfAttentionOp::create(c.H, scale, c.B, c.N, E, c.dt, nullptr, op).is_ok());
+        EXPECT(op->run(dx, dy, c.B, c.N, E).is_ok());
+        // more tokens than the op was created for: rejected before any launch (ResourceExhausted for the workspace, or
+        // InvalidArgument first when the larger extents of the two adjacent buffers overlap)
+        if (f32) EXPECT(!op->run(dx, dy, c.B, c.N + 1, E).is_ok());
+        EXPECT(op->run(dx, dy, c.B, c.N, E).is_ok());
+        HIP_OK(hipDeviceSynchronize());
+        std::vector<uint16_t> got(n_out);
+        if (f32) {
+            std::vector<float> g(n_out);
+            HIP_OK(hipMemcpy(g.data(), dy, n_out * 4, hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < n_out; i++) got[i] = to_half(g[i]);  // compared at the f16 tolerance
+        } else {
+            HIP_OK(hipMemcpy(got.data(), dy, n_out * 2, hipMemcpyDeviceToHost));
+        }
+        std::vector<double> ref(n_out);
+        for (int b = 0; b < c.B; b++) {
+            const uint16_t * base = xh.data() + (size_t)b * c.N * 3 * E;
+            EXPECT(oracle_attention_f64(c.H, c.H, c.D, c.N, 0, c.N, 0, scale, base, 3 * E, base + E, base + 2 * E, 3 * E,
+                                        ref.data() + (size_t)b * c.N * E, E, nullptr) == 0);
+        }
+        EXPECT(close(got, ref, f32 ? "self_attention f32 hd80" : "self_attention f16 hd64"));
+        (void)hipFree(dx);
+        (void)hipFree(dy);
+    }
+    std::unique_ptr<SelfAttentionOp> op;
+    EXPECT(SelfAttentionOp::create(0, 1.f, 1, 4, 64, DType::F16, nullptr, op).code == Code::InvalidArgument);
+    EXPECT(SelfAttentionOp::create(3, 1.f, 1, 4, 64, DType::F16, nullptr, op).code == Code::InvalidArgument);
+    EXPECT(SelfAttentionOp::create(2, NAN, 1, 4, 64, DType::F16, nullptr, op).code == Code::InvalidArgument);
+    EXPECT(SelfAttentionOp::create(1, 1.f, 1, 4, 192, DType::F16, nullptr, op).code == Code::Unsupported);
+}
+
+// A q|k|v projection with the RMS norm and bias through Projection: a 3-row decode step (GEMV) and a 20-row prompt
+// chunk (GEMM) against oracle_linear_f64, and a chunk larger than the declared maximum.
+TEST(projection_decode_and_prompt_rows) {
+    using namespace dooms_amd;
+    const int N = 48, K = 96, maxM = 20;
+    Rng rng{77};
+    std::vector<float> x((size_t)maxM * K), g(K), bias(N);
+    std::vector<uint16_t> w((size_t)N * K);
+    for (auto & v : x) v = 2 * rng.normal();
+    for (auto & v : g) v = (float)(0.2 + 1.8 * rng.uniform());
+    for (auto & v : bias) v = rng.normal();
+    for (auto & v : w) v = to_half(rng.normal() / std::sqrt((float)K));
+    float * dx = nullptr, * dg = nullptr, * db = nullptr, * dy = nullptr;
+    uint16_t * dw = nullptr;
+    HIP_OK(hipMalloc(&dx, x.size() * 4));
+    HIP_OK(hipMalloc(&dg, g.size() * 4));
+    HIP_OK(hipMalloc(&db, bias.size() * 4));
+    HIP_OK(hipMalloc(&dy, (size_t)maxM * N * 4));
+    HIP_OK(hipMalloc(&dw, w.size() * 2));
+    HIP_OK(hipMemcpy(dx, x.data(), x.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dg, g.data(), g.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(db, bias.data(), bias.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dw, w.data(), w.size() * 2, hipMemcpyHostToDevice));
+    const uint32_t flags = MX_LINEAR_RMS_NORM | MX_LINEAR_BIAS;
+    std::unique_ptr<Projection> proj;
+    EXPECT(Projection::create(N, K, flags, 1e-5f, maxM, nullptr, proj).is_ok());
+    const uint16_t * W[1] = {dw};
+    void * Y[1] = {dy};
+    const float * B[1] = {db};
+    for (int M : {3, maxM}) {
+        EXPECT(proj->run(M, 1, W, dx, K, Y, N, dg, B).is_ok());
+        HIP_OK(hipDeviceSynchronize());
+        std::vector<float> got((size_t)M * N);
+        HIP_OK(hipMemcpy(got.data(), dy, got.size() * 4, hipMemcpyDeviceToHost));
+        std::vector<double> ref((size_t)M * N, 0.0);
+        EXPECT(oracle_linear_f64(M, N, K, flags, M > 8, 1e-5f, x.data(), K, w.data(), g.data(), bias.data(), ref.data()) == 0);
+        double worst = 0;
+        for (size_t i = 0; i < ref.size(); i++) worst = std::max(worst, std::fabs(got[i] - ref[i]));
+        if (!(worst <= 2e-2)) std::fprintf(stderr, "  projection M=%d: max abs err %.3e\n", M, worst);
+        EXPECT(worst <= 2e-2);  // |y| ~ 2 sqrt(K) / sqrt(K): f32 accumulation of half operands stays far below this
+    }
+    EXPECT(proj->run(maxM + 1, 1, W, dx, K, Y, N, dg, B).code == Code::ResourceExhausted);
+    (void)hipFree(dx);
+    (void)hipFree(dg);
+    (void)hipFree(db);
+    (void)hipFree(dy);
+    (void)hipFree(dw);
 }
 
 int main() {

@@ -63,6 +63,66 @@ def torch_reference(case):
     return out.transpose(0, 1).reshape(n_q, n_head * hd).numpy(), lse.transpose(0, 1).numpy()
 
 
+# IR SelfAttention (sa_*): the reference's own test shapes (kAttnCases, tests/unit/test_backend_ggml.cpp:679-681),
+# packed [B, N, 3E] rows in f16, U(-1, 1) like the reference's rnd(); name: (B, N, heads, head_dim, seed)
+SA_CASES = {
+    "sa_b1_n5_h2_d4": (1, 5, 2, 4, 705),
+    "sa_b2_n7_h3_d8": (2, 7, 3, 8, 707),
+    "sa_b1_n9_h2_d6": (1, 9, 2, 6, 709),
+    "sa_b1_n17_h4_d64": (1, 17, 4, 64, 717),
+    "sa_b1_n40_h2_d80": (1, 40, 2, 80, 740),
+}
+
+# projections (lin_*): x f32 [M][K], w f16 [N][K], gamma, bias; name: (M, N, K, flags, seed). M <= 8 is the f32-input
+# GEMV form, M > 8 the half-staged GEMM form (llama_kernels.h:96-126, 186-199)
+LIN_CASES = {
+    "lin_gemv_m3_norm_bias": (3, 40, 64, 1 | 4, 31),
+    "lin_gemm_m20_norm_bias": (20, 48, 96, 1 | 4, 32),
+    "lin_gemm_m12_plain": (12, 24, 160, 0, 33),
+}
+
+
+def make_sa_case(B, N, H, D, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    E = H * D
+    qkv = rng.uniform(-1, 1, (B, N, 3 * E)).astype(np.float16)
+    scale = D ** -0.5
+    y = O.self_attention_f64(qkv, H, scale)
+    x = torch.from_numpy(qkv.astype(np.float64))
+    q, k, v = (x[..., i * E:(i + 1) * E].reshape(B, N, H, D).transpose(1, 2) for i in range(3))
+    t = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale).transpose(1, 2).reshape(B, N, E)
+    assert np.abs(t.numpy() - y).max() < 1e-12
+    return dict(qkv=qkv, y=y, heads=np.int64(H), scale=np.float64(scale))
+
+
+def make_lin_case(M, N, K, flags, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((M, K), dtype=np.float32) * 2).astype(np.float32)
+    w = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float16)
+    g = rng.uniform(0.2, 2.0, K).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    eps = 1e-5
+    half_input = M > 8
+    y = O.linear_f64(x, w, flags=flags, half_input=half_input, eps=eps, gamma=g if flags & 1 else None,
+                     bias=b if flags & 4 else None)
+    # independent restatement in numpy (the two staging forms of the reference)
+    xs = x.astype(np.float64)
+    scale = (1 / np.sqrt((xs ** 2).mean(axis=1) + eps)).astype(np.float32)
+    if half_input:
+        a = (x * (g[None, :] * scale[:, None])).astype(np.float16) if flags & 1 else x.astype(np.float16)
+        ref = a.astype(np.float64) @ w.astype(np.float64).T
+    else:
+        a = (x * g[None, :]).astype(np.float64) if flags & 1 else xs
+        ref = a @ w.astype(np.float64).T
+        if flags & 1:
+            ref = ref * scale[:, None].astype(np.float64)
+    if flags & 4:
+        ref = ref + b
+    assert np.abs(ref - y).max() < 1e-9
+    return dict(x=x, w=w, gamma=g, bias=b, y=y, flags=np.int64(flags), eps=np.float64(eps))
+
+
 def main():
     for name, args in CASES.items():
         c = make_case(*args)
@@ -71,6 +131,14 @@ def main():
         assert np.abs(tl - c["lse"]).max() < 1e-12, name
         np.savez(os.path.join(HERE, name + ".npz"), **c)
         print(name, c["out"].shape)
+    for name, args in SA_CASES.items():
+        c = make_sa_case(*args)
+        np.savez(os.path.join(HERE, name + ".npz"), **c)
+        print(name, c["y"].shape)
+    for name, args in LIN_CASES.items():
+        c = make_lin_case(*args)
+        np.savez(os.path.join(HERE, name + ".npz"), **c)
+        print(name, c["y"].shape)
 
 
 if __name__ == "__main__":

@@ -23,6 +23,9 @@ import torch
 from oracle import oracle as O
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+# the attention fixtures (the sa_* and lin_* files hold the self-attention and projection fixtures)
+ATTN_FIXTURES = sorted(p for p in glob.glob(os.path.join(GOLDEN, "*.npz"))
+                       if not os.path.basename(p).startswith(("sa_", "lin_")))
 
 
 def rand_f16(rng, shape, sigma=1.0):
@@ -150,7 +153,7 @@ def test_f16_decoding_matches_numpy_on_every_bit_pattern():
     assert same.all()
 
 
-@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))), ids=os.path.basename)
+@pytest.mark.parametrize("path", ATTN_FIXTURES, ids=os.path.basename)
 def test_golden_fixture(path):
     z = np.load(path)
     n_head, n_head_kv, hd, n_q, n_kv, p0, causal = (int(x) for x in z["meta"])
@@ -163,7 +166,24 @@ def test_golden_fixture(path):
 
 
 def test_golden_fixtures_present():
-    assert len(glob.glob(os.path.join(GOLDEN, "*.npz"))) >= 7
+    assert len(ATTN_FIXTURES) >= 7
+    assert len(glob.glob(os.path.join(GOLDEN, "sa_*.npz"))) >= 5 and len(glob.glob(os.path.join(GOLDEN, "lin_*.npz"))) >= 3
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "sa_*.npz"))), ids=os.path.basename)
+def test_golden_self_attention_fixture(path):
+    z = np.load(path)
+    y = O.self_attention_f64(z["qkv"], int(z["heads"]), float(z["scale"]))
+    np.testing.assert_allclose(y, z["y"], rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "lin_*.npz"))), ids=os.path.basename)
+def test_golden_linear_fixture(path):
+    z = np.load(path)
+    flags = int(z["flags"])
+    y = O.linear_f64(z["x"], z["w"], flags=flags, half_input=z["x"].shape[0] > 8, eps=float(z["eps"]),
+                     gamma=z["gamma"] if flags & 1 else None, bias=z["bias"] if flags & 4 else None)
+    np.testing.assert_allclose(y, z["y"], rtol=0, atol=1e-12)
 
 
 @pytest.mark.parametrize("causal", [0, 1])
