@@ -23,7 +23,7 @@ FLAGS = [
 def build(verbose: bool = False) -> str:
     """Compiles every HIP source into dooms_amd/libmx_attn.so; returns its path. Raises on a compile error."""
     cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-           *[os.path.join(CSRC, s) for s in SOURCES], "-o", LIB + ".tmp"]
+           *[os.path.join(CSRC, s) for s in SOURCES], "-lhipblaslt", "-o", LIB + ".tmp"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     msg = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)

@@ -21,6 +21,17 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, params=["hipblaslt", "hip"])
+def gemm_path(request, monkeypatch):
+    """Prompt chunks (M > 8) run their GEMM on hipBLASLt, or on the library's own gemm_kernel when hipBLASLt offers no
+    algorithm; MX_LINEAR_GEMM=hip forces the latter, so every test here covers both."""
+    if request.param == "hip":
+        monkeypatch.setenv("MX_LINEAR_GEMM", "hip")
+    else:
+        monkeypatch.delenv("MX_LINEAR_GEMM", raising=False)
+    return request.param
+
+
 def check(got, x, w, gamma, bias, eps, half_input, accumulate_from=None, out_f16=False, rows=None, what=""):
     rows = np.arange(x.shape[0]) if rows is None else np.asarray(rows)
     flags = (1 if gamma is not None else 0) | (4 if bias is not None else 0) | (2 if accumulate_from is not None else 0)
