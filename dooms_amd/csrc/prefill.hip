@@ -332,15 +332,31 @@ __global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams 
     const int h = r / (hdp / 8), d0 = 8 * (r % (hdp / 8));
     if (part == 0 && !p.q) return;
     float x[8];
-    const int64_t src = row * 3 * E + (int64_t)part * E + (int64_t)h * hd;
+    const int64_t src = row * 3 * E + (int64_t)part * E + (int64_t)h * hd + d0;
+    if (hd % 8 == 0) {  // uniform: whole 8-wide groups, 16-byte (f16/bf16) or 2 x 16-byte (f32) loads, or padding
+        if (d0 < hd) {
+            if (p.dtype == 0) {
+                load8f(static_cast<const float *>(p.qkv) + src, x);
+            } else {
+                const u32x4 v = load16(static_cast<const uint16_t *>(p.qkv) + src);
+                const uint16_t * u = reinterpret_cast<const uint16_t *>(&v);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int d = d0 + e;
-        x[e] = 0.f;
-        if (d < hd) {
-            if (p.dtype == 1) x[e] = (float)static_cast<const half_t *>(p.qkv)[src + d];
-            else if (p.dtype == 2) x[e] = __uint_as_float((uint32_t)static_cast<const uint16_t *>(p.qkv)[src + d] << 16);
-            else x[e] = static_cast<const float *>(p.qkv)[src + d];
+                for (int e = 0; e < 8; e++)
+                    x[e] = p.dtype == 1 ? (float)__builtin_bit_cast(half_t, u[e]) : __uint_as_float((uint32_t)u[e] << 16);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            x[e] = 0.f;
+            if (d0 + e < hd) {
+                if (p.dtype == 1) x[e] = (float)static_cast<const half_t *>(p.qkv)[src + e];
+                else if (p.dtype == 2) x[e] = __uint_as_float((uint32_t)static_cast<const uint16_t *>(p.qkv)[src + e] << 16);
+                else x[e] = static_cast<const float *>(p.qkv)[src + e];
+            }
         }
     }
     if (part == 0) {
@@ -352,21 +368,36 @@ __global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams 
     }
 }
 
+// one thread per 4 consecutive outputs of a head (head_dim a multiple of 4), else per output
+__device__ __forceinline__ uint16_t to_bf16(float v) {  // round to nearest even; NaN stays a (quiet) NaN
+    const uint32_t b = __float_as_uint(v);
+    return v != v ? (uint16_t)0x7FC0u : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
 __global__ __launch_bounds__(256) void self_attn_unpack_kernel(SelfAttnUnpackParams p) {
     const int H = p.heads, hd = p.hd, E = H * hd;
-    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int V = hd % 4 == 0 ? 4 : 1;
+    const int64_t i = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) * V;
     if (i >= p.rows * E) return;
     const int64_t row = i / E;
     const int c = (int)(i % E), h = c / hd, d = c % hd;
-    const float v = p.o[row * H * p.hdp + (int64_t)h * p.hdp + d];
-    if (p.dtype == 1) {
-        static_cast<half_t *>(p.y)[i] = (half_t)v;
-    } else if (p.dtype == 2) {  // bf16, round to nearest even; NaN stays a (quiet) NaN
-        const uint32_t b = __float_as_uint(v);
-        static_cast<uint16_t *>(p.y)[i] = v != v ? (uint16_t)0x7FC0u : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
-    } else {
-        static_cast<float *>(p.y)[i] = v;
+    const float * o = p.o + row * H * p.hdp + (int64_t)h * p.hdp + d;
+    if (V == 4) {
+        const float4_t v = *reinterpret_cast<const float4_t *>(o);
+        if (p.dtype == 1) {
+            *reinterpret_cast<half4_t *>(static_cast<half_t *>(p.y) + i) = half4_t{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+        } else if (p.dtype == 2) {
+            const u32x2 w = {(uint32_t)to_bf16(v[0]) | ((uint32_t)to_bf16(v[1]) << 16), (uint32_t)to_bf16(v[2]) | ((uint32_t)to_bf16(v[3]) << 16)};
+            *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(p.y) + i) = w;
+        } else {
+            *reinterpret_cast<float4_t *>(static_cast<float *>(p.y) + i) = v;
+        }
+        return;
     }
+    const float v = o[0];
+    if (p.dtype == 1) static_cast<half_t *>(p.y)[i] = (half_t)v;
+    else if (p.dtype == 2) static_cast<uint16_t *>(p.y)[i] = to_bf16(v);
+    else static_cast<float *>(p.y)[i] = v;
 }
 
 hipError_t launch_self_attn_pack(const SelfAttnPackParams & p, hipStream_t stream) {
@@ -377,7 +408,7 @@ hipError_t launch_self_attn_pack(const SelfAttnPackParams & p, hipStream_t strea
 }
 
 hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t stream) {
-    const int64_t n = p.rows * p.heads * p.hd;
+    const int64_t n = p.rows * p.heads * p.hd / (p.hd % 4 == 0 ? 4 : 1);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(self_attn_unpack_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, stream, p);
     return hipGetLastError();
