@@ -308,13 +308,18 @@ void prefill_kernel(PrefillParams p) {
 
 }  // namespace
 
-// Waves per workgroup: 8 (256 query rows, every K/V tile shared by all 8 waves of a CU) when that gives workgroups for
-// at least half of the CUs (measured: a 2048-row chunk of 28 heads, 224 workgroups, runs ~20 % faster than with 448
-// workgroups of 4 waves), else 4 (128 rows), so that short prompts spread over the chip.
+// Waves per workgroup: 8 (256 query rows, one workgroup per CU, every K/V tile shared by all 8 waves) or 4 (128 rows,
+// two workgroups per CU), whichever leaves the least work on the busiest CU: rounds of workgroups per CU times the
+// rows of one, with the 8-wave tile's rows weighted 0.8 for its shared K/V tiles (measured: a 2048-row chunk of 28
+// heads runs ~20 % faster as 224 workgroups of 8 waves than as 448 of 4; 96 problems of 577 rows run 1.6x faster as
+// 480 workgroups of 4 waves than as 288 of 8, of which 32 would wait for a second round). n_head counts every
+// (batch, head) problem of the launch.
 constexpr int kCUs = 256;
 int prefill_waves(int n_q, int n_head) {
-    const int64_t tiles8 = (int64_t)((n_q + 255) / 256) * n_head;
-    return tiles8 >= kCUs / 2 ? 8 : 4;
+    const int64_t wg8 = (int64_t)((n_q + 255) / 256) * n_head, wg4 = (int64_t)((n_q + 127) / 128) * n_head;
+    const double cost8 = (double)((wg8 + kCUs - 1) / kCUs) * 256 * 0.8;
+    const double cost4 = (double)((wg4 + kCUs - 1) / kCUs) * 128;
+    return cost8 <= cost4 ? 8 : 4;
 }
 
 int prefill_rows_per_workgroup(int n_q, int n_head) { return 32 * prefill_waves(n_q, n_head); }
