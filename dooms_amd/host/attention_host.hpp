@@ -245,6 +245,7 @@ public:
     }
 
     int32_t head_dim() const { return cfg_.n_state / cfg_.n_head; }
+    const WhisperAttentionConfig & config() const { return cfg_; }
     uint16_t * self_k(int32_t l) const { return sk_ + (size_t)l * cfg_.n_text_ctx * cfg_.n_state; }
     uint16_t * self_v(int32_t l) const { return sv_ + (size_t)l * cfg_.n_text_ctx * cfg_.n_state; }
     uint16_t * cross_k(int32_t l) const { return ck_ + (size_t)l * cfg_.n_audio_ctx * cfg_.n_state; }

@@ -5,8 +5,10 @@
 //     (src/ir/op.h:31-32, 64-71; src/backend/ggml/ggml_backend.cpp:398-412;
 //     self_attention_params src/ir/op.cpp:69-76)
 //   the decoders' matvec / matmul dispatches around the attention             Projection::create / run
-//     (src/backend/metal/metal_llama_decoder.mm:160-235, 318-352;
-//     encode_cross, src/backend/metal/metal_whisper_decoder.mm:295-316)
+//     (src/backend/metal/metal_llama_decoder.mm:160-235, 318-352)
+//   MetalWhisperDecoder::set_audio / encode_cross: every layer's cross-       WhisperCrossCache::create / set_audio
+//     attention K (no bias) and V (bias) from the encoder states, rounded
+//     to half into the cross caches (metal_whisper_decoder.mm:295-316, 500-520)
 //
 // As in the reference's Executable::run (src/backend/backend.h:50-53: no device allocation in run), the workspace is
 // sized once, at create, for the largest shape the caller declares; run() with a larger shape returns
@@ -143,6 +145,50 @@ private:
     float eps_;
     hipStream_t stream_;
     DeviceBuffer ws_;
+};
+
+// The Whisper decoder's cross-attention cache producer: for every layer l, K_l = X W_k[l]^T and V_l = X W_v[l]^T + b_v[l]
+// over the n_audio_ctx encoder states X [n_audio_ctx][n_state] (f32), rounded to half into the caches of a
+// WhisperAttention (layer l at l * n_audio_ctx rows). One mx_linear call for all 2 n_layer matrices (n_layer <= 32).
+class WhisperCrossCache {
+public:
+    static Status create(const WhisperAttentionConfig & c, hipStream_t stream, std::unique_ptr<WhisperCrossCache> & out) {
+        if (c.n_layer < 1 || 2 * c.n_layer > 64) return {Code::InvalidArgument, "n_layer must be in [1, 32]"};
+        std::unique_ptr<Projection> proj;
+        if (Status st = Projection::create(c.n_state, c.n_state, MX_LINEAR_OUT_F16 | MX_LINEAR_BIAS, 0.f, c.n_audio_ctx,
+                                           stream, proj);
+            !st.is_ok())
+            return st;
+        out.reset(new WhisperCrossCache(c, std::move(proj)));
+        return {};
+    }
+
+    // states: device, f32 [n_audio_ctx][n_state]; w_k, w_v: host arrays [n_layer] of device f16 [n_state][n_state]
+    // weights; b_v: host array [n_layer] of device f32 [n_state] biases (an entry may be null).
+    Status set_audio(WhisperAttention & attn, const float * states, const uint16_t * const * w_k,
+                     const uint16_t * const * w_v, const float * const * b_v) {
+        const WhisperAttentionConfig & a = attn.config();
+        if (a.n_layer != cfg_.n_layer || a.n_state != cfg_.n_state || a.n_audio_ctx != cfg_.n_audio_ctx)
+            return {Code::InvalidArgument, "the attention's shape differs from the producer's"};
+        if (!states || !w_k || !w_v) return {Code::InvalidArgument, "states and weights must not be null"};
+        const uint16_t * W[64];
+        void * Y[64];
+        const float * B[64];
+        for (int32_t l = 0; l < cfg_.n_layer; l++) {
+            W[2 * l] = w_k[l];
+            W[2 * l + 1] = w_v[l];
+            Y[2 * l] = attn.cross_k(l);
+            Y[2 * l + 1] = attn.cross_v(l);
+            B[2 * l] = nullptr;  // the key projection has no bias
+            B[2 * l + 1] = b_v ? b_v[l] : nullptr;
+        }
+        return proj_->run(cfg_.n_audio_ctx, 2 * cfg_.n_layer, W, states, cfg_.n_state, Y, cfg_.n_state, nullptr, B);
+    }
+
+private:
+    WhisperCrossCache(const WhisperAttentionConfig & c, std::unique_ptr<Projection> p) : cfg_(c), proj_(std::move(p)) {}
+    WhisperAttentionConfig cfg_;
+    std::unique_ptr<Projection> proj_;
 };
 
 }  // namespace dooms_amd

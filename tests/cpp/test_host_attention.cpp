@@ -440,6 +440,82 @@ TEST(projection_decode_and_prompt_rows) {
     (void)hipFree(dw);
 }
 
+// The Whisper cross-attention cache from encoder states (set_audio / encode_cross, metal_whisper_decoder.mm:295-316,
+// 500-520): two layers' K (no bias) and V (bias) through WhisperCrossCache, checked against oracle_linear_f64 (the
+// half-staged form, rounded to half), then cross-attention over the produced cache against the attention oracle.
+TEST(whisper_cross_cache_from_encoder_states) {
+    using namespace dooms_amd;
+    const int n_layer = 2, n_state = 128, nh = 2, hd = 64, n_text = 16, n_audio = 150;
+    Dev sk((size_t)n_layer * n_text * n_state), sv((size_t)n_layer * n_text * n_state);
+    Dev ck((size_t)n_layer * n_audio * n_state), cv((size_t)n_layer * n_audio * n_state);
+    const WhisperAttentionConfig cfg{n_layer, n_state, nh, n_text, n_audio, 8};
+    std::unique_ptr<WhisperAttention> w;
+    std::unique_ptr<WhisperCrossCache> prod;
+    EXPECT(WhisperAttention::create(cfg, sk.p, sv.p, ck.p, cv.p, nullptr, w).is_ok());
+    EXPECT(WhisperCrossCache::create(cfg, nullptr, prod).is_ok());
+    if (!w || !prod) return;
+    Rng rng{31};
+    std::vector<float> X((size_t)n_audio * n_state);
+    for (auto & x : X) x = rng.normal();
+    std::vector<std::vector<uint16_t>> Wk(n_layer), Wv(n_layer);
+    std::vector<std::vector<float>> Bv(n_layer);
+    float * dX = nullptr;
+    HIP_OK(hipMalloc(&dX, X.size() * 4));
+    HIP_OK(hipMemcpy(dX, X.data(), X.size() * 4, hipMemcpyHostToDevice));
+    std::vector<uint16_t *> dWk(n_layer), dWv(n_layer);
+    std::vector<float *> dBv(n_layer);
+    for (int l = 0; l < n_layer; l++) {
+        Wk[l].resize((size_t)n_state * n_state);
+        Wv[l].resize((size_t)n_state * n_state);
+        Bv[l].resize(n_state);
+        for (auto & x : Wk[l]) x = to_half(rng.normal() / std::sqrt((float)n_state));
+        for (auto & x : Wv[l]) x = to_half(rng.normal() / std::sqrt((float)n_state));
+        for (auto & x : Bv[l]) x = rng.normal();
+        HIP_OK(hipMalloc(&dWk[l], Wk[l].size() * 2));
+        HIP_OK(hipMalloc(&dWv[l], Wv[l].size() * 2));
+        HIP_OK(hipMalloc(&dBv[l], Bv[l].size() * 4));
+        HIP_OK(hipMemcpy(dWk[l], Wk[l].data(), Wk[l].size() * 2, hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(dWv[l], Wv[l].data(), Wv[l].size() * 2, hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(dBv[l], Bv[l].data(), Bv[l].size() * 4, hipMemcpyHostToDevice));
+    }
+    EXPECT(prod->set_audio(*w, dX, dWk.data(), dWv.data(), dBv.data()).is_ok());
+    HIP_OK(hipDeviceSynchronize());
+    for (int l = 0; l < n_layer; l++) {
+        for (int kv = 0; kv < 2; kv++) {
+            std::vector<uint16_t> got((size_t)n_audio * n_state);
+            HIP_OK(hipMemcpy(got.data(), kv ? w->cross_v(l) : w->cross_k(l), got.size() * 2, hipMemcpyDeviceToHost));
+            std::vector<double> ref((size_t)n_audio * n_state, 0.0);
+            EXPECT(oracle_linear_f64(n_audio, n_state, n_state, kv ? 4u : 0u, 1, 0.f, X.data(), n_state,
+                                     kv ? Wv[l].data() : Wk[l].data(), nullptr, kv ? Bv[l].data() : nullptr, ref.data()) == 0);
+            double worst = 0;
+            for (size_t i = 0; i < ref.size(); i++) worst = std::max(worst, std::fabs(from_half(got[i]) - ref[i]) / (1.0 + std::fabs(ref[i])));
+            if (!(worst <= 4e-3)) std::fprintf(stderr, "  cross cache layer %d %s: max scaled err %.3e\n", l, kv ? "V" : "K", worst);
+            EXPECT(worst <= 4e-3);  // f32 accumulation of half operands, then one rounding to half (2^-11 relative)
+        }
+        // cross-attention (greedy row) over the produced cache
+        std::vector<uint16_t> CK((size_t)n_audio * n_state), CV((size_t)n_audio * n_state);
+        HIP_OK(hipMemcpy(CK.data(), w->cross_k(l), CK.size() * 2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(CV.data(), w->cross_v(l), CV.size() * 2, hipMemcpyDeviceToHost));
+        const std::vector<uint16_t> q = random_half(rng, n_state);
+        Dev dq(n_state), dout(n_state);
+        HIP_OK(hipMemcpy(dq.p, q.data(), q.size() * 2, hipMemcpyHostToDevice));
+        EXPECT(w->cross_attention(l, dq.p, dout.p, 1).is_ok());
+        HIP_OK(hipDeviceSynchronize());
+        std::vector<uint16_t> got(n_state);
+        HIP_OK(hipMemcpy(got.data(), dout.p, got.size() * 2, hipMemcpyDeviceToHost));
+        std::vector<double> ref(n_state);
+        oracle_attention_f64(nh, nh, hd, 1, 0, n_audio, 0, 1.0 / 8.0, q.data(), n_state, CK.data(), CV.data(), n_state,
+                             ref.data(), n_state, nullptr);
+        EXPECT(close(got, ref, "cross-attention over the produced cache"));
+    }
+    (void)hipFree(dX);
+    for (int l = 0; l < n_layer; l++) {
+        (void)hipFree(dWk[l]);
+        (void)hipFree(dWv[l]);
+        (void)hipFree(dBv[l]);
+    }
+}
+
 int main() {
     int dev_count = 0;
     if (hipGetDeviceCount(&dev_count) != hipSuccess || dev_count < 1) {
