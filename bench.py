@@ -429,6 +429,7 @@ def main():
         extra["decode_rope_llama3_8b_b1_L8192"] = {
             "us_per_layer": round(ms_f * 1e3 / 32, 3),
             "GBps": round(32 * fp.bytes_per_launch() / (ms_f * 1e-3) / 1e9, 1),
+            "roofline": {"bound": "hbm", "frac": round(32 * fp.bytes_per_launch() / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
             "note": "mx_attn_decode_rope: f32 q|k|v row in, q/k rotated, new k/v written at position 8191, f32 out"}
         del fp
         torch.cuda.empty_cache()
@@ -534,8 +535,9 @@ def main():
                     sp.step()
             ms_s, _ = time_graph(torch, step, max(5, K), max(1, W))
             us = ms_s * 1e3 / reps
-            sa[name] = {"us_per_call": round(us, 2), "TFLOPs": round(sp.flops() / (us * 1e-6) / 1e12, 2),
-                        "flops_per_call": sp.flops()}
+            tf = sp.flops() / (us * 1e-6) / 1e12
+            sa[name] = {"us_per_call": round(us, 2), "TFLOPs": round(tf, 2), "flops_per_call": sp.flops(),
+                        "roofline": {"bound": "mfma", "frac": round(tf / F16_PEAK_TFLOPS, 4)}}
             if not args.no_cpu and name.startswith("vit_h"):
                 sa[name]["cpu_baseline"] = cpu_self_attention_baseline(sp, H, D, min(5.0, args.cpu_seconds), threads)
             del sp
