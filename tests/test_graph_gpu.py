@@ -50,3 +50,63 @@ def test_graph_replays_match_eager(device):
         step()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(d_out, ref_d)
+
+
+@pytest.mark.parametrize("gemm_path", ["hipblaslt", "hip"])
+def test_graph_replays_linear_and_self_attention(device, monkeypatch, gemm_path):
+    """The projections (GEMV row, staged GEMM chunk through hipBLASLt or the hand-written kernel) and the IR
+    self-attention in all three workspace modes, captured together: the library calls inside (hipBLASLt) must not
+    record anything that changes the result on later replays."""
+    if gemm_path == "hip":
+        monkeypatch.setenv("MX_LINEAR_GEMM", "hip")
+    else:
+        monkeypatch.delenv("MX_LINEAR_GEMM", raising=False)
+    rng = np.random.default_rng(91)
+    K, N = 512, 384
+    w = torch.from_numpy(normal_f16(rng, (N, K), 0.05)).to(device)
+    gamma = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32)).to(device)
+    bias = torch.from_numpy(rng.normal(0, 1, N).astype(np.float32)).to(device)
+    x1 = torch.from_numpy(rng.normal(0, 1, (1, K)).astype(np.float32)).to(device)
+    xm = torch.from_numpy(rng.normal(0, 1, (200, K)).astype(np.float32)).to(device)
+    y1 = torch.empty(1, N, dtype=torch.float32, device=device)
+    ym = torch.empty(200, N, dtype=torch.float32, device=device)
+    sa = {
+        "f16_hd64": torch.from_numpy(normal_f16(rng, (2, 150, 3 * 256))).to(device),
+        "f32_hd128": torch.from_numpy(rng.normal(0, 1, (1, 97, 3 * 512)).astype(np.float32)).to(device),
+        "bf16_hd80": torch.from_numpy(rng.normal(0, 1, (3, 40, 3 * 160)).astype(np.float32)).to(device)
+        .to(torch.bfloat16),
+    }
+    heads = {"f16_hd64": 4, "f32_hd128": 4, "bf16_hd80": 2}
+    sa_out = {k: torch.empty(v.shape[0], v.shape[1], v.shape[2] // 3, dtype=v.dtype, device=device)
+              for k, v in sa.items()}
+
+    def step():
+        A.linear(x1, w, out=y1, gamma=gamma, bias=bias)
+        A.linear(xm, w, out=ym, gamma=gamma, bias=bias)
+        for name, qkv in sa.items():
+            A.self_attention(qkv, heads=heads[name], out=sa_out[name])
+
+    outs = [y1, ym] + list(sa_out.values())
+    step()
+    torch.cuda.synchronize()
+    refs = [o.clone() for o in outs]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    names = ["gemv", "gemm"] + list(sa_out)
+    for i in range(4):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, o, r in zip(names, outs, refs):
+            assert torch.equal(o, r), f"{name} replay {i}"
+        step()
+        torch.cuda.synchronize()
+        for name, o, r in zip(names, outs, refs):
+            assert torch.equal(o, r), f"{name} eager after replay {i}"
