@@ -69,11 +69,23 @@ int32_t hip_status(hipError_t e, const char * what) {
 //   * then as small as possible while the launch stays within workgroup_cap() workgroups (measured on MI355X for
 //     Llama-3-8B batches of 4 and 16: 1536 streams best; two workgroups per CU are resident at once, 512 in all).
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
-constexpr int kMinChunk = 256, kMaxSplits = 32;
+#ifndef MX_DEC_MIN_CHUNK
+#define MX_DEC_MIN_CHUNK 256
+#endif
+constexpr int kMinChunk = MX_DEC_MIN_CHUNK, kMaxSplits = 32;
 int workgroup_cap() {
     const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
     const int v = s ? std::atoi(s) : 0;
     return v > 0 ? v : 1536;
+}
+
+// Waves per workgroup: 8 when the launch has fewer workgroups than the chip has CUs (short or few sequences: each wave
+// then walks half as many 32-key blocks one after another, and the CUs are idle anyway), else 4.
+int decode_waves(int64_t wgs) {
+    const char * s = std::getenv("MX_ATTN_DECODE_WAVES");  // tuning override, read per call
+    const int v = s ? std::atoi(s) : 0;
+    if (v == 4 || v == 8) return v;
+    return wgs <= 256 ? 8 : 4;
 }
 
 struct DecodeShape {
@@ -289,7 +301,8 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
             p.max_split = std::max(p.max_split, p.seq[i].n_split);
         }
         for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
-        if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, st), "decode launch")) return rc;
+        const int waves = decode_waves(launch_wgs(p.chunk));
+        if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, waves, st), "decode launch")) return rc;
     }
     return MX_ATTN_OK;
 }

@@ -18,7 +18,7 @@
 //     hands each lane 4 consecutive keys of one head dimension); P^T is the score MFMA's result layout, rounded to
 //     f16, so the probabilities never leave registers and the vector ALUs only run the softmax.
 //   * Each wave walks 32-key blocks of its workgroup's split with the next block's K/V already in flight (register
-//     double buffer); the 4 waves are merged through LDS.
+//     double buffer); the NW (4 or 8) waves are merged through LDS.
 //   * Splits are merged inside the same launch: each workgroup publishes its partial (acc[head_dim], m, l per row) with
 //     device-scope atomic stores, waits for their completion, and bumps a per-tile counter; the workgroup that brings the
 //     counter to the split count merges and resets it to 0. Publishing with atomic stores (coherent at device scope by
@@ -32,8 +32,6 @@ namespace mx {
 
 namespace {
 
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kBlockKeys = 32;  // keys per wave iteration
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -78,15 +76,18 @@ __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, 
 // With p.append it is the fused decode step (one query row per sequence): q, k and v of the new token come unrotated
 // from the q|k|v row; q and the new key are rotated for position kv_len - 1 and rounded to half, the new key and value
 // are used from registers for that position and written into the caches by the one workgroup whose split holds it.
-template <int HD, int RT, bool F32>
-__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) {
+template <int HD, int RT, bool F32, int NW>
+__global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     using B = KvBlock<HD>;
     constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
 
     constexpr int VP = HD + 16;  // halves per row of a wave's V block in LDS (conflict-free transposing reads)
-    __shared__ half_t s_v[kDecodeWaves][kBlockKeys * VP];
-    __shared__ float s_m[kDecodeWaves][RT], s_l[kDecodeWaves][RT];
-    __shared__ float s_o[kDecodeWaves][RT * HD];
+    constexpr int kThreads = NW * kWave;
+    static_assert(RT * HD * 4 <= kBlockKeys * VP * 2, "a wave's O rows reuse its V block's LDS");
+    __shared__ half_t s_v[NW][kBlockKeys * VP];
+    __shared__ float s_m[NW][RT], s_l[NW][RT];
+    // after its last block each wave's V staging area holds its O rows (RT x HD f32)
+    auto s_o = [&](int w) { return reinterpret_cast<float *>(s_v[w]); };
     __shared__ int s_last;
     __shared__ float2 s_cs[F32 ? HD / 2 : 1];  // fused step: (cos, sin) of each rotary pair's angle
 
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
 
     // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
     const int jb_new = (L - 1) & ~(kBlockKeys - 1);
-    const bool wave_new = F32 && p.append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % kDecodeWaves == wave;
+    const bool wave_new = F32 && p.append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % NW == wave;
     const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
     const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
     u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
@@ -206,8 +207,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     half_t * vw = s_v[wave];
     const int v_rd = (4 * sgrp + (lane % 16) / 4) * VP + 4 * (lane % 4);
 
-    for (; jb < j1; jb += kBlockKeys * kDecodeWaves) {
-        const int jn = jb + kBlockKeys * kDecodeWaves;
+    for (; jb < j1; jb += kBlockKeys * NW) {
+        const int jn = jb + kBlockKeys * NW;
         if (jn < j1) load_block(jn, nxt);
         if constexpr (F32) {
             if (wave_new && jb == jb_new) {  // the new key and value replace what the cache held at L - 1
@@ -292,33 +293,33 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     if (srow < RT) {
 #pragma unroll
         for (int dt = 0; dt < HD / 16; dt++)
-            *reinterpret_cast<float4_t *>(&s_o[wave][srow * HD + 16 * dt + 4 * sgrp]) = o[dt];
+            *reinterpret_cast<float4_t *>(s_o(wave) + srow * HD + 16 * dt + 4 * sgrp) = o[dt];
     }
     __syncthreads();
 
-    // ---- merge the 4 waves; write the output (one split) or publish this split's partial ----
+    // ---- merge the NW waves; write the output (one split) or publish this split's partial ----
     // Each thread owns head-dim pairs (r, 2 dp .. + 2) of the tile's RT x HD outputs.
     const bool single = sq.n_split == 1;
     const int64_t tile = ((int64_t)bl * p.n_head_kv + g) * p.n_rowtiles + rt;  // (sequence, kv head, row tile)
     float * part_tile = p.part + tile * p.max_split * RT * (HD + 4);
     constexpr int64_t SS = (int64_t)RT * (HD + 4);  // floats between the partials of consecutive splits
     constexpr int NP = RT * HD / 2;                 // output pairs of the tile
-    for (int idx = threadIdx.x; idx < NP; idx += kDecodeThreads) {
+    for (int idx = threadIdx.x; idx < NP; idx += kThreads) {
         const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
         const int row = rt * RT + r;
         if (row >= p.rows) continue;
         float M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; w++)
+        for (int w = 0; w < NW; w++)
             if (s_l[w][r] > 0.f) M = fmaxf(M, s_m[w][r]);
         float tot = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; w++) {
+        for (int w = 0; w < NW; w++) {
             if (!(s_l[w][r] > 0.f)) continue;
             const float wt = exp2_fast(s_m[w][r] - M);
             tot += s_l[w][r] * wt;
-            a0 += s_o[w][r * HD + d] * wt;
-            a1 += s_o[w][r * HD + d + 1] * wt;
+            a0 += s_o(w)[r * HD + d] * wt;
+            a1 += s_o(w)[r * HD + d + 1] * wt;
         }
         if (single) {
             const int t = row / G, h = g * G + row % G;
@@ -349,10 +350,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     // chunk's splits; the row's (m, l) loads of a wave coalesce), then folds them with a running maximum. One memory
     // round trip per chunk, no LDS, no barrier. ----
     const int ns = sq.n_split;
-    constexpr int PPT = (NP + kDecodeThreads - 1) / kDecodeThreads;  // output pairs per thread
+    constexpr int PPT = (NP + kThreads - 1) / kThreads;  // output pairs per thread
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
-        const int idx = threadIdx.x + j * kDecodeThreads;
+        const int idx = threadIdx.x + j * kThreads;
         if (idx >= NP) break;
         const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
         const int row = rt * RT + r;
@@ -392,14 +393,21 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeParams p) 
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int HD, int RT>
+template <int HD, int RT, int NW>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
     const int tiles = n_seq * p.n_head_kv * p.n_rowtiles;
     if (p.f32)
-        hipLaunchKernelGGL((decode_kernel<HD, RT, true>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
+        hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW>), dim3(p.max_split, tiles), dim3(NW * kWave), 0, stream, p);
     else
-        hipLaunchKernelGGL((decode_kernel<HD, RT, false>), dim3(p.max_split, tiles), dim3(kDecodeThreads), 0, stream, p);
+        hipLaunchKernelGGL((decode_kernel<HD, RT, false, NW>), dim3(p.max_split, tiles), dim3(NW * kWave), 0, stream, p);
     return hipGetLastError();
+}
+
+template <int HD, int NW>
+hipError_t launch_decode_hd(const DecodeParams & p, int n_seq, int rt, hipStream_t stream) {
+    if (rt == 4) return launch_decode_t<HD, 4, NW>(p, n_seq, stream);
+    if (rt == 8) return launch_decode_t<HD, 8, NW>(p, n_seq, stream);
+    return launch_decode_t<HD, 16, NW>(p, n_seq, stream);
 }
 
 // Zero fill (the split counters start at 0); a kernel rather than a memset so that a caller may capture it in a graph.
@@ -411,15 +419,10 @@ __global__ void fill_zero_kernel(uint32_t * p, size_t n) {
 
 int decode_rows_per_tile(int rows) { return rows <= 4 ? 4 : rows <= 8 ? 8 : 16; }
 
-hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, hipStream_t stream) {
-    if (head_dim == 64) {
-        if (rt == 4) return launch_decode_t<64, 4>(p, n_seq, stream);
-        if (rt == 8) return launch_decode_t<64, 8>(p, n_seq, stream);
-        return launch_decode_t<64, 16>(p, n_seq, stream);
-    }
-    if (rt == 4) return launch_decode_t<128, 4>(p, n_seq, stream);
-    if (rt == 8) return launch_decode_t<128, 8>(p, n_seq, stream);
-    return launch_decode_t<128, 16>(p, n_seq, stream);
+hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, int waves, hipStream_t stream) {
+    if (head_dim == 64)
+        return waves == 8 ? launch_decode_hd<64, 8>(p, n_seq, rt, stream) : launch_decode_hd<64, 4>(p, n_seq, rt, stream);
+    return waves == 8 ? launch_decode_hd<128, 8>(p, n_seq, rt, stream) : launch_decode_hd<128, 4>(p, n_seq, rt, stream);
 }
 
 hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream) {

@@ -112,7 +112,7 @@ struct LinearParams {
 };
 
 int decode_rows_per_tile(int rows);
-hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, hipStream_t stream);
+hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, int waves, hipStream_t stream);
 hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 
 int prefill_rows_per_workgroup(int n_q, int n_head);  // query rows one prefill workgroup covers

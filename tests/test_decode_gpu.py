@@ -222,3 +222,21 @@ def test_f32_whisper_prompt_rows(device):
 
 def test_f32_llama3_8b_batch3(device):
     run_decode_f32(device, 43, 32, 8, 128, [1, 700, 5000], check_heads=[0, 13, 31])
+
+
+@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("case", ["qwen513", "llama_b4", "whisper_cross_b5", "causal_rows", "gqa16_hd128"])
+def test_waves_per_workgroup(device, monkeypatch, waves, case):
+    # both workgroup shapes (4 or 8 waves; the library picks 8 when a launch fits the CUs in one round) on every tile
+    # size: rows per tile 4 (GQA 4), 8 (GQA 7, beam 5), 16 (causal rows, GQA 16)
+    monkeypatch.setenv("MX_ATTN_DECODE_WAVES", waves)
+    if case == "qwen513":
+        run_decode(device, 1, 14, 2, 64, [513])
+    elif case == "llama_b4":
+        run_decode(device, 34, 32, 8, 128, [6841, 1638, 33, 2721], check_heads=[0, 5, 31])
+    elif case == "whisper_cross_b5":
+        run_decode(device, 95, 20, 20, 64, [1500] * 5, n_q=1, shared_cache=True, check_heads=[0, 7, 19])
+    elif case == "causal_rows":
+        run_decode(device, 108, 14, 2, 64, [300], n_q=8, causal=True)
+    else:
+        run_decode(device, 114, 16, 1, 128, [777])

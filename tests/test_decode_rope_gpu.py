@@ -103,3 +103,11 @@ def test_rope_decode_rejects_shared_cache(device):
     with pytest.raises(_lib.MxAttnError) as e:
         A.decode_rope(qkv, [k, k], [v, v], [4, 5], n_head=4, n_head_kv=2, head_dim=64, rope_mode=0)
     assert e.value.code == _lib.INVALID_ARGUMENT
+
+
+# the new position in every wave of both workgroup shapes (4 or 8 waves of 32-key blocks per split)
+@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("L", [33, 100, 129, 200, 257, 8192])
+def test_rope_decode_waves_per_workgroup(device, monkeypatch, waves, L):
+    monkeypatch.setenv("MX_ATTN_DECODE_WAVES", waves)
+    run_rope(device, 500 + L, 32, 8, 128, [L], 0, 500000.0, check_heads=[0, 5, 17, 31] if L > 4000 else None)
