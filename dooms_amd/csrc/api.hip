@@ -69,10 +69,7 @@ int32_t hip_status(hipError_t e, const char * what) {
 //   * then as small as possible while the launch stays within workgroup_cap() workgroups (measured on MI355X for
 //     Llama-3-8B batches of 4 and 16: 1536 streams best; two workgroups per CU are resident at once, 512 in all).
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
-#ifndef MX_DEC_MIN_CHUNK
-#define MX_DEC_MIN_CHUNK 256
-#endif
-constexpr int kMinChunk = MX_DEC_MIN_CHUNK, kMaxSplits = 32;
+constexpr int kMinChunk = 256, kMaxSplits = 32;
 int workgroup_cap() {
     const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
     const int v = s ? std::atoi(s) : 0;
