@@ -371,6 +371,20 @@ def main():
     torch.cuda.synchronize()
     extra["copy_GBps"] = round(2 * a.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
     del a, b
+    # same-run dense f16 GEMM through the vendor library (torch.matmul -> hipBLASLt), 8192^3: what the matrix cores
+    # sustain on this box under its power limit, a second denominator beside the published 2.5 PFLOP/s
+    a = torch.randn(8192, 8192, device="cuda", generator=gen).half()
+    b = torch.randn(8192, 8192, device="cuda", generator=gen).half()
+    for _ in range(3):
+        c = a @ b.t()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(8):
+        c = a @ b.t()
+    e1.record()
+    torch.cuda.synchronize()
+    extra["f16_gemm_8192_TFLOPs"] = round(2 * 8192 ** 3 * 8 / (e0.elapsed_time(e1) * 1e-3) / 1e12, 1)
+    del a, b, c
 
     model, ncpu = cpu_info()
     threads = max(1, min(16, ncpu))

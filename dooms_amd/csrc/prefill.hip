@@ -33,12 +33,14 @@ namespace {
 constexpr int kBK = 64;  // keys per block
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef half_t half2_t __attribute__((ext_vector_type(2)));
+constexpr half2_t kOnes2 = {(half_t)1.f, (half_t)1.f};
 
 // LDS tiles are row-major with padded rows: K rows HD + 8 halves apart (the 16-byte reads of 16 consecutive rows at one
 // column land on 16 distinct 4-bank groups), V rows HD + 32 halves apart (a row step of 16 banks mod 64: the 4 rows x
 // 32 bytes that each 16-lane group reads through the transposing read, for both groups of a 32-lane phase, land on 64
-// distinct banks; the tile store writes 4 rows x 4 chunks per 16 lanes, also 16 distinct 4-bank groups). Every read address is a per-lane base plus a compile-time
-// offset, so the loop spends no ALU on addressing.
+// distinct banks; the tile store writes 4 rows x 4 chunks per 16 lanes, also 16 distinct 4-bank groups). Every read
+// address is a per-lane base plus a compile-time offset, so the loop spends no ALU on addressing.
 template <int HD>
 struct PrefillSmem {
     static constexpr int KP = HD + 8;
@@ -233,16 +235,12 @@ void prefill_kernel(PrefillParams p) {
         const float m_use = none ? 0.f : m_new;   // then every exponent below is 2^-inf = 0
         const float corr = none ? 1.f : exp2_fast(m_run - m_new);
         m_run = m_new;
-        float bsum = 0.f;
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const float e = exp2_fast(POS ? __builtin_fmaf(sc[mt][v], c, -m_use) : sc[mt][v] - m_use);
-                sc[mt][v] = e;
-                bsum += e;
+                sc[mt][v] = exp2_fast(POS ? __builtin_fmaf(sc[mt][v], c, -m_use) : sc[mt][v] - m_use);
             }
-        l_run = l_run * corr + bsum;
         if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {  // the running max moved in some row of the wave
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
@@ -268,6 +266,14 @@ void prefill_kernel(PrefillParams p) {
             for (int u = 0; u < 4; u++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) pb[u][e] = (half_t)sc[u / 2][8 * (u % 2) + e];
+            // the row sum of the half probabilities that multiply V, on v_dot2_f32_f16 (two per instruction, f32 sum)
+            float bsum = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    bsum = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, bsum, false);
+            l_run = l_run * corr + bsum;
             vread(0, vt[0]);
 #pragma unroll
             for (int i = 0; i < NP; i++) {
