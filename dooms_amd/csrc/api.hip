@@ -239,9 +239,15 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     const WsLayout wl = decode_ws_layout(desc, batch, max_len);
 
     const DecodeShape s = decode_shape(desc);
+    // the grid's y dimension holds (sequence, kv head, row tile) and is limited to 65535
+    const int64_t tiles_per_seq = (int64_t)d.n_head_kv * s.n_rowtiles;
+    if (tiles_per_seq > 65535)
+        return fail(MX_ATTN_UNSUPPORTED, "n_head * n_q (%lld query rows per sequence) is too large for one decode launch",
+                    (long long)d.n_head * d.n_q);
+    const int32_t seq_per_launch = (int32_t)std::min<int64_t>(mx::kMaxSeqPerLaunch, 65535 / tiles_per_seq);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    for (int32_t b0 = 0; b0 < batch; b0 += mx::kMaxSeqPerLaunch) {
-        const int n_seq = std::min<int32_t>(mx::kMaxSeqPerLaunch, batch - b0);
+    for (int32_t b0 = 0; b0 < batch; b0 += seq_per_launch) {
+        const int n_seq = std::min<int32_t>(seq_per_launch, batch - b0);
         mx::DecodeParams p;
         p.q = static_cast<const mx::half_t *>(q);
         p.out = static_cast<mx::half_t *>(out);

@@ -124,6 +124,8 @@ def test_decode_checks():
     assert decode(d, lens=(5000,), ws=0) == _lib.INVALID_ARGUMENT and "workspace is null" in _lib.last_error()
     assert decode(d, lens=(5000,), ws=A + 16) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
     assert decode(desc(n_q=0), lens=(5,)) == _lib.OK
+    # (kv head, row tile) pairs of one sequence beyond the grid's 65535: refused before anything is enqueued
+    assert decode(desc(n_q=40000, causal=0), lens=(100,)) == _lib.UNSUPPORTED and "too large" in _lib.last_error()
 
 
 def rope_decode(d, mode=0, base=500000.0, lens=(100,), kp=None, vp=None, qkv=A, rope=True):
