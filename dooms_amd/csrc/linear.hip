@@ -393,7 +393,9 @@ const BlasPlan * blas_plan(const LinearParams & p, int kp, hipblasLtHandle_t h, 
     return ok ? &pl : nullptr;
 }
 
-// Runs the count products on hipBLASLt; done = false (and hipSuccess) when it offers no algorithm for the shape.
+// Runs the product on hipBLASLt (count == 1); done = false (and hipSuccess) when it offers no algorithm for the shape or
+// refuses the call (an operand alignment its algorithm does not take, for one), so that gemm_kernel runs instead: a
+// refused hipblasLtMatmul enqueues nothing.
 hipError_t blas_gemm(const LinearParams & p, int kp, hipStream_t stream, bool & done) {
     done = false;
     int dev = 0;
@@ -407,18 +409,13 @@ hipError_t blas_gemm(const LinearParams & p, int kp, hipStream_t stream, bool & 
     const BlasPlan * pl = blas_plan(p, kp, h, dev);
     if (!pl) return hipSuccess;
     const float alpha = 1.f, beta = (p.flags & kLinearAccumulate) ? 1.f : 0.f;
-    for (int i = 0; i < p.count; i++) {
-        const hipblasLtEpilogue_t ep =
-            ((p.flags & kLinearBias) && p.bias[i]) ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
-        const void * bias = p.bias[i];
-        if (hipblasLtMatmulDescSetAttribute(pl->op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof ep) != HIPBLAS_STATUS_SUCCESS ||
-            hipblasLtMatmulDescSetAttribute(pl->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof bias) != HIPBLAS_STATUS_SUCCESS)
-            return hipErrorUnknown;
-        if (hipblasLtMatmul(h, pl->op, &alpha, p.w[i], pl->a, p.xh, pl->b, &beta, p.y[i], pl->c, p.y[i], pl->c, &pl->algo,
-                            nullptr, 0, stream) != HIPBLAS_STATUS_SUCCESS)
-            return hipErrorUnknown;
-    }
-    done = true;
+    const hipblasLtEpilogue_t ep =
+        ((p.flags & kLinearBias) && p.bias[0]) ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
+    const void * bias = p.bias[0];
+    done = hipblasLtMatmulDescSetAttribute(pl->op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof ep) == HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatmulDescSetAttribute(pl->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof bias) == HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatmul(h, pl->op, &alpha, p.w[0], pl->a, p.xh, pl->b, &beta, p.y[0], pl->c, p.y[0], pl->c, &pl->algo,
+                           nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
     return hipSuccess;
 }
 
