@@ -508,6 +508,34 @@ def main():
             "reference_note": "M1 Pro GPU time of prompt attention for a 512-token prompt (site/data.js:142-146); "
                               "a different metric and machine, so vs_baseline stays null"}
         del p2
+        # ---- the reference's prompt path on its f32 q|k|v rows (mx_attn_prefill_rope: rope_store + attention),
+        # cfg5's 32k prompt in 2048-row chunks, split-half rotation (Qwen2), base 1e6 ----
+        from dooms_amd import _lib as L
+        nq, nkv, hd, N, C = 28, 4, 128, 32768, 2048
+        qkv = torch.randn(N, (nq + 2 * nkv) * hd, generator=gen, device="cuda") * 0.5
+        kc = torch.empty(N, nkv * hd, dtype=torch.float16, device="cuda")
+        vc = torch.empty_like(kc)
+        o32 = torch.empty(N, nq * hd, dtype=torch.float32, device="cuda")
+        rdescs = [L.make_desc(nq, nkv, hd, C, qkv.stride(0), kc.stride(0), o32.stride(0), 1.0 / math.sqrt(hd),
+                              p0=p0, causal=1) for p0 in range(0, N, C)]
+
+        def rope_step():
+            for ci, d in enumerate(rdescs):
+                p0 = ci * C
+                L.check(L.prefill_rope_raw(d, 1, 1e6, qkv.data_ptr() + p0 * qkv.stride(0) * 4, kc.data_ptr(),
+                                           vc.data_ptr(), o32.data_ptr() + p0 * o32.stride(0) * 4, 0,
+                                           torch.cuda.current_stream().cuda_stream))
+        ms_r, _ = time_graph(torch, rope_step, max(3, K // 4), max(1, W // 2))
+        fl_r = sum(prefill_flops(C, p0, nq, hd) for p0 in range(0, N, C))
+        tf_r = fl_r / (ms_r * 1e-3) / 1e12
+        extra["prefill_rope_qwen7b_32k"] = {
+            "ms_per_step": round(ms_r, 3), "TFLOPs": round(tf_r, 1),
+            "roofline": {"bound": "mfma", "frac": round(tf_r / F16_PEAK_TFLOPS, 4)},
+            "note": "mx_attn_prefill_rope per 2048-row chunk: f32 q|k|v rows in, keys/values rotated into the f16 "
+                    "caches (rope_store_kernel), queries rotated in the attention kernel, f32 out; same FLOPs as the "
+                    "prefill line"}
+        del qkv, kc, vc, o32
+        torch.cuda.empty_cache()
 
     if args.only in ("linear", "all"):
         # ---- the projections either side of the attention (mx_linear): Llama-3-8B shapes, Whisper cross cache ----
