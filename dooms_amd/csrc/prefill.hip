@@ -7,7 +7,7 @@
 //
 // MI355X design:
 //   * One workgroup = 8 waves = 256 query rows of one query head (4 waves = 128 rows for short prompts); each wave owns
-//     32 rows. The register budget is held to 256 per lane, so each SIMD interleaves two waves: one wave's softmax runs
+//     32 rows. When even those would leave most CUs idle, two waves share a 32-row tile and split its key blocks. The register budget is held to 256 per lane, so each SIMD interleaves two waves: one wave's softmax runs
 //     on the vector ALU while the other's products run on the matrix core; all waves of a CU share each K/V tile.
 //   * Key/value blocks of 64 rows pass through LDS, double-buffered: block i + 1 goes from registers into the free LDS
 //     buffer and block i + 2 is loaded from HBM/L2 into registers while block i is multiplied; one barrier per block.
@@ -26,6 +26,8 @@
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
+#include <cstdlib>
+
 namespace mx {
 
 namespace {
@@ -41,29 +43,35 @@ constexpr half2_t kOnes2 = {(half_t)1.f, (half_t)1.f};
 // 32 bytes that each 16-lane group reads through the transposing read, for both groups of a 32-lane phase, land on 64
 // distinct banks; the tile store writes 4 rows x 4 chunks per 16 lanes, also 16 distinct 4-bank groups). Every read
 // address is a per-lane base plus a compile-time offset, so the loop spends no ALU on addressing.
-template <int HD>
+template <int HD, int KSP>
 struct PrefillSmem {
     static constexpr int KP = HD + 8;
     static constexpr int VP = HD + 32;
-    half_t k[2][kBK * KP];
-    half_t v[2][kBK * VP];
+    half_t k[2][KSP * kBK * KP];
+    half_t v[2][KSP * kBK * VP];
 };
 
 // POS: the scale is > 0, so the block maximum can be taken on raw scores and the scale folded into the exponent's FMA.
-// W: waves per workgroup (32 query rows each); all W waves share each K/V tile in LDS.
+// W: waves per workgroup; all W waves share each K/V tile in LDS.
+// KSP: waves per 32-row query tile. With KSP = 1 each wave owns 32 query rows and walks every key block; with KSP = 2
+// (short prompts, where the workgroups would not fill the chip) the two waves of a row tile take alternate 64-key
+// blocks of each 128-key step and merge their (m, l, O) through LDS at the end, halving the chain of dependent blocks.
 // ROPE: the reference's prompt path (rope_store, then attention_prefill on f32 q rows, llama_kernels.h:520-545, 660):
 // query rows are read in f32 from the q|k|v rows, rotated for their position and rounded to half; the output is f32.
-template <int HD, bool POS, int W, bool ROPE>
-__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int HD, bool POS, int W, bool ROPE, int KSP>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 ? 2 : 1, KSP == 1 ? 2 : 1)))
 void prefill_kernel(PrefillParams p) {
-    constexpr int kWaves = W, kPrefillRows = 32 * W;
+    constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
+    static_assert(W % KSP == 0, "whole row tiles");
     constexpr int KS = HD / 16;          // MFMA steps along head_dim for S^T
     constexpr int DT = HD / 32;          // 32-wide output tiles along head_dim
     constexpr int C8 = HD / 8;           // 16-byte chunks per key row
-    constexpr int NB = (kBK / 16) * (C8 / 4);  // (16 keys x 4 chunks) load blocks per tile
-    constexpr int NI = NB / kWaves;      // loads per thread per tile, for each of K and V
-    constexpr int KP = PrefillSmem<HD>::KP, VP = PrefillSmem<HD>::VP;
-    __shared__ PrefillSmem<HD> sm;
+    constexpr int KB = KSP * kBK;        // keys per step (one 64-key block per wave of a row tile)
+    constexpr int NB = (KB / 16) * (C8 / 4);  // (16 keys x 4 chunks) load blocks per step
+    constexpr int NI = NB / kWaves;      // loads per thread per step, for each of K and V
+    static_assert(NB % kWaves == 0, "whole loads per thread");
+    constexpr int KP = PrefillSmem<HD, KSP>::KP, VP = PrefillSmem<HD, KSP>::VP;
+    __shared__ PrefillSmem<HD, KSP> sm;
 
     // ---- work item: heavy query tiles first, GQA groups adjacent, contiguous ranges per XCD ----
     const uint32_t n_work = (uint32_t)p.n_qtiles * p.n_head;
@@ -80,16 +88,17 @@ void prefill_kernel(PrefillParams p) {
     float * const lse_g = p.lse ? p.lse + blockIdx.y * p.lse_batch : nullptr;
 
     const int wave = threadIdx.x / kWave;  // wave-uniform, in a scalar register
+    const int rt = wave % RPW, kh = wave / RPW;  // the wave's row tile and its block of each step
     const int lane = threadIdx.x % kWave;
     const int l32 = lane % 32, hgrp = lane / 32;
-    const int qrow = q0 + 32 * wave + l32;      // this lane's query row (chunk index)
+    const int qrow = q0 + 32 * rt + l32;        // this lane's query row (chunk index)
     const int qpos = p.p0 + qrow;               // its cache position
-    const int wave_last = p.p0 + q0 + 32 * wave + 31;  // the wave's last query position
+    const int wave_last = p.p0 + q0 + 32 * rt + 31;  // the wave's last query position
 
     // keys this workgroup must visit
     const int last_row = min(q0 + kPrefillRows, p.n_q) - 1;
     const int kend = p.causal ? min(p.n_kv, p.p0 + last_row + 1) : p.n_kv;
-    const int nblk = (kend + kBK - 1) / kBK;
+    const int nblk = (kend + KB - 1) / KB;  // steps of KB keys
 
     const half_t * kg = p.k + bkv + (int64_t)kvh * HD;
     const half_t * vg = p.v + bkv + (int64_t)kvh * HD;
@@ -97,10 +106,10 @@ void prefill_kernel(PrefillParams p) {
     //   K: row 16 (b % 4) + lane % 16, chunk 4 (b / 4) + lane / 16 (16 lanes of one LDS write phase: 16 rows, one chunk)
     //   V: row 16 (b % 4) + 4 (lane / 16) + (lane % 16) / 4, chunk 4 (b / 4) + lane % 4 (16 lanes: 4 rows x 4 chunks)
     u32x4 kreg[NI], vreg[NI];
-    auto krow = [&](int b) { return 16 * (b % (kBK / 16)) + lane % 16; };
-    auto kchunk = [&](int b) { return 4 * (b / (kBK / 16)) + lane / 16; };
-    auto vrow = [&](int b) { return 16 * (b % (kBK / 16)) + 4 * (lane / 16) + (lane % 16) / 4; };
-    auto vchunk = [&](int b) { return 4 * (b / (kBK / 16)) + lane % 4; };
+    auto krow = [&](int b) { return 16 * (b % (KB / 16)) + lane % 16; };
+    auto kchunk = [&](int b) { return 4 * (b / (KB / 16)) + lane / 16; };
+    auto vrow = [&](int b) { return 16 * (b % (KB / 16)) + 4 * (lane / 16) + (lane % 16) / 4; };
+    auto vchunk = [&](int b) { return 4 * (b / (KB / 16)) + lane % 4; };
     auto load_tile = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -147,7 +156,7 @@ void prefill_kernel(PrefillParams p) {
     if (nblk > 0) {
         load_tile(0);
         store_tile(0);
-        if (nblk > 1) load_tile(kBK);
+        if (nblk > 1) load_tile(KB);
     }
     // Wait here for the query operand (and the prologue's loads): inside the loop the only loads in flight are then the
     // prefetch of a later block, whose registers the block's math does not read, so no wait inside the loop has to
@@ -168,16 +177,16 @@ void prefill_kernel(PrefillParams p) {
     const int v_base = (4 * hgrp + (lane % 16) / 4) * VP + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
 
     for (int ib = 0; ib < nblk; ib++) {
-        const int kb = ib * kBK;
+        const int kb = ib * KB + kh * kBK;  // this wave's block of the step
         const int buf = ib & 1;
-        __syncthreads();  // block ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
+        __syncthreads();  // step ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
         if (ib + 1 < nblk) {
             store_tile(buf ^ 1);
-            if (ib + 2 < nblk) load_tile(kb + 2 * kBK);
+            if (ib + 2 < nblk) load_tile((ib + 2) * KB);
         }
-        if (p.causal && kb > wave_last) continue;  // every key of the block is past this wave's rows
-        const half_t * ks_ = sm.k[buf];
-        const half_t * vs_ = sm.v[buf];
+        if (kb >= kend || (p.causal && kb > wave_last)) continue;  // every key of the block is past this wave's rows
+        const half_t * ks_ = sm.k[buf] + kh * kBK * KP;
+        const half_t * vs_ = sm.v[buf] + kh * kBK * VP;
 
         // S^T = K Q^T: 2 tiles of 32 keys. The K operand of step i + 1 is read before the product of step i, so each
         // product waits only for reads issued one product earlier.
@@ -202,7 +211,7 @@ void prefill_kernel(PrefillParams p) {
         }
         // block max (raw scores when the scale is positive); the mask only where a block crosses the diagonal or the
         // end of the cache (a wave-uniform branch)
-        const bool need_mask = (p.causal && kb + kBK - 1 > p.p0 + q0 + 32 * wave) || kb + kBK > p.n_kv;
+        const bool need_mask = (p.causal && kb + kBK - 1 > p.p0 + q0 + 32 * rt) || kb + kBK > p.n_kv;
         const float c = p.scale_log2;
         float bmax = kNegInf;
         if (need_mask) {
@@ -286,8 +295,42 @@ void prefill_kernel(PrefillParams p) {
         }
     }
 
-    // ---- normalize and store: lane holds O[qrow][32 dt + 8 (v / 4) + 4 hgrp + v % 4] ----
     l_run += shfl_xor(l_run, 32);
+    if constexpr (KSP > 1) {
+        // ---- the KSP waves of a row tile merge their (m, l, O): waves kh > 0 leave theirs in LDS (the tiles are no
+        // longer read), the wave kh = 0 folds them in ----
+        constexpr int XS = DT * 16 + 2;  // floats per lane
+        static_assert((int64_t)RPW * (KSP - 1) * kWave * XS * 4 <= (int64_t)sizeof(sm), "merge scratch fits the tiles");
+        float * xs = reinterpret_cast<float *>(&sm);
+        __syncthreads();
+        if (kh > 0) {
+            float * d = xs + ((rt * (KSP - 1) + kh - 1) * kWave + lane) * XS;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) d[16 * dt + v] = o[dt][v];
+            d[16 * DT] = m_run;
+            d[16 * DT + 1] = l_run;
+        }
+        __syncthreads();
+        if (kh > 0) return;
+#pragma unroll
+        for (int j = 0; j < KSP - 1; j++) {
+            const float * d = xs + ((rt * (KSP - 1) + j) * kWave + lane) * XS;
+            const float m1 = d[16 * DT], l1 = d[16 * DT + 1];
+            const float mn = fmaxf(m_run, m1);
+            const float w0 = m_run == kNegInf ? 0.f : exp2_fast(m_run - mn);
+            const float w1 = m1 == kNegInf ? 0.f : exp2_fast(m1 - mn);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) o[dt][v] = o[dt][v] * w0 + d[16 * dt + v] * w1;
+            l_run = l_run * w0 + l1 * w1;
+            m_run = mn;
+        }
+    }
+
+    // ---- normalize and store: lane holds O[qrow][32 dt + 8 (v / 4) + 4 hgrp + v % 4] ----
     if (qrow < p.n_q) {
         const float inv = 1.f / l_run;
         const int64_t off = (int64_t)qrow * p.out_stride + (int64_t)h * HD + 4 * hgrp;
@@ -320,15 +363,25 @@ void prefill_kernel(PrefillParams p) {
 // heads runs ~20 % faster as 224 workgroups of 8 waves than as 448 of 4; 96 problems of 577 rows run 1.6x faster as
 // 480 workgroups of 4 waves than as 288 of 8, of which 32 would wait for a second round). n_head counts every
 // (batch, head) problem of the launch.
+// When even the 128-row workgroups would leave half the CUs idle and there are at least 512 keys, the plan is 64-row
+// workgroups of 4 waves, two per row tile splitting the key blocks (KSP = 2): one round on the CUs, half the chain of
+// dependent blocks per wave, but twice the K/V bytes through the load path per step. Measured: the Qwen2.5-0.5B
+// 512-token prompt 12.0 -> 10.8 us per layer, a 16-row chunk at 30k keys (28 heads, hd 128) 629 -> 559 us; a
+// 300-token Llama-3-8B prompt (5 blocks) ran 7 % slower split, hence the 512-key floor.
+// Plans: 8 = 8 waves x 32 rows, 4 = 4 waves x 32 rows, 2 = 4 waves over 2 row tiles x 2 key halves (64 rows).
 constexpr int kCUs = 256;
-int prefill_waves(int n_q, int n_head) {
+int prefill_plan(int n_q, int n_head, int n_kv) {
+    const char * s = std::getenv("MX_PREFILL_PLAN");  // tuning and test override, read per call
+    const int forced = s ? std::atoi(s) : 0;
+    if (forced == 2 || forced == 4 || forced == 8) return forced;
     const int64_t wg8 = (int64_t)((n_q + 255) / 256) * n_head, wg4 = (int64_t)((n_q + 127) / 128) * n_head;
+    if (2 * wg4 <= kCUs && n_kv >= 8 * kBK) return 2;
     const double cost8 = (double)((wg8 + kCUs - 1) / kCUs) * 256 * 0.8;
     const double cost4 = (double)((wg4 + kCUs - 1) / kCUs) * 128;
     return cost8 <= cost4 ? 8 : 4;
 }
 
-int prefill_rows_per_workgroup(int n_q, int n_head) { return 32 * prefill_waves(n_q, n_head); }
+int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv) { return 32 * prefill_plan(n_q, n_head, n_kv); }
 
 // ---- the IR self-attention's operand packing (row f4): one thread per 8 consecutive padded head dims ----
 __global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams p) {
@@ -426,27 +479,29 @@ hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t s
 }
 
 template <int HD, bool POS, bool ROPE>
-void launch_prefill_r(const PrefillParams & p, int waves, int n_batch, hipStream_t stream) {
+void launch_prefill_r(const PrefillParams & p, int plan, int n_batch, hipStream_t stream) {
     const dim3 grid((uint32_t)p.n_qtiles * p.n_head, (uint32_t)n_batch);
-    if (waves == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE>), grid, dim3(8 * kWave), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE>), grid, dim3(4 * kWave), 0, stream, p);
+    if (plan == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE, 1>), grid, dim3(8 * kWave), 0, stream, p);
+    else if (plan == 4) hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 1>), grid, dim3(4 * kWave), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 2>), grid, dim3(4 * kWave), 0, stream, p);
 }
 
 template <int HD, bool POS>
-void launch_prefill_t(const PrefillParams & p, int waves, int n_batch, hipStream_t stream) {
-    if (p.rope) launch_prefill_r<HD, POS, true>(p, waves, n_batch, stream);
-    else launch_prefill_r<HD, POS, false>(p, waves, n_batch, stream);
+void launch_prefill_t(const PrefillParams & p, int plan, int n_batch, hipStream_t stream) {
+    if (p.rope) launch_prefill_r<HD, POS, true>(p, plan, n_batch, stream);
+    else launch_prefill_r<HD, POS, false>(p, plan, n_batch, stream);
 }
 
 hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, hipStream_t stream) {
     const bool pos = p.scale_log2 > 0.f;
-    const int waves = prefill_waves(p.n_q, p.n_head * n_batch);
+    const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv);
+    if (p.n_qtiles != (p.n_q + 32 * plan - 1) / (32 * plan)) return hipErrorInvalidValue;  // planned with other inputs
     if (head_dim == 64) {
-        if (pos) launch_prefill_t<64, true>(p, waves, n_batch, stream);
-        else launch_prefill_t<64, false>(p, waves, n_batch, stream);
+        if (pos) launch_prefill_t<64, true>(p, plan, n_batch, stream);
+        else launch_prefill_t<64, false>(p, plan, n_batch, stream);
     } else {
-        if (pos) launch_prefill_t<128, true>(p, waves, n_batch, stream);
-        else launch_prefill_t<128, false>(p, waves, n_batch, stream);
+        if (pos) launch_prefill_t<128, true>(p, plan, n_batch, stream);
+        else launch_prefill_t<128, false>(p, plan, n_batch, stream);
     }
     return hipGetLastError();
 }

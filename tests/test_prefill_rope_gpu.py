@@ -104,3 +104,11 @@ def test_prompt_in_chunks_matches_one_call(device):
     assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
     # per row the same keys in the same block order: the chunked result equals the one-call result
     assert torch.equal(torch.cat(parts), one)
+
+
+# the reference's prompt path under every workgroup plan (see test_prefill_gpu.test_workgroup_plans)
+@pytest.mark.parametrize("plan", ["2", "4", "8"])
+def test_workgroup_plans(device, monkeypatch, plan):
+    monkeypatch.setenv("MX_PREFILL_PLAN", plan)
+    run_prefill_rope(device, 300, 14, 2, 64, 300, 170, 1, 1000000.0)
+    run_prefill_rope(device, 301, 8, 2, 128, 200, 0, 0, 500000.0)
