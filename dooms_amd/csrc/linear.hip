@@ -9,9 +9,10 @@
 //     here the GEMM rounds to half in its epilogue and writes the cache row directly.
 //
 // MI355X design:
-//   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). A workgroup of 4 waves
-//     stages the (normalized) input rows in LDS once; each wave owns 4 weight rows and streams them in 16-byte loads,
-//     two iterations of 4 loads in flight per lane; the dot products stay f32 and are reduced across the wave at the end.
+//   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). One workgroup per CU
+//     (1 to 8 waves, as the rows divide) stages the (normalized) input rows in LDS once; each wave owns 4 weight rows and
+//     streams them in 16-byte loads, 4 sweeps of 4 loads in flight per lane, the first ones issued before the staging;
+//     the dot products stay f32 and are reduced across the wave at the end.
 //   * M > 8 (prompt): stage_kernel writes each input row once as half(x * gamma * scale) into the workspace (the
 //     reference stages the same values per tile); gemm_kernel, v_mfma_f32_32x32x16_f16 on 128 x 128 output tiles, K in
 //     steps of 64 through LDS (double buffer, rows padded to 72 halves so that the 16-byte operand reads of 16
@@ -98,18 +99,45 @@ __device__ __forceinline__ void store_y(const LinearParams & p, int mi, int m, i
 }
 
 // ---- M <= 8: f32 input rows in LDS, 4 weight rows per wave ----
-constexpr int kGemvRows = 4;  // weight rows per wave
+constexpr int kGemvRows = 4;       // weight rows per wave
+constexpr int kGemvMaxWaves = 8;   // waves per workgroup (the launch sizes workgroups so that each CU gets one)
+constexpr int kGemvDepth = 4;      // 64-lane sweeps of 16-byte weight loads in flight per wave
 
 // STAGE: the input rows (times gamma) fit the LDS budget and are staged once; otherwise every wave reads them from
 // L2 as it goes (the reference's kStageInput = false variant, metal_llama_decoder.mm:45-47).
+// The wave's first kGemvDepth sweeps of weight loads are issued before the input is staged, so the staging and its
+// barriers overlap the first HBM round trip.
 template <int MT, bool STAGE, bool OUT16>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(LinearParams p) {
+__global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParams p) {
     extern __shared__ float xs[];  // [MT][K]: x (* gamma) of each input row, when staged
-    __shared__ float red[MT][kWaves];
+    __shared__ float red[MT][kGemvMaxWaves];
     __shared__ float s_scale[MT];
     const int K = p.K, M = p.M;
     const bool norm = p.flags & kLinearNorm;
+    const int nw = blockDim.x / kWave;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+
+    // work item: (matrix, group of 4 rows) per wave
+    const int groups = (p.N + kGemvRows - 1) / kGemvRows;
+    const int item = blockIdx.x * nw + wave;
+    const bool active = item < groups * p.count;
+    const int mi = active ? item / groups : 0;
+    const int r0 = active ? (item % groups) * kGemvRows : 0;
+    const half_t * w = p.w[mi];
+    const half_t * wr[kGemvRows];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; i++) wr[i] = w + (int64_t)min(r0 + i, p.N - 1) * K;
+    const int C8 = K / 8;  // 16-byte chunks per row
+    half8_t wv[kGemvDepth][kGemvRows];
+    auto load_sweep = [&](int j, int c) __attribute__((always_inline)) {
+        const int cc = min(c, C8 - 1);  // past the row: a valid chunk, not used
+#pragma unroll
+        for (int i = 0; i < kGemvRows; i++) wv[j][i] = as_half8(load16(wr[i] + 8 * cc));
+    };
+    if (active) {
+#pragma unroll
+        for (int j = 0; j < kGemvDepth; j++) load_sweep(j, lane + kWave * j);
+    }
 
     // stage the rows and, with the norm, reduce their sums of squares (stage_input, llama_kernels.h:62-80)
 #pragma unroll
@@ -117,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(LinearParams p) {
         float ss = 0.f;
         if (m < M) {
             const float * xr = p.x + (int64_t)m * p.x_stride;
-            for (int k = threadIdx.x * 4; k < K; k += kThreads * 4) {
+            for (int k = threadIdx.x * 4; k < K; k += blockDim.x * 4) {
                 float4_t v = *reinterpret_cast<const float4_t *>(xr + k);
                 ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
                 if constexpr (STAGE) {
@@ -135,34 +163,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(LinearParams p) {
     __syncthreads();
     if (norm && threadIdx.x < MT) {
         float t = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) t += red[threadIdx.x][w];
+        for (int w2 = 0; w2 < nw; w2++) t += red[threadIdx.x][w2];
         s_scale[threadIdx.x] = 1.f / __builtin_sqrtf(t / (float)K + p.eps);
     }
     __syncthreads();
-
-    // work item: (matrix, group of 4 rows) per wave
-    const int groups = (p.N + kGemvRows - 1) / kGemvRows;
-    const int item = blockIdx.x * kWaves + wave;
-    if (item >= groups * p.count) return;  // after the last barrier
-    const int mi = item / groups;
-    const int r0 = (item % groups) * kGemvRows;
-    const half_t * w = p.w[mi];
-    const half_t * wr[kGemvRows];
-#pragma unroll
-    for (int i = 0; i < kGemvRows; i++) wr[i] = w + (int64_t)min(r0 + i, p.N - 1) * K;
+    if (!active) return;  // after the last barrier
 
     float acc[kGemvRows][MT];
 #pragma unroll
     for (int i = 0; i < kGemvRows; i++)
 #pragma unroll
         for (int m = 0; m < MT; m++) acc[i][m] = 0.f;
-    const int C8 = K / 8;  // 16-byte chunks per row
-#pragma unroll 2
-    for (int c = lane; c < C8; c += kWave) {
-        half8_t wv[kGemvRows];
-#pragma unroll
-        for (int i = 0; i < kGemvRows; i++) wv[i] = as_half8(load16(wr[i] + 8 * c));
+    auto sweep = [&](int j, int c) __attribute__((always_inline)) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             float4_t x0, x1;
@@ -182,12 +194,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(LinearParams p) {
             for (int i = 0; i < kGemvRows; i++) {
                 float a = acc[i][m];
 #pragma unroll
-                for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[i][e], x0[e], a);
+                for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[j][i][e], x0[e], a);
 #pragma unroll
-                for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[i][4 + e], x1[e], a);
+                for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[j][i][4 + e], x1[e], a);
                 acc[i][m] = a;
             }
         }
+    };
+    // sweep j of pass q covers chunk 256 q + 64 j + lane; its registers are reloaded for the next pass right after use.
+    // The loads are unconditional inside the loop and the last pass is peeled off (no loads), so the compiler's waits
+    // track each sweep's own loads instead of draining every load at the top of a pass.
+    constexpr int kPass = kWave * kGemvDepth;
+    const int npass = (C8 + kPass - 1) / kPass;
+    for (int q = 0; q + 1 < npass; q++) {
+#pragma unroll
+        for (int j = 0; j < kGemvDepth; j++) {
+            const int c = q * kPass + kWave * j + lane;  // < C8: not the last pass
+            sweep(j, c);
+            load_sweep(j, c + kPass);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kGemvDepth; j++) {
+        const int c = (npass - 1) * kPass + kWave * j + lane;
+        if (c < C8) sweep(j, c);
     }
     // reduce over the wave; lane i * MT + m stores (row r0 + i, input row m)
     float mine = 0.f;
@@ -321,18 +351,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
         }
 }
 
+// Waves per workgroup: the (matrix, 4-row group) items spread evenly over the CUs, one workgroup per CU (the weight
+// stream of each CU then ends at the same time), up to 8 waves; beyond 2048 items, several workgroups of 8 per CU.
 template <int MT>
 hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
-    const int groups = (p.N + kGemvRows - 1) / kGemvRows;
-    const dim3 grid((uint32_t)((groups * p.count + kWaves - 1) / kWaves));
+    const int64_t items = (int64_t)((p.N + kGemvRows - 1) / kGemvRows) * p.count;
+    const int nw = (int)std::min<int64_t>(kGemvMaxWaves, std::max<int64_t>(1, (items + 255) / 256));
+    const dim3 grid((uint32_t)((items + nw - 1) / nw));
+    const dim3 block((uint32_t)(nw * kWave));
     const size_t lds = (size_t)MT * p.K * sizeof(float);
     const bool out16 = p.flags & kLinearOutF16;
     if (lds <= kLinearGemvLds) {
-        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, true, true>), grid, dim3(kThreads), lds, stream, p);
-        else hipLaunchKernelGGL((gemv_kernel<MT, true, false>), grid, dim3(kThreads), lds, stream, p);
+        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, true, true>), grid, block, lds, stream, p);
+        else hipLaunchKernelGGL((gemv_kernel<MT, true, false>), grid, block, lds, stream, p);
     } else {
-        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, false, true>), grid, dim3(kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((gemv_kernel<MT, false, false>), grid, dim3(kThreads), 0, stream, p);
+        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, false, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((gemv_kernel<MT, false, false>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
 }
