@@ -68,8 +68,12 @@ int32_t hip_status(hipError_t e, const char * what) {
 //     merge (measured: 64 splits of an 8192-key Llama-3-8B row cost ~5 us more than 32);
 //   * then as small as possible while the launch stays within workgroup_cap() workgroups (measured on MI355X for
 //     Llama-3-8B batches of 4 and 16: 1536 streams best; two workgroups per CU are resident at once, 512 in all).
+//   * but when the longest sequence is short (keys x head_dim <= kOneSplitWork: at most 20 KB of K and V for each of
+//     the 8 waves), one split per sequence: the waves of its workgroup walk the keys and no merge follows. Measured:
+//     Qwen2.5-0.5B at 513 keys 7.6 -> 6.8 us, Whisper self-attention at 449 keys 8.3 -> 7.7 us; but Qwen2.5-0.5B at
+//     700 keys 7.5 -> 8.1 us and Llama-3-8B (hd 128) at 600-768 keys 9.8 -> 13.6 us, hence the bound.
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
-constexpr int kMinChunk = 256, kMaxSplits = 32;
+constexpr int kMinChunk = 256, kMaxSplits = 32, kOneSplitWork = 40960;
 int workgroup_cap() {
     const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
     const int v = s ? std::atoi(s) : 0;
@@ -278,6 +282,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
         auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
         int64_t chunk = std::max<int64_t>(round_up(kMinChunk), round_up((lmax + kMaxSplits - 1) / kMaxSplits));
+        if (lmax * d.head_dim <= kOneSplitWork) chunk = round_up(lmax);  // short caches: one split, no merge
         auto launch_wgs = [&](int64_t c) {
             int64_t n = 0;
             for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
