@@ -182,6 +182,7 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.out32 = static_cast<float *>(out);
     p.rope_mode = rope ? rope->mode : 2;
     p.q_batch = p.kv_batch = p.out_batch = p.lse_batch = 0;
+    p.hdv = p.head_stride = d.head_dim;
     fill_freq(p.rope_freq, rope, d.head_dim);
     if (rope) {  // the chunk's keys and values go into the caches first (stream order)
         mx::RopeStoreParams r;
@@ -332,9 +333,12 @@ int32_t check_self_attn(const mx_self_attn_desc * d) {
     return MX_ATTN_OK;
 }
 
-// How a descriptor runs: in place (f16, head_dim 64/128), with f16 keys/values copied (f32, head_dim 64/128), or padded.
+// How a descriptor runs: 0 the f16 rows in place (head_dim 64 or 128); 1 the rows in place through the kernel variant
+// for their type (f32, bf16, or f16 with another head_dim), when head_dim is a multiple of 8 (every 8-element chunk
+// 16-byte aligned): Q, K, V rounded to half as they are loaded, zero columns up to the kernel's head_dim, the output
+// in the rows' type; 2 otherwise: packed into padded f32 Q and f16 K|V in the workspace, and unpacked afterwards.
 struct SelfAttnPlan {
-    int mode;       // 0 in place, 1 f16 copy of K/V, 2 padded operands
+    int mode;       // 0 in place, 1 in place with conversion, 2 packed
     int hd, hdp;    // head_dim and the kernel's head_dim
     size_t q_off, kv_off, o_off, bytes;  // workspace layout
 };
@@ -343,14 +347,11 @@ SelfAttnPlan self_attn_plan(const mx_self_attn_desc & d) {
     SelfAttnPlan s{};
     s.hd = d.embed / d.heads;
     const bool native = s.hd == 64 || s.hd == 128;
-    s.mode = native && d.dtype == MX_ATTN_F16 ? 0 : native && d.dtype == MX_ATTN_F32 ? 1 : 2;
+    s.mode = native && d.dtype == MX_ATTN_F16 ? 0 : s.hd % 8 == 0 ? 1 : 2;
     s.hdp = s.hd <= 64 ? 64 : 128;
     const int64_t rows = (int64_t)d.batch * d.n_tok;
     auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-    if (s.mode == 1) {
-        s.kv_off = 0;
-        s.bytes = up((size_t)rows * 2 * d.embed * 2);
-    } else if (s.mode == 2) {
+    if (s.mode == 2) {
         const size_t w = (size_t)rows * d.heads * s.hdp;
         s.q_off = 0;
         s.kv_off = up(w * 4);
@@ -403,27 +404,31 @@ MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void
     p.lse = nullptr;
     p.lse_batch = 0;
     fill_freq(p.rope_freq, nullptr, s.hdp);
-    if (s.mode == 0) {  // the packed f16 rows in place: q at column 0, k at E, v at 2E of each 3E row
-        const mx::half_t * x = static_cast<const mx::half_t *>(qkv);
-        p.q = x;
-        p.k = x + E;
-        p.v = x + 2 * E;
+    if (s.mode != 2) {  // the rows in place: q at column 0, k at E, v at 2E of each 3E row (elements of the rows' type)
+        const char * x = static_cast<const char *>(qkv);
+        p.q = reinterpret_cast<const mx::half_t *>(x);
+        p.k = reinterpret_cast<const mx::half_t *>(x + E * esz);
+        p.v = reinterpret_cast<const mx::half_t *>(x + 2 * E * esz);
         p.out = static_cast<mx::half_t *>(y);
+        p.out32 = static_cast<float *>(y);
         p.q_stride = p.kv_stride = 3 * E;
         p.out_stride = E;
         p.q_batch = p.kv_batch = (int64_t)d.n_tok * 3 * E;
         p.out_batch = (int64_t)d.n_tok * E;
         p.rope = 0;
-        return hip_status(mx::launch_prefill_batched(p, s.hd, d.batch, st), "self_attention launch");
+        p.hdv = s.hd;
+        p.head_stride = s.hd;
+        const int sa = s.mode == 0 ? 0 : d.dtype == MX_ATTN_F32 ? 1 : d.dtype == MX_ATTN_BF16 ? 2 : 3;
+        return hip_status(mx::launch_prefill_batched(p, s.hdp, d.batch, sa, st), "self_attention launch");
     }
     mx::SelfAttnPackParams pk;
     pk.qkv = qkv;
-    pk.q = s.mode == 2 ? reinterpret_cast<float *>(ws + s.q_off) : nullptr;
+    pk.q = reinterpret_cast<float *>(ws + s.q_off);
     pk.kv = reinterpret_cast<mx::half_t *>(ws + s.kv_off);
     pk.rows = rows;
     pk.heads = d.heads;
     pk.hd = s.hd;
-    pk.hdp = s.mode == 2 ? s.hdp : s.hd;
+    pk.hdp = s.hdp;
     pk.dtype = d.dtype;
     if (int32_t rc = hip_status(mx::launch_self_attn_pack(pk, st), "self_attention pack launch")) return rc;
     const int64_t W = (int64_t)d.heads * pk.hdp;  // padded row width of one third
@@ -432,15 +437,6 @@ MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void
     p.kv_stride = 2 * W;
     p.kv_batch = (int64_t)d.n_tok * 2 * W;
     p.rope = 1;  // f32 query rows (no rotation, rope_mode 2) and f32 output
-    if (s.mode == 1) {  // f32 query rows read in place, f32 output straight into y
-        p.qkv = static_cast<const float *>(qkv);
-        p.q_stride = 3 * E;
-        p.q_batch = (int64_t)d.n_tok * 3 * E;
-        p.out32 = static_cast<float *>(y);
-        p.out_stride = E;
-        p.out_batch = (int64_t)d.n_tok * E;
-        return hip_status(mx::launch_prefill_batched(p, s.hd, d.batch, st), "self_attention launch");
-    }
     p.qkv = pk.q;
     p.q_stride = W;
     p.q_batch = (int64_t)d.n_tok * W;
@@ -448,7 +444,7 @@ MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void
     p.out32 = o;
     p.out_stride = W;
     p.out_batch = (int64_t)d.n_tok * W;
-    if (int32_t rc = hip_status(mx::launch_prefill_batched(p, s.hdp, d.batch, st), "self_attention launch")) return rc;
+    if (int32_t rc = hip_status(mx::launch_prefill_batched(p, s.hdp, d.batch, 0, st), "self_attention launch")) return rc;
     mx::SelfAttnUnpackParams u;
     u.o = o;
     u.y = y;

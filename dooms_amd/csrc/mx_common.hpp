@@ -122,6 +122,19 @@ __device__ __forceinline__ void load8f(const float * src, float (&x)[8]) {
     }
 }
 
+// bf16 <-> f32: a bf16 value is the upper half of an f32; to_bf16 rounds to nearest even, NaN stays a (quiet) NaN
+__device__ __forceinline__ uint16_t to_bf16(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return v != v ? (uint16_t)0x7FC0u : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ void bf16x8_to_f32(u32x4 w, float (&x)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        x[2 * e] = __uint_as_float(w[e] << 16);
+        x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+    }
+}
+
 __device__ __forceinline__ u32x4 to_half8(const float (&x)[8]) {
     half8_t h;
 #pragma unroll

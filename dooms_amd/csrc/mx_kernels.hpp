@@ -62,6 +62,9 @@ struct PrefillParams {
     // independent problems along blockIdx.y (the IR self-attention's batch): elements between the q (or qkv), cache,
     // output and lse blocks of consecutive problems; 0 for one problem
     int64_t q_batch, kv_batch, out_batch, lse_batch;
+    // the IR self-attention's rows read in place (kernel variants for f32, bf16 or f16 rows): head_dim of the rows
+    // (<= the kernel's, a multiple of 8; columns past it are zeros) and the elements between consecutive heads
+    int32_t hdv, head_stride;
     float rope_freq[kMaxHeadDim / 2];
 };
 
@@ -120,7 +123,7 @@ hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t str
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
 // n_batch problems of the prefill kernel along blockIdx.y, offsets from p.*_batch
-hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, hipStream_t stream);
+hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, int sa, hipStream_t stream);
 hipError_t launch_self_attn_pack(const SelfAttnPackParams & p, hipStream_t stream);
 hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t stream);
 

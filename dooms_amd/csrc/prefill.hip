@@ -58,11 +58,18 @@ struct PrefillSmem {
 // blocks of each 128-key step and merge their (m, l, O) through LDS at the end, halving the chain of dependent blocks.
 // ROPE: the reference's prompt path (rope_store, then attention_prefill on f32 q rows, llama_kernels.h:520-545, 660):
 // query rows are read in f32 from the q|k|v rows, rotated for their position and rounded to half; the output is f32.
-template <int HD, bool POS, int W, bool ROPE, int KSP>
+// SA: the IR self-attention's own [B][N][3E] rows read in place (0: no, the f16 operands of the attention entry
+// points): 1 f32, 2 bf16, 3 f16 rows with head_dim p.hdv (a multiple of 8, at most HD) and heads p.head_stride
+// elements apart. Q, K and V are rounded to half as they are loaded (K and V when the tile goes into LDS, so the
+// prefetch stays in flight), columns past p.hdv read as zeros, and the output is written in the rows' type.
+template <int HD, bool POS, int W, bool ROPE, int KSP, int SA>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 ? 2 : 1, KSP == 1 ? 2 : 1)))
 void prefill_kernel(PrefillParams p) {
     constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
     static_assert(W % KSP == 0, "whole row tiles");
+    static_assert(!(ROPE && SA), "the rotated prompt path reads f16 operands");
+    constexpr int ES = SA == 1 ? 4 : 2;  // bytes per element of the q, k, v rows
+    constexpr int NR = SA == 1 ? 2 : 1;  // 16-byte loads per 8 elements
     constexpr int KS = HD / 16;          // MFMA steps along head_dim for S^T
     constexpr int DT = HD / 32;          // 32-wide output tiles along head_dim
     constexpr int C8 = HD / 8;           // 16-byte chunks per key row
@@ -100,12 +107,39 @@ void prefill_kernel(PrefillParams p) {
     const int kend = p.causal ? min(p.n_kv, p.p0 + last_row + 1) : p.n_kv;
     const int nblk = (kend + KB - 1) / KB;  // steps of KB keys
 
-    const half_t * kg = p.k + bkv + (int64_t)kvh * HD;
-    const half_t * vg = p.v + bkv + (int64_t)kvh * HD;
+    const int64_t hstride = SA ? p.head_stride : HD;  // elements between consecutive heads of a row
+    const char * kg = reinterpret_cast<const char *>(p.k) + (bkv + (int64_t)kvh * hstride) * ES;
+    const char * vg = reinterpret_cast<const char *>(p.v) + (bkv + (int64_t)kvh * hstride) * ES;
+    // 8 elements of column col (a multiple of 8) from byte address a, as loaded (NR 16-byte words); columns past the
+    // rows' head_dim load the row's last 8 instead (a valid address; half8() then gives zeros)
+    auto ld8 = [&](const char * row, int col, u32x4 (&r)[NR]) __attribute__((always_inline)) {
+        const int c = SA ? min(col, p.hdv - 8) : col;
+#pragma unroll
+        for (int j = 0; j < NR; j++) r[j] = load16(row + (int64_t)c * ES + 16 * j);
+    };
+    auto half8 = [&](const u32x4 (&r)[NR], int col) __attribute__((always_inline)) -> u32x4 {
+        if constexpr (SA == 0 || SA == 3) {
+            if (SA == 3 && col >= p.hdv) return u32x4{0u, 0u, 0u, 0u};
+            return r[0];
+        } else {
+            float x[8];
+            if constexpr (SA == 1) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[e] = __uint_as_float(r[0][e]);
+                    x[4 + e] = __uint_as_float(r[NR - 1][e]);
+                }
+            } else {
+                bf16x8_to_f32(r[0], x);
+            }
+            if (col >= p.hdv) return u32x4{0u, 0u, 0u, 0u};
+            return to_half8(x);
+        }
+    };
     // tile-load mapping, block b = i * W + wave of 16 rows x 4 chunks (64 contiguous bytes per row):
     //   K: row 16 (b % 4) + lane % 16, chunk 4 (b / 4) + lane / 16 (16 lanes of one LDS write phase: 16 rows, one chunk)
     //   V: row 16 (b % 4) + 4 (lane / 16) + (lane % 16) / 4, chunk 4 (b / 4) + lane % 4 (16 lanes: 4 rows x 4 chunks)
-    u32x4 kreg[NI], vreg[NI];
+    u32x4 kreg[NI][NR], vreg[NI][NR];
     auto krow = [&](int b) { return 16 * (b % (KB / 16)) + lane % 16; };
     auto kchunk = [&](int b) { return 4 * (b / (KB / 16)) + lane / 16; };
     auto vrow = [&](int b) { return 16 * (b % (KB / 16)) + 4 * (lane / 16) + (lane % 16) / 4; };
@@ -115,16 +149,16 @@ void prefill_kernel(PrefillParams p) {
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
             const int kkey = min(kb + krow(b), p.n_kv - 1), vkey = min(kb + vrow(b), p.n_kv - 1);
-            kreg[i] = load16(kg + (int64_t)kkey * p.kv_stride + 8 * kchunk(b));
-            vreg[i] = load16(vg + (int64_t)vkey * p.kv_stride + 8 * vchunk(b));
+            ld8(kg + (int64_t)kkey * p.kv_stride * ES, 8 * kchunk(b), kreg[i]);
+            ld8(vg + (int64_t)vkey * p.kv_stride * ES, 8 * vchunk(b), vreg[i]);
         }
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
-            *reinterpret_cast<u32x4 *>(&sm.k[buf][krow(b) * KP + 8 * kchunk(b)]) = kreg[i];
-            *reinterpret_cast<u32x4 *>(&sm.v[buf][vrow(b) * VP + 8 * vchunk(b)]) = vreg[i];
+            *reinterpret_cast<u32x4 *>(&sm.k[buf][krow(b) * KP + 8 * kchunk(b)]) = half8(kreg[i], 8 * kchunk(b));
+            *reinterpret_cast<u32x4 *>(&sm.v[buf][vrow(b) * VP + 8 * vchunk(b)]) = half8(vreg[i], 8 * vchunk(b));
         }
     };
 
@@ -145,12 +179,15 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(x[ks]));
     } else {
-        const half_t * qp = p.q + bq + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
+        const char * qp = reinterpret_cast<const char *>(p.q) + (bq + (int64_t)qrow * p.q_stride + (int64_t)h * hstride) * ES;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (qrow < p.n_q) v = load16(qp + 16 * ks);
-            qb[ks] = as_half8(v);
+            const int col = 16 * ks + 8 * hgrp;
+            u32x4 r[NR];
+#pragma unroll
+            for (int j = 0; j < NR; j++) r[j] = u32x4{0u, 0u, 0u, 0u};
+            if (qrow < p.n_q) ld8(qp, col, r);
+            qb[ks] = as_half8(half8(r, col));
         }
     }
     if (nblk > 0) {
@@ -333,12 +370,28 @@ void prefill_kernel(PrefillParams p) {
     // ---- normalize and store: lane holds O[qrow][32 dt + 8 (v / 4) + 4 hgrp + v % 4] ----
     if (qrow < p.n_q) {
         const float inv = 1.f / l_run;
-        const int64_t off = (int64_t)qrow * p.out_stride + (int64_t)h * HD + 4 * hgrp;
+        const int64_t off = (int64_t)qrow * p.out_stride + (int64_t)h * hstride + 4 * hgrp;
 #pragma unroll
         for (int dt = 0; dt < DT; dt++)
 #pragma unroll
             for (int gq = 0; gq < 4; gq++) {
-                if constexpr (ROPE) {
+                if constexpr (SA) {
+                    const int col = 32 * dt + 8 * gq + 4 * hgrp;
+                    if (col >= p.hdv) continue;
+                    float r[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) r[e] = o[dt][4 * gq + e] * inv;
+                    if constexpr (SA == 1) {
+                        *reinterpret_cast<float4_t *>(p.out32 + bo + off + 32 * dt + 8 * gq) = float4_t{r[0], r[1], r[2], r[3]};
+                    } else if constexpr (SA == 2) {
+                        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.out) + bo + off + 32 * dt + 8 * gq) =
+                            u32x2{(uint32_t)to_bf16(r[0]) | ((uint32_t)to_bf16(r[1]) << 16),
+                                  (uint32_t)to_bf16(r[2]) | ((uint32_t)to_bf16(r[3]) << 16)};
+                    } else {
+                        *reinterpret_cast<half4_t *>(p.out + bo + off + 32 * dt + 8 * gq) =
+                            half4_t{(half_t)r[0], (half_t)r[1], (half_t)r[2], (half_t)r[3]};
+                    }
+                } else if constexpr (ROPE) {
                     float4_t r;
 #pragma unroll
                     for (int e = 0; e < 4; e++) r[e] = o[dt][4 * gq + e] * inv;
@@ -433,10 +486,6 @@ __global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams 
 }
 
 // one thread per 4 consecutive outputs of a head (head_dim a multiple of 4), else per output
-__device__ __forceinline__ uint16_t to_bf16(float v) {  // round to nearest even; NaN stays a (quiet) NaN
-    const uint32_t b = __float_as_uint(v);
-    return v != v ? (uint16_t)0x7FC0u : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
-}
 
 __global__ __launch_bounds__(256) void self_attn_unpack_kernel(SelfAttnUnpackParams p) {
     const int H = p.heads, hd = p.hd, E = H * hd;
@@ -478,36 +527,39 @@ hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t s
     return hipGetLastError();
 }
 
-template <int HD, bool POS, bool ROPE>
+template <int HD, bool POS, bool ROPE, int SA>
 void launch_prefill_r(const PrefillParams & p, int plan, int n_batch, hipStream_t stream) {
     const dim3 grid((uint32_t)p.n_qtiles * p.n_head, (uint32_t)n_batch);
-    if (plan == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE, 1>), grid, dim3(8 * kWave), 0, stream, p);
-    else if (plan == 4) hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 1>), grid, dim3(4 * kWave), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 2>), grid, dim3(4 * kWave), 0, stream, p);
+    if (plan == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE, 1, SA>), grid, dim3(8 * kWave), 0, stream, p);
+    else if (plan == 4) hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 1, SA>), grid, dim3(4 * kWave), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 2, SA>), grid, dim3(4 * kWave), 0, stream, p);
 }
 
 template <int HD, bool POS>
-void launch_prefill_t(const PrefillParams & p, int plan, int n_batch, hipStream_t stream) {
-    if (p.rope) launch_prefill_r<HD, POS, true>(p, plan, n_batch, stream);
-    else launch_prefill_r<HD, POS, false>(p, plan, n_batch, stream);
+void launch_prefill_t(const PrefillParams & p, int plan, int n_batch, int sa, hipStream_t stream) {
+    if (sa == 1) launch_prefill_r<HD, POS, false, 1>(p, plan, n_batch, stream);
+    else if (sa == 2) launch_prefill_r<HD, POS, false, 2>(p, plan, n_batch, stream);
+    else if (sa == 3) launch_prefill_r<HD, POS, false, 3>(p, plan, n_batch, stream);
+    else if (p.rope) launch_prefill_r<HD, POS, true, 0>(p, plan, n_batch, stream);
+    else launch_prefill_r<HD, POS, false, 0>(p, plan, n_batch, stream);
 }
 
-hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, hipStream_t stream) {
+hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, int sa, hipStream_t stream) {
     const bool pos = p.scale_log2 > 0.f;
     const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv);
     if (p.n_qtiles != (p.n_q + 32 * plan - 1) / (32 * plan)) return hipErrorInvalidValue;  // planned with other inputs
     if (head_dim == 64) {
-        if (pos) launch_prefill_t<64, true>(p, plan, n_batch, stream);
-        else launch_prefill_t<64, false>(p, plan, n_batch, stream);
+        if (pos) launch_prefill_t<64, true>(p, plan, n_batch, sa, stream);
+        else launch_prefill_t<64, false>(p, plan, n_batch, sa, stream);
     } else {
-        if (pos) launch_prefill_t<128, true>(p, plan, n_batch, stream);
-        else launch_prefill_t<128, false>(p, plan, n_batch, stream);
+        if (pos) launch_prefill_t<128, true>(p, plan, n_batch, sa, stream);
+        else launch_prefill_t<128, false>(p, plan, n_batch, sa, stream);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream) {
-    return launch_prefill_batched(p, head_dim, 1, stream);
+    return launch_prefill_batched(p, head_dim, 1, 0, stream);
 }
 
 }  // namespace mx

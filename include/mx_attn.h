@@ -226,10 +226,10 @@ typedef struct mx_self_attn_desc {
 } mx_self_attn_desc;
 
 /*
- * Device workspace bytes mx_self_attention needs: 0 for f16 input with head_dim 64 or 128 (the kernel reads the packed
- * rows in place); for f32 input with head_dim 64 or 128 the keys and values as f16 (2 B N E halves; the reference's GPU
- * path makes the same f16 copy, ggml_backend.cpp:332-335); for any other head_dim or bf16 the operands padded to
- * head_dim 64 or 128. Returns 0 and sets the last error for an invalid descriptor.
+ * Device workspace bytes mx_self_attention needs: 0 when head_dim is a multiple of 8 (the kernel reads the packed rows
+ * in place in every dtype, rounding Q, K and V to half as it loads them, as the reference's GPU path rounds them,
+ * ggml_backend.cpp:332-335); for any other head_dim the operands padded to head_dim 64 or 128. Returns 0 and sets the
+ * last error for an invalid descriptor.
  */
 MX_ATTN_API size_t mx_self_attention_workspace_bytes(const mx_self_attn_desc * desc);
 
@@ -237,8 +237,9 @@ MX_ATTN_API size_t mx_self_attention_workspace_bytes(const mx_self_attn_desc * d
  * SelfAttention on the GPU. Replaces the reference's lowering of the op (ggml_backend.cpp:398-412: the fused
  * ggml_flash_attn_ext of lower_attention_fused, :325-340, the unfused chain of :342-356 for head dims flash attention does
  * not take, and the CPU op attention_cpu_op, :292-312). One prefill-kernel launch (non-causal, every batch element along
- * the grid) on the packed rows, plus a packing launch before and an unpacking launch after it when the head_dim or dtype
- * needs them. Scores and accumulation are f32 over half operands (as the reference's GPU path, which rounds Q/K/V to half).
+ * the grid) on the packed rows, plus a packing launch before and an unpacking launch after it when head_dim is not a
+ * multiple of 8. Scores and accumulation are f32 over half operands (as the reference's GPU path, which rounds Q/K/V to
+ * half).
  *
  *   qkv        device, [batch][n_tok][3 embed] of desc->dtype, contiguous, 16-byte aligned
  *   y          device, [batch][n_tok][embed] of desc->dtype, contiguous, 16-byte aligned, not overlapping qkv

@@ -281,12 +281,14 @@ def test_self_attention_checks():
     assert call(sd(), qkv=A + 4) == _lib.INVALID_ARGUMENT and "aligned" in _lib.last_error()
     assert call(sd(), y=A) == _lib.INVALID_ARGUMENT and "overlaps" in _lib.last_error()
     assert call(sd(n_tok=0), qkv=0, y=0) == _lib.OK
-    # workspace: none for f16 at head_dim 64/128, the f16 K/V copy for f32 there, padded operands otherwise
-    assert _lib.self_attention_workspace_bytes(sd(heads=20, dtype=_lib.DTYPE_F16)) == 0
-    assert _lib.self_attention_workspace_bytes(sd(heads=20)) == 210 * 2 * 1280 * 2
-    w = 210 * 16 * 128  # ViT-H: head_dim 80 padded to 128
-    assert _lib.self_attention_workspace_bytes(sd()) == w * 4 + w * 4 + w * 4
-    n = _lib.self_attention_workspace_bytes(sd())
-    assert call(sd(), ws_bytes=n - 1) == _lib.RESOURCE_EXHAUSTED
-    assert call(sd(), ws=0, ws_bytes=n) == _lib.INVALID_ARGUMENT
-    assert call(sd(), ws=A + 16, ws_bytes=n) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
+    # workspace: none when head_dim is a multiple of 8 (the rows are read in place, any dtype), padded operands otherwise
+    for dt in (_lib.DTYPE_F32, _lib.DTYPE_F16, _lib.DTYPE_BF16):
+        assert _lib.self_attention_workspace_bytes(sd(heads=20, dtype=dt)) == 0  # head_dim 64
+        assert _lib.self_attention_workspace_bytes(sd(dtype=dt)) == 0            # ViT-H: head_dim 80
+    w = 210 * 16 * 64  # head_dim 6 padded to 64: f32 Q, f16 K and V, f32 O
+    odd = sd(embed=16 * 6)
+    assert _lib.self_attention_workspace_bytes(odd) == w * 4 + w * 2 * 2 + w * 4
+    n = _lib.self_attention_workspace_bytes(odd)
+    assert call(odd, ws_bytes=n - 1) == _lib.RESOURCE_EXHAUSTED
+    assert call(odd, ws=0, ws_bytes=n) == _lib.INVALID_ARGUMENT
+    assert call(odd, ws=A + 16, ws_bytes=n) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
