@@ -68,11 +68,12 @@ struct PrefillParams {
     float rope_freq[kMaxHeadDim / 2];
 };
 
-// Packing of the IR self-attention's [B][N][3E] q|k|v rows (f32 or f16) into the attention kernel's operands when the
-// rows cannot be read in place: f32 query rows and f16 key|value rows with head_dim padded to hdp (zeros), and back.
+// Packing of the IR self-attention's [B][N][3E] q|k|v rows into the attention kernel's operands when the rows cannot be
+// read in place (head_dim not a multiple of 8): f32 query rows and f16 key|value rows with head_dim padded to hdp
+// (zeros), and back.
 struct SelfAttnPackParams {
     const void * qkv;     // [rows][3 E], of dtype (0 f32, 1 f16, 2 bf16)
-    float * q;            // [rows][H hdp] f32, or null (the query is read in place)
+    float * q;            // [rows][H hdp] f32
     half_t * kv;          // [rows][2 H hdp] f16: keys at column 0, values at column H hdp
     int64_t rows;         // B N
     int32_t heads, hd, hdp, dtype;

@@ -447,7 +447,6 @@ __global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams 
     const int part = r / (H * (hdp / 8));  // 0 q, 1 k, 2 v
     r %= H * (hdp / 8);
     const int h = r / (hdp / 8), d0 = 8 * (r % (hdp / 8));
-    if (part == 0 && !p.q) return;
     float x[8];
     const int64_t src = row * 3 * E + (int64_t)part * E + (int64_t)h * hd + d0;
     if (hd % 8 == 0) {  // uniform: whole 8-wide groups, 16-byte (f16/bf16) or 2 x 16-byte (f32) loads, or padding
