@@ -406,7 +406,7 @@ def main():
                                    "K/V (1.07 GB per step)",
                        "batch": 1, "kv_len": L, "layers_per_step": 32, "n_head": 32, "n_head_kv": 8, "head_dim": 128,
                        "timing": "HIP graph replay of the 32-launch step, events on the launch stream"},
-            "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,4>", "achieved": round(achieved, 1),
+            "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,4,false,8>", "achieved": round(achieved, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic, "bytes_per_launch": bpl, "avg_launch_us": round(avg_us, 3),
                          "launch_timing": "graph-timed region / launches (includes the gaps between launches)"},
@@ -484,7 +484,7 @@ def main():
                            "chunks of 2048 queries against the growing f16 cache, N(0, 0.5) inputs; FLOPs count "
                            "unmasked pairs only (7.697 TFLOP per step)",
                "flops_per_step": fl,
-               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128,true,8>", "achieved": round(tflops, 1),
+               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128,true,8,false,1,0>", "achieved": round(tflops, 1),
                             "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / F16_PEAK_TFLOPS, 4),
                             "traffic": measured_traffic("prefill_qwen7b_32k"), "avg_launch_us": round(avg_us, 2),
                             "launch_timing": "graph-timed region / launches; FLOPs per launch differ by chunk, so "
