@@ -150,30 +150,50 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         }
     }
 
-    // the first block of keys and values goes out right behind the query
-    int jb = j0 + kBlockKeys * wave;
-    B cur, nxt;
-    if (jb < j1) load_block(jb, cur);
-
     // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
     const int jb_new = (L - 1) & ~(kBlockKeys - 1);
     const bool wave_new = F32 && p.append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % NW == wave;
     const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
     const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
-    u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
-    if constexpr (F32) {  // fused step: the query and the new key rotated, the new key and value rounded to half
+    // The fused step's own loads (the new key and value, the rotary frequencies) go out before the first block of keys
+    // and values: a wait for them then leaves that block's loads in flight (loads complete in the order issued).
+    float x[F32 ? KS : 1][8], xv[8], freq = 0.f;
+    if constexpr (F32) {
         const float * row = p.qkv + seq_row0 * p.q_stride;
-        float x[KS][8], xv[8];
         if (k_lane_new) {
             const float * kr = row + (int64_t)(p.n_head + g) * HD + 8 * sgrp;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(kr + 32 * ks, x[ks]);
         }
         if (v_lane_new) load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, xv);
+        // uniform indices: scalar loads from the kernel arguments (an index per lane would make it a vector load,
+        // which waits behind the whole chip's K/V burst)
+#pragma unroll
+        for (int i = 0; i < HD / 2; i++)
+            if (threadIdx.x == i) freq = p.rope_freq[i];
+    }
+
+    // the first block of keys and values goes out right behind the query (unconditionally: keys past the split are
+    // clamped to valid rows and never used, and the compiler then knows how many loads follow the ones above)
+    int jb = j0 + kBlockKeys * wave;
+    B cur, nxt;
+    load_block(jb, cur);
+    if constexpr (F32) {
+        // the new key and value are used only from here on, so any wait for them leaves the block's loads in flight
+#pragma unroll
+        for (int e = 0; e < 8; e++) asm volatile("" : "+v"(xv[e])::"memory");
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) asm volatile("" : "+v"(x[ks][e])::"memory");
+    }
+
+    u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
+    if constexpr (F32) {  // fused step: the query and the new key rotated, the new key and value rounded to half
         if (p.append && p.rope_mode != 2) {  // the 64 (hd 128) angles of position L - 1, once per workgroup
             if (threadIdx.x < HD / 2) {
                 float sn, cs;
-                sincos_rope((float)(L - 1) * p.rope_freq[threadIdx.x], sn, cs);
+                sincos_rope((float)(L - 1) * freq, sn, cs);
                 s_cs[threadIdx.x] = make_float2(cs, sn);
             }
             __syncthreads();
