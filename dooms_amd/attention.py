@@ -25,8 +25,10 @@ def _rows(t: torch.Tensor, name: str, dtype=torch.float16) -> torch.Tensor:
 
 
 def prefill(q, k_cache, v_cache, *, n_head, n_head_kv, head_dim, p0=0, causal=True, n_kv=None, scale=None,
-            out=None, lse=None, want_lse=False):
-    """mx_attn_prefill: q [n_q][>= n_head*hd], caches [n_kv][>= n_head_kv*hd]. Returns (out, lse or None)."""
+            out=None, lse=None, want_lse=False, workspace=None):
+    """mx_attn_prefill: q [n_q][>= n_head*hd], caches [n_kv][>= n_head_kv*hd]. Returns (out, lse or None).
+    workspace: "auto" (sized and zeroed here) or a zeroed uint8 device tensor runs mx_attn_prefill_ws, which takes the
+    split-KV kernel for chunks of few rows; None runs mx_attn_prefill."""
     _rows(q, "q"), _rows(k_cache, "k_cache"), _rows(v_cache, "v_cache")
     if k_cache.stride(0) != v_cache.stride(0):
         raise ValueError("k_cache and v_cache must share a row stride")
@@ -40,8 +42,15 @@ def prefill(q, k_cache, v_cache, *, n_head, n_head_kv, head_dim, p0=0, causal=Tr
         scale = 1.0 / math.sqrt(head_dim)
     d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, q.stride(0), k_cache.stride(0), out.stride(0), scale,
                        p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0)
-    _lib.check(_lib.prefill_raw(d, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
-                                lse.data_ptr() if lse is not None else 0, _stream()))
+    if workspace is None:
+        _lib.check(_lib.prefill_raw(d, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                    lse.data_ptr() if lse is not None else 0, _stream()))
+        return out, lse
+    if isinstance(workspace, str):
+        workspace = new_workspace(_lib.prefill_workspace_bytes(d), q.device)
+    _lib.check(_lib.prefill_ws_raw(d, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                   lse.data_ptr() if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
+                                   _stream()))
     return out, lse
 
 

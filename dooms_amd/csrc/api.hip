@@ -111,7 +111,8 @@ struct WsLayout {
 WsLayout decode_ws_layout(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len) {
     const DecodeShape s = decode_shape(d);
     const int64_t seqs = std::min<int64_t>(batch, mx::kMaxSeqPerLaunch);
-    const int64_t max_split = ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum;
+    // the split plan never makes more than kMaxSplits splits of a sequence, nor more than one per quantum of keys
+    const int64_t max_split = std::min<int64_t>(kMaxSplits, ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum);
     WsLayout w{0, 0};
     if (max_split <= 1) return w;  // one split per sequence: no partials, no counters
     w.counter_bytes = (size_t)((seqs * d->n_head_kv * s.n_rowtiles * 4 + 255) / 256 * 256);
@@ -316,6 +317,22 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     return MX_ATTN_OK;
 }
 
+// ---- prefill chunks on the split-KV decode kernel ----
+// A chunk whose rows per kv head (n_q x group, the decode kernel's packed GQA rows) are at most kPrefillSplitRows runs
+// on the decode kernel: its causal rows at the end of the cache are the chunk's own semantics (row t sees keys
+// 0 .. p0 + t), and it spreads the keys over the CUs, which the flash kernel (one workgroup per head and query tile,
+// every workgroup walking all keys) cannot. Measured (28 q / 4 kv heads, hd 128): 2 rows at 30k keys 610 -> 28 us, 16
+// rows 611 -> 74 us, 128 rows 598 -> 306 us; at 256 rows and 4k keys the flash kernel wins (87 vs 113 us).
+constexpr int64_t kPrefillSplitRows = 512;
+bool prefill_split_route(const mx_attn_desc & d) {
+    return d.n_q >= 1 && (int64_t)d.n_q * (d.n_head / d.n_head_kv) <= kPrefillSplitRows;
+}
+// keys the decode kernel walks: a causal chunk's rows see keys up to p0 + n_q - 1 (keys past them are masked anyway)
+int64_t prefill_split_keys(const mx_attn_desc & d) {
+    if (d.causal) return (int64_t)d.p0 + d.n_q;
+    return d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
+}
+
 // ---- IR SelfAttention (src/ir/op.h:31-32) ----
 
 int32_t check_self_attn(const mx_self_attn_desc * d) {
@@ -464,6 +481,33 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
                                     uint16_t * out, float * lse, mx_attn_stream stream) {
     if (int32_t rc = check_desc(desc)) return rc;
     return prefill_impl(desc, q, k_cache, v_cache, out, lse, stream, nullptr);
+}
+
+MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc) {
+    if (check_desc(desc)) return 0;
+    if (!prefill_split_route(*desc)) return 0;
+    const int64_t L = prefill_split_keys(*desc);
+    if (L < 1 || L > INT32_MAX) return 0;
+    return decode_ws_bytes(desc, 1, (int32_t)L);
+}
+
+MX_ATTN_API int32_t mx_attn_prefill_ws(const mx_attn_desc * desc, const uint16_t * q, const uint16_t * k_cache,
+                                       const uint16_t * v_cache, uint16_t * out, float * lse, void * workspace,
+                                       size_t ws_bytes, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    const mx_attn_desc & d = *desc;
+    if (!workspace || !prefill_split_route(d)) return prefill_impl(desc, q, k_cache, v_cache, out, lse, stream, nullptr);
+    if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
+    if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
+    if (d.n_q == 0) return MX_ATTN_OK;
+    if (d.causal && d.n_kv != 0 && d.n_kv < (int64_t)d.p0 + d.n_q)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= p0 + n_q (%lld): the chunk's own rows are in the cache",
+                    d.n_kv, (long long)d.p0 + d.n_q);
+    const int64_t L = prefill_split_keys(d);
+    if (L > INT32_MAX) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 + n_q overflows");
+    const int32_t kv_len = (int32_t)L;
+    const void * kp = k_cache, * vp = v_cache;
+    return decode_impl(desc, 1, &kv_len, q, &kp, &vp, out, lse, workspace, ws_bytes, stream, nullptr, false);
 }
 
 MX_ATTN_API int32_t mx_attn_prefill_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, const float * qkv, uint16_t * k_cache,

@@ -108,8 +108,16 @@ public:
         if (c.head_dim != 64 && c.head_dim != 128)
             return {Code::Unsupported, "head_dim " + std::to_string(c.head_dim) + " is not supported (64 or 128)"};
         std::unique_ptr<LlamaAttention> a(new LlamaAttention(c, k_cache, v_cache, stream));
+        // one workspace for the decode rows and for the prompt chunks of few rows that mx_attn_prefill_ws runs on the
+        // split-KV kernel (up to 512 rows per kv head), at the full context
         mx_attn_desc d = a->desc(1, 0, 0);
-        if (Status st = a->ws_.reserve(mx_attn_decode_workspace_bytes(&d, 1, c.n_ctx), stream); !st.is_ok()) return st;
+        size_t bytes = mx_attn_decode_workspace_bytes(&d, 1, c.n_ctx);
+        const int32_t m_split = std::min<int32_t>(c.n_ctx, std::max(1, 512 / (c.n_head / c.n_head_kv)));
+        mx_attn_desc dp = a->desc(m_split, 0, 0);
+        dp.p0 = c.n_ctx - m_split;
+        dp.causal = 1;
+        bytes = std::max(bytes, mx_attn_prefill_workspace_bytes(&dp));
+        if (Status st = a->ws_.reserve(bytes, stream); !st.is_ok()) return st;
         out = std::move(a);
         return {};
     }
@@ -137,8 +145,9 @@ public:
     }
 
     // Attention of M query rows at positions p0 .. p0 + M - 1 of layer l over cache rows 0 .. p0 + M - 1 (already
-    // appended): one decode row (M == 1) through the split-KV decode path, a prompt chunk through flash prefill. q rows
-    // are q_stride halves apart, out rows out_stride.
+    // appended): one decode row (M == 1) through the split-KV decode path, a prompt chunk through mx_attn_prefill_ws
+    // (flash prefill, or the split-KV kernel for chunks of few rows). q rows are q_stride halves apart, out rows
+    // out_stride.
     Status attention(int32_t layer, const uint16_t * q, int64_t q_stride, uint16_t * out, int64_t out_stride, int32_t M,
                      int32_t p0) {
         if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
@@ -155,7 +164,7 @@ public:
         mx_attn_desc d = desc(M, q_stride, out_stride);
         d.p0 = p0;
         d.causal = 1;
-        return Status::from(mx_attn_prefill(&d, q, k, v, out, nullptr, stream_));
+        return Status::from(mx_attn_prefill_ws(&d, q, k, v, out, nullptr, ws_.data(), ws_.size(), stream_));
     }
 
     // A prompt chunk of M tokens at positions p0 .. p0 + M - 1 on the reference's buffers (rope_store + attention with

@@ -103,6 +103,26 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
                                     const uint16_t * v_cache, uint16_t * out, float * lse, mx_attn_stream stream);
 
 /*
+ * mx_attn_prefill with a workspace: a chunk of few rows (n_q * n_head / n_head_kv <= 512) runs on the split-KV decode
+ * kernel, which spreads a long cache over the whole chip (the flash kernel has one workgroup per head and 256 query rows,
+ * each walking every key): for example 16 rows of a 28 q / 4 kv-head model at 30k keys, 611 -> 74 us. Larger chunks,
+ * and any call with workspace == NULL, run the flash kernel exactly as mx_attn_prefill. Same arguments, semantics and
+ * results within the stated tolerance (the summation order differs). No counterpart in the reference, whose chunks
+ * always take attention_prefill; the extra argument is the decode workspace:
+ *
+ *   workspace  device, 256-byte aligned, at least mx_attn_prefill_workspace_bytes(desc) bytes, zeroed once by
+ *              mx_attn_decode_workspace_init; every call leaves its counters at zero. Calls sharing it (with each other
+ *              or with mx_attn_decode) must be ordered on one stream. NULL runs the flash kernel.
+ */
+MX_ATTN_API int32_t mx_attn_prefill_ws(const mx_attn_desc * desc, const uint16_t * q, const uint16_t * k_cache,
+                                       const uint16_t * v_cache, uint16_t * out, float * lse, void * workspace,
+                                       size_t ws_bytes, mx_attn_stream stream);
+
+/* Workspace bytes mx_attn_prefill_ws needs for desc (0 when the chunk runs on the flash kernel); 0 and the last error
+ * set for an invalid descriptor. */
+MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc);
+
+/*
  * Decode attention over per-sequence caches: split-KV over the keys, then a log-sum-exp merge of the splits. Replaces the
  * per-query `attention` kernel (llama_kernels.h:552-630; decode dispatch metal_llama_decoder.mm:298-306, Whisper self
  * attention metal_whisper_decoder.mm:167-203) and attention_split + attention_combine (llama_kernels.h:856-929; long

@@ -179,10 +179,28 @@ def test_workspace_size():
     assert ws(1, 1) == 0 and ws(1, 128) == 0  # one split: no partials
     assert ws(1, 129) > 0
     assert ws(1, 8192) <= ws(1, 8193) <= ws(4, 8193) <= ws(32, 8193) == ws(100, 8193)  # launches of 32 reuse it
-    # counters (256-byte padded) plus 8192/128 = 64 splits x 8 kv heads x 4 rows x (128 + 4) floats
-    assert ws(1, 8192) == 256 + 64 * 8 * 4 * 132 * 4
+    # counters (256-byte padded) plus min(8192/128, 32) = 32 splits x 8 kv heads x 4 rows x (128 + 4) floats
+    assert ws(1, 8192) == 256 + 32 * 8 * 4 * 132 * 4
+    assert ws(1, 4096) == ws(1, 8192) and ws(1, 2048) == 256 + 16 * 8 * 4 * 132 * 4
     assert _lib.decode_workspace_bytes(desc(n_head=3, n_head_kv=2), 1, 1000) == 0
     assert "multiple" in _lib.last_error()
+
+
+def test_prefill_ws_checks():
+    # the split-KV route for chunks of few rows: a decode workspace sized for the chunk's rows over p0 + n_q keys
+    d16 = desc(n_head=28, n_head_kv=4, n_q=16, p0=30000, q_stride=3584, kv_stride=512, out_stride=3584)
+    n = _lib.prefill_workspace_bytes(d16)  # 16 x 7 rows: 7 row tiles of 16 per kv head
+    assert n == 256 + 32 * 4 * 7 * 16 * 132 * 4
+    big = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584)
+    assert _lib.prefill_workspace_bytes(big) == 0  # the flash kernel, no workspace
+    assert _lib.prefill_workspace_bytes(desc(n_head=3, n_head_kv=2)) == 0 and "multiple" in _lib.last_error()
+    call = lambda d, ws=A, nb=1 << 40: _lib.prefill_ws_raw(d, A, A, A, A, 0, ws, nb, 0)
+    assert call(d16, nb=n - 1) == _lib.RESOURCE_EXHAUSTED and "workspace" in _lib.last_error()
+    assert call(d16, ws=A + 16) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
+    bad = desc(n_head=28, n_head_kv=4, n_q=16, p0=100, n_kv=50, q_stride=3584, kv_stride=512, out_stride=3584)
+    assert call(bad) == _lib.INVALID_ARGUMENT and "n_kv" in _lib.last_error()
+    assert call(desc(n_head=28, n_head_kv=4, n_q=16, p0=-1, q_stride=3584, kv_stride=512, out_stride=3584)) == \
+        _lib.INVALID_ARGUMENT
 
 
 def test_last_error_is_per_thread():

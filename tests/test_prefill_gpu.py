@@ -24,7 +24,7 @@ def make(device, seed, n_q_total, n_head, n_head_kv, hd, sigma=1.0, kv_pad=0, q_
 
 
 def check_prefill(device, seed, N, n_head, n_head_kv, hd, rows=None, heads=None, causal=True, sigma=1.0, scale=None,
-                  kv_pad=0, q_pad=0, chunk=None):
+                  kv_pad=0, q_pad=0, chunk=None, workspace=None):
     q, k, v, (dq, dk, dv) = make(device, seed, N, n_head, n_head_kv, hd, sigma, kv_pad, q_pad)
     scale = 1.0 / np.sqrt(hd) if scale is None else scale
     if chunk is None:
@@ -36,7 +36,7 @@ def check_prefill(device, seed, N, n_head, n_head_kv, hd, rows=None, heads=None,
         for p0 in range(0, N, chunk):
             m = min(chunk, N - p0)
             A.prefill(dq[p0:p0 + m], dk[:p0 + m], dv[:p0 + m], n_head=n_head, n_head_kv=n_head_kv, head_dim=hd,
-                      p0=p0, scale=scale, out=out[p0:p0 + m], lse=lse[p0:p0 + m])
+                      p0=p0, scale=scale, out=out[p0:p0 + m], lse=lse[p0:p0 + m], workspace=workspace)
     torch.cuda.synchronize()
     got = out.cpu().numpy().astype(np.float64)
     gl = lse.cpu().numpy()
@@ -157,3 +157,34 @@ def test_workgroup_plans(device, monkeypatch, plan, case):
         check_prefill(device, 203, 257, 4, 1, 128)
     else:
         check_prefill(device, 204, 60, 4, 2, 64)
+
+
+# mx_attn_prefill_ws: chunks of few rows on the split-KV decode kernel (n_q x group <= 512), larger ones on the flash
+# kernel; the last chunk of each prompt is short, so every case below takes both routes
+@pytest.mark.parametrize("N,chunk,n_head,n_head_kv,hd", [(1000, 17, 28, 4, 128), (700, 64, 14, 2, 64),
+                                                         (3000, 2000, 32, 8, 128), (300, 1, 8, 8, 64)])
+def test_prefill_ws_routes(device, N, chunk, n_head, n_head_kv, hd):
+    rows = sorted(set(list(range(0, N, max(1, N // 60))) + [N - 1, N - 2, chunk - 1, chunk]))
+    rows = [r for r in rows if r < N]
+    check_prefill(device, 400 + N, N, n_head, n_head_kv, hd, rows=rows, chunk=chunk, workspace="auto")
+
+
+def test_prefill_ws_noncausal_and_extra_keys(device):
+    # non-causal rows over n_kv keys, and a causal chunk with cache rows past its own (masked, not read)
+    rng = np.random.default_rng(410)
+    L, M, hd = 5000, 12, 128
+    q = torch.from_numpy(normal_f16(rng, (M, 28 * hd))).to(device)
+    k = torch.from_numpy(normal_f16(rng, (L, 4 * hd))).to(device)
+    v = torch.from_numpy(normal_f16(rng, (L, 4 * hd))).to(device)
+    for causal, p0, n_kv in [(False, 0, L), (True, 3000, L)]:
+        a, la = A.prefill(q, k, v, n_head=28, n_head_kv=4, head_dim=hd, p0=p0, n_kv=n_kv, causal=causal,
+                          want_lse=True, workspace="auto")
+        b, lb = A.prefill(q, k, v, n_head=28, n_head_kv=4, head_dim=hd, p0=p0, n_kv=n_kv, causal=causal,
+                          want_lse=True)
+        torch.cuda.synchronize()
+        ro, rl = ref_attention(q.cpu().numpy(), k.cpu().numpy()[:n_kv], v.cpu().numpy()[:n_kv], 28, 4, hd,
+                               1 / np.sqrt(hd), p0=p0, causal=causal, heads=[0, 6, 7, 27])
+        cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in [0, 6, 7, 27]])
+        for out, lse in ((a, la), (b, lb)):
+            assert_close(out.cpu().numpy().astype(np.float64)[:, cols], ro, hd, f"causal={causal}",
+                         lse.cpu().numpy()[:, [0, 6, 7, 27]], rl)
