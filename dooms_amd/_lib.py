@@ -21,7 +21,7 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
 
 # Every symbol include/mx_attn.h declares.
 EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_prefill_ws",
-           "mx_attn_prefill_workspace_bytes", "mx_attn_prefill_rope", "mx_attn_decode",
+           "mx_attn_prefill_workspace_bytes", "mx_attn_prefill_rope", "mx_attn_prefill_rope_ws", "mx_attn_decode",
            "mx_attn_decode_f32", "mx_attn_decode_rope", "mx_linear", "mx_linear_workspace_bytes",
            "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init", "mx_self_attention",
            "mx_self_attention_workspace_bytes")
@@ -90,6 +90,9 @@ def lib() -> ctypes.CDLL:
         L.mx_attn_prefill.argtypes = [ctypes.POINTER(MxAttnDesc), P, P, P, P, P, P]
         L.mx_attn_prefill_ws.restype = ctypes.c_int32
         L.mx_attn_prefill_ws.argtypes = [ctypes.POINTER(MxAttnDesc), P, P, P, P, P, P, ctypes.c_size_t, P]
+        L.mx_attn_prefill_rope_ws.restype = ctypes.c_int32
+        L.mx_attn_prefill_rope_ws.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.POINTER(MxAttnRope), P, P, P, P, P, P,
+                                              ctypes.c_size_t, P]
         L.mx_attn_prefill_workspace_bytes.restype = ctypes.c_size_t
         L.mx_attn_prefill_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc)]
         L.mx_attn_decode.restype = ctypes.c_int32
@@ -145,6 +148,14 @@ def prefill_ws_raw(desc: MxAttnDesc, q: int, k: int, v: int, out: int, lse: int,
                    stream: int) -> int:
     """mx_attn_prefill_ws on raw device addresses; returns the code."""
     return lib().mx_attn_prefill_ws(ctypes.byref(desc), q, k, v, out, lse or None, ws or None, ws_bytes, stream or None)
+
+
+def prefill_rope_ws_raw(desc: MxAttnDesc, mode: int, base: float, qkv: int, k: int, v: int, out: int, lse: int,
+                        ws: int, ws_bytes: int, stream: int) -> int:
+    """mx_attn_prefill_rope_ws on raw device addresses; returns the code."""
+    rope = MxAttnRope(mode=mode, base=base)
+    return lib().mx_attn_prefill_rope_ws(ctypes.byref(desc), ctypes.byref(rope), qkv, k, v, out, lse or None,
+                                         ws or None, ws_bytes, stream or None)
 
 
 def prefill_workspace_bytes(desc: MxAttnDesc) -> int:

@@ -132,10 +132,11 @@ def decode_rope(qkv, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim,
 
 
 def prefill_rope(qkv, k_cache, v_cache, *, n_head, n_head_kv, head_dim, rope_mode, rope_base=10000.0, p0=0,
-                 causal=True, n_kv=None, scale=None, out=None, lse=None, want_lse=False):
+                 causal=True, n_kv=None, scale=None, out=None, lse=None, want_lse=False, workspace=None):
     """mx_attn_prefill_rope: qkv f32 [n_q][>= (n_head + 2 n_head_kv) hd] unrotated rows at positions p0 ..; their keys
     and values are written (rotated, f16) into rows p0 .. of k_cache / v_cache, then the chunk attends.
-    Returns (out f32 [n_q][n_head hd], lse or None)."""
+    Returns (out f32 [n_q][n_head hd], lse or None). workspace ("auto" or a zeroed uint8 device tensor) runs
+    mx_attn_prefill_rope_ws."""
     _rows(qkv, "qkv", torch.float32), _rows(k_cache, "k_cache"), _rows(v_cache, "v_cache")
     if k_cache.stride(0) != v_cache.stride(0):
         raise ValueError("k_cache and v_cache must share a row stride")
@@ -149,9 +150,16 @@ def prefill_rope(qkv, k_cache, v_cache, *, n_head, n_head_kv, head_dim, rope_mod
         scale = 1.0 / math.sqrt(head_dim)
     d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, qkv.stride(0), k_cache.stride(0), out.stride(0), scale,
                        p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0)
-    _lib.check(_lib.prefill_rope_raw(d, rope_mode, rope_base, qkv.data_ptr(), k_cache.data_ptr(),
-                                     v_cache.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else 0,
-                                     _stream()))
+    if workspace is None:
+        _lib.check(_lib.prefill_rope_raw(d, rope_mode, rope_base, qkv.data_ptr(), k_cache.data_ptr(),
+                                         v_cache.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else 0,
+                                         _stream()))
+        return out, lse
+    if isinstance(workspace, str):
+        workspace = new_workspace(_lib.prefill_workspace_bytes(d), qkv.device)
+    _lib.check(_lib.prefill_rope_ws_raw(d, rope_mode, rope_base, qkv.data_ptr(), k_cache.data_ptr(),
+                                        v_cache.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else 0,
+                                        workspace.data_ptr(), workspace.numel(), _stream()))
     return out, lse
 
 

@@ -197,6 +197,7 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
         r.n_rows = d.n_q;
         r.p0 = d.p0;
         r.rope_mode = rope->mode;
+        r.q_out = nullptr;
         fill_freq(r.rope_freq, rope, d.head_dim);
         if (int32_t rc = hip_status(mx::launch_rope_store(r, d.head_dim, st), "rope_store launch")) return rc;
     }
@@ -332,6 +333,8 @@ int64_t prefill_split_keys(const mx_attn_desc & d) {
     if (d.causal) return (int64_t)d.p0 + d.n_q;
     return d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
 }
+// workspace of the split route: the decode workspace, then (for mx_attn_prefill_rope_ws) the rotated f32 query rows
+size_t prefill_split_q_offset(const mx_attn_desc & d, int32_t L) { return (decode_ws_bytes(&d, 1, L) + 255) / 256 * 256; }
 
 // ---- IR SelfAttention (src/ir/op.h:31-32) ----
 
@@ -488,7 +491,7 @@ MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc) {
     if (!prefill_split_route(*desc)) return 0;
     const int64_t L = prefill_split_keys(*desc);
     if (L < 1 || L > INT32_MAX) return 0;
-    return decode_ws_bytes(desc, 1, (int32_t)L);
+    return prefill_split_q_offset(*desc, (int32_t)L) + (size_t)desc->n_q * desc->n_head * desc->head_dim * sizeof(float);
 }
 
 MX_ATTN_API int32_t mx_attn_prefill_ws(const mx_attn_desc * desc, const uint16_t * q, const uint16_t * k_cache,
@@ -515,6 +518,52 @@ MX_ATTN_API int32_t mx_attn_prefill_rope(const mx_attn_desc * desc, const mx_att
     if (int32_t rc = check_desc(desc)) return rc;
     if (int32_t rc = check_rope(*desc, rope)) return rc;
     return prefill_impl(desc, qkv, k_cache, v_cache, out, lse, stream, rope);
+}
+
+MX_ATTN_API int32_t mx_attn_prefill_rope_ws(const mx_attn_desc * desc, const mx_attn_rope * rope, const float * qkv,
+                                            uint16_t * k_cache, uint16_t * v_cache, float * out, float * lse,
+                                            void * workspace, size_t ws_bytes, mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    if (int32_t rc = check_rope(*desc, rope)) return rc;
+    const mx_attn_desc & d = *desc;
+    if (!workspace || !prefill_split_route(d)) return prefill_impl(desc, qkv, k_cache, v_cache, out, lse, stream, rope);
+    if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
+    if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
+    if (d.n_q == 0) return MX_ATTN_OK;
+    const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
+    if (n_kv > INT32_MAX) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 + n_q overflows");
+    if (n_kv < (int64_t)d.p0 + d.n_q)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%lld) must be >= p0 + n_q (%lld): the chunk's own rows are in the cache",
+                    (long long)n_kv, (long long)d.p0 + d.n_q);
+    if (!qkv || !k_cache || !v_cache || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "qkv, k_cache, v_cache and out must not be null");
+    if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "qkv, k_cache, v_cache and out must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    const int32_t L = (int32_t)prefill_split_keys(d);
+    const size_t q_off = prefill_split_q_offset(d, L);
+    const size_t need = q_off + (size_t)d.n_q * d.n_head * d.head_dim * sizeof(float);
+    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // the chunk's keys and values into the caches, its query rows rotated into the workspace, then the split-KV
+    // kernel on those f32 rows (rounded to half as it loads them, as the flash kernel's rotated path does)
+    mx::RopeStoreParams r;
+    r.qkv = qkv;
+    r.k = reinterpret_cast<mx::half_t *>(k_cache);
+    r.v = reinterpret_cast<mx::half_t *>(v_cache);
+    r.q_out = reinterpret_cast<float *>(static_cast<char *>(workspace) + q_off);
+    r.qkv_stride = d.q_stride;
+    r.kv_stride = d.kv_stride;
+    r.n_head = d.n_head;
+    r.n_head_kv = d.n_head_kv;
+    r.n_rows = d.n_q;
+    r.p0 = d.p0;
+    r.rope_mode = rope->mode;
+    fill_freq(r.rope_freq, rope, d.head_dim);
+    if (int32_t rc = hip_status(mx::launch_rope_store(r, d.head_dim, st), "rope_store launch")) return rc;
+    mx_attn_desc dq = d;
+    dq.q_stride = (int64_t)d.n_head * d.head_dim;
+    const void * kp = k_cache, * vp = v_cache;
+    return decode_impl(&dq, 1, &L, r.q_out, &kp, &vp, out, lse, workspace, q_off, stream, nullptr, true);
 }
 
 MX_ATTN_API size_t mx_attn_decode_workspace_bytes(const mx_attn_desc * desc, int32_t batch, int32_t max_kv_len) {

@@ -91,6 +91,7 @@ struct RopeStoreParams {
     const float * qkv;  // [n_rows][qkv_stride] f32: q | k | v
     half_t * k;
     half_t * v;
+    float * q_out;      // [n_rows][n_head head_dim] f32: the rotated query rows, or null (not written)
     int64_t qkv_stride, kv_stride;
     int32_t n_head, n_head_kv, n_rows, p0, rope_mode;
     float rope_freq[kMaxHeadDim / 2];

@@ -178,7 +178,8 @@ public:
         d.p0 = p0;
         d.causal = 1;
         const mx_attn_rope rope{cfg_.rope_neox ? 1 : 0, cfg_.rope_base};
-        return Status::from(mx_attn_prefill_rope(&d, &rope, qkv, k_layer(layer), v_layer(layer), out, nullptr, stream_));
+        return Status::from(mx_attn_prefill_rope_ws(&d, &rope, qkv, k_layer(layer), v_layer(layer), out, nullptr,
+                                                    ws_.data(), ws_.size(), stream_));
     }
 
     // One decode step of layer l at position p, the reference's attention(enc, cache_off, 1, p, fused_rope = true)

@@ -118,8 +118,8 @@ MX_ATTN_API int32_t mx_attn_prefill_ws(const mx_attn_desc * desc, const uint16_t
                                        const uint16_t * v_cache, uint16_t * out, float * lse, void * workspace,
                                        size_t ws_bytes, mx_attn_stream stream);
 
-/* Workspace bytes mx_attn_prefill_ws needs for desc (0 when the chunk runs on the flash kernel); 0 and the last error
- * set for an invalid descriptor. */
+/* Workspace bytes mx_attn_prefill_ws and mx_attn_prefill_rope_ws need for desc (0 when the chunk runs on the flash
+ * kernel); 0 and the last error set for an invalid descriptor. */
 MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc);
 
 /*
@@ -211,6 +211,16 @@ MX_ATTN_API int32_t mx_attn_decode_rope(const mx_attn_desc * desc, const mx_attn
 MX_ATTN_API int32_t mx_attn_prefill_rope(const mx_attn_desc * desc, const mx_attn_rope * rope, const float * qkv,
                                          uint16_t * k_cache, uint16_t * v_cache, float * out, float * lse,
                                          mx_attn_stream stream);
+
+/*
+ * mx_attn_prefill_rope with a workspace (sized by mx_attn_prefill_workspace_bytes, zeroed once by
+ * mx_attn_decode_workspace_init; NULL runs mx_attn_prefill_rope): a chunk of few rows (n_q * n_head / n_head_kv <= 512)
+ * writes its keys and values into the caches and its rotated query rows into the workspace, then attends on the
+ * split-KV decode kernel, as mx_attn_prefill_ws does. No counterpart in the reference.
+ */
+MX_ATTN_API int32_t mx_attn_prefill_rope_ws(const mx_attn_desc * desc, const mx_attn_rope * rope, const float * qkv,
+                                            uint16_t * k_cache, uint16_t * v_cache, float * out, float * lse,
+                                            void * workspace, size_t ws_bytes, mx_attn_stream stream);
 
 /*
  * Zero-fills a decode workspace on `stream` (with a kernel, not a memset, so that a caller may capture it in a HIP

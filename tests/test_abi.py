@@ -190,17 +190,28 @@ def test_prefill_ws_checks():
     # the split-KV route for chunks of few rows: a decode workspace sized for the chunk's rows over p0 + n_q keys
     d16 = desc(n_head=28, n_head_kv=4, n_q=16, p0=30000, q_stride=3584, kv_stride=512, out_stride=3584)
     n = _lib.prefill_workspace_bytes(d16)  # 16 x 7 rows: 7 row tiles of 16 per kv head
-    assert n == 256 + 32 * 4 * 7 * 16 * 132 * 4
+    # the decode workspace (counters, 32 splits of partials), then room for the rotated f32 query rows of the rope call
+    assert n == 256 + 32 * 4 * 7 * 16 * 132 * 4 + 16 * 28 * 128 * 4
     big = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584)
     assert _lib.prefill_workspace_bytes(big) == 0  # the flash kernel, no workspace
     assert _lib.prefill_workspace_bytes(desc(n_head=3, n_head_kv=2)) == 0 and "multiple" in _lib.last_error()
     call = lambda d, ws=A, nb=1 << 40: _lib.prefill_ws_raw(d, A, A, A, A, 0, ws, nb, 0)
-    assert call(d16, nb=n - 1) == _lib.RESOURCE_EXHAUSTED and "workspace" in _lib.last_error()
+    n_dec = n - 16 * 28 * 128 * 4  # mx_attn_prefill_ws itself needs only the decode part
+    assert call(d16, nb=n_dec - 1) == _lib.RESOURCE_EXHAUSTED and "workspace" in _lib.last_error()
     assert call(d16, ws=A + 16) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
     bad = desc(n_head=28, n_head_kv=4, n_q=16, p0=100, n_kv=50, q_stride=3584, kv_stride=512, out_stride=3584)
     assert call(bad) == _lib.INVALID_ARGUMENT and "n_kv" in _lib.last_error()
     assert call(desc(n_head=28, n_head_kv=4, n_q=16, p0=-1, q_stride=3584, kv_stride=512, out_stride=3584)) == \
         _lib.INVALID_ARGUMENT
+    # the rope variant: the same workspace, its tail holding the rotated f32 query rows
+    dr = desc(n_head=28, n_head_kv=4, n_q=16, p0=30000, q_stride=4608, kv_stride=512, out_stride=3584)
+    nr = _lib.prefill_workspace_bytes(dr)
+    assert nr == n
+    rcall = lambda d, ws=A, nb=1 << 40: _lib.prefill_rope_ws_raw(d, 0, 500000.0, A, A, A, A, 0, ws, nb, 0)
+    assert rcall(dr, nb=nr - 1) == _lib.RESOURCE_EXHAUSTED and "workspace" in _lib.last_error()
+    assert rcall(dr, ws=A + 16) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
+    assert rcall(desc(n_head=28, n_head_kv=4, n_q=16, q_stride=3584, kv_stride=512, out_stride=3584)) == \
+        _lib.INVALID_ARGUMENT and "q_stride" in _lib.last_error()
 
 
 def test_last_error_is_per_thread():

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run_prefill_rope(device, seed, n_head, n_head_kv, hd, M, p0, mode, base, spare=5, rows=None, heads=None,
-                     qkv_pad=0, kv_pad=0, n_kv=None, causal=True):
+                     qkv_pad=0, kv_pad=0, n_kv=None, causal=True, workspace=None):
     rng = np.random.default_rng(seed)
     qw, kvw = n_head * hd, n_head_kv * hd
     qkv = rng.standard_normal((M, qw + 2 * kvw + qkv_pad), dtype=np.float32)
@@ -30,7 +30,7 @@ def run_prefill_rope(device, seed, n_head, n_head_kv, hd, M, p0, mode, base, spa
     scale = 1.0 / np.sqrt(hd)
     out, lse = A.prefill_rope(torch.from_numpy(qkv).to(device), dk, dv, n_head=n_head, n_head_kv=n_head_kv,
                               head_dim=hd, rope_mode=mode, rope_base=base, p0=p0, n_kv=n_kv, causal=causal,
-                              want_lse=True)
+                              want_lse=True, workspace=workspace)
     torch.cuda.synchronize()
     out = out.cpu().numpy().astype(np.float64)
     lse = lse.cpu().numpy()
@@ -112,3 +112,13 @@ def test_workgroup_plans(device, monkeypatch, plan):
     monkeypatch.setenv("MX_PREFILL_PLAN", plan)
     run_prefill_rope(device, 300, 14, 2, 64, 300, 170, 1, 1000000.0)
     run_prefill_rope(device, 301, 8, 2, 128, 200, 0, 0, 500000.0)
+
+
+# mx_attn_prefill_rope_ws: chunks of few rows take the split-KV kernel (keys/values cached and queries rotated by
+# rope_store, then the decode kernel on the f32 query rows); larger ones the flash kernel
+@pytest.mark.parametrize("n_head,n_head_kv,hd,M,p0,mode", [(32, 8, 128, 1, 4000, 0), (32, 8, 128, 16, 4000, 0),
+                                                           (28, 4, 128, 64, 3000, 1), (14, 2, 64, 200, 100, 1),
+                                                           (8, 8, 64, 40, 0, 2)])
+def test_prefill_rope_ws(device, n_head, n_head_kv, hd, M, p0, mode):
+    heads = [0, n_head // 2, n_head - 1]
+    run_prefill_rope(device, 600 + M, n_head, n_head_kv, hd, M, p0, mode, 500000.0, heads=heads, workspace="auto")
