@@ -323,10 +323,16 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
 // on the decode kernel: its causal rows at the end of the cache are the chunk's own semantics (row t sees keys
 // 0 .. p0 + t), and it spreads the keys over the CUs, which the flash kernel (one workgroup per head and query tile,
 // every workgroup walking all keys) cannot. Measured (28 q / 4 kv heads, hd 128): 2 rows at 30k keys 610 -> 28 us, 16
-// rows 611 -> 74 us, 128 rows 598 -> 306 us; at 256 rows and 4k keys the flash kernel wins (87 vs 113 us).
-constexpr int64_t kPrefillSplitRows = 512;
+// rows 611 -> 74 us, 128 rows 598 -> 306 us; at 256 rows and 4k keys the flash kernel wins (87 vs 113 us). Up to 512
+// packed rows always, up to 1024 when the cache holds at least 64 keys per query row (Llama-3-8B, 256 rows at 30k keys:
+// 607 vs 640 us, the one measured loss at that bound).
+constexpr int64_t kPrefillSplitRows = 512, kPrefillSplitRowsLong = 1024, kPrefillSplitKeysPerRow = 64;
+int64_t prefill_split_keys(const mx_attn_desc & d);
 bool prefill_split_route(const mx_attn_desc & d) {
-    return d.n_q >= 1 && (int64_t)d.n_q * (d.n_head / d.n_head_kv) <= kPrefillSplitRows;
+    if (d.n_q < 1) return false;
+    const int64_t rows = (int64_t)d.n_q * (d.n_head / d.n_head_kv);
+    return rows <= kPrefillSplitRows ||
+           (rows <= kPrefillSplitRowsLong && prefill_split_keys(d) >= kPrefillSplitKeysPerRow * d.n_q);
 }
 // keys the decode kernel walks: a causal chunk's rows see keys up to p0 + n_q - 1 (keys past them are masked anyway)
 int64_t prefill_split_keys(const mx_attn_desc & d) {

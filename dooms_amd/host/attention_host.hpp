@@ -109,14 +109,16 @@ public:
             return {Code::Unsupported, "head_dim " + std::to_string(c.head_dim) + " is not supported (64 or 128)"};
         std::unique_ptr<LlamaAttention> a(new LlamaAttention(c, k_cache, v_cache, stream));
         // one workspace for the decode rows and for the prompt chunks of few rows that mx_attn_prefill_ws runs on the
-        // split-KV kernel (up to 512 rows per kv head), at the full context
+        // split-KV kernel (up to 512, or with a long enough cache 1024, rows per kv head), at the full context
         mx_attn_desc d = a->desc(1, 0, 0);
         size_t bytes = mx_attn_decode_workspace_bytes(&d, 1, c.n_ctx);
-        const int32_t m_split = std::min<int32_t>(c.n_ctx, std::max(1, 512 / (c.n_head / c.n_head_kv)));
-        mx_attn_desc dp = a->desc(m_split, 0, 0);
-        dp.p0 = c.n_ctx - m_split;
-        dp.causal = 1;
-        bytes = std::max(bytes, mx_attn_prefill_workspace_bytes(&dp));
+        for (int32_t rows : {512, 1024}) {
+            const int32_t m_split = std::min<int32_t>(c.n_ctx, std::max(1, rows / (c.n_head / c.n_head_kv)));
+            mx_attn_desc dp = a->desc(m_split, 0, 0);
+            dp.p0 = c.n_ctx - m_split;
+            dp.causal = 1;
+            bytes = std::max(bytes, mx_attn_prefill_workspace_bytes(&dp));
+        }
         if (Status st = a->ws_.reserve(bytes, stream); !st.is_ok()) return st;
         out = std::move(a);
         return {};

@@ -103,9 +103,10 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
                                     const uint16_t * v_cache, uint16_t * out, float * lse, mx_attn_stream stream);
 
 /*
- * mx_attn_prefill with a workspace: a chunk of few rows (n_q * n_head / n_head_kv <= 512) runs on the split-KV decode
- * kernel, which spreads a long cache over the whole chip (the flash kernel has one workgroup per head and 256 query rows,
- * each walking every key): for example 16 rows of a 28 q / 4 kv-head model at 30k keys, 611 -> 74 us. Larger chunks,
+ * mx_attn_prefill with a workspace: a chunk of few rows (n_q * n_head / n_head_kv <= 512, or <= 1024 with at least 64
+ * keys per query row) runs on the split-KV decode kernel, which spreads a long cache over the whole chip (the flash
+ * kernel has one workgroup per head and 256 query rows, each walking every key): for example 16 rows of a
+ * 28 q / 4 kv-head model at 30k keys, 611 -> 74 us. Larger chunks,
  * and any call with workspace == NULL, run the flash kernel exactly as mx_attn_prefill. Same arguments, semantics and
  * results within the stated tolerance (the summation order differs). No counterpart in the reference, whose chunks
  * always take attention_prefill; the extra argument is the decode workspace:
