@@ -246,7 +246,8 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     const WsLayout wl = decode_ws_layout(desc, batch, max_len);
 
     const DecodeShape s = decode_shape(desc);
-    // the grid's y dimension holds (sequence, kv head, row tile) and is limited to 65535
+    // one launch holds at most 65535 (sequence, kv head, row tile) tiles, so its 1-D grid of up to 32 splits per tile
+    // stays far inside the grid's range
     const int64_t tiles_per_seq = (int64_t)d.n_head_kv * s.n_rowtiles;
     if (tiles_per_seq > 65535)
         return fail(MX_ATTN_UNSUPPORTED, "n_head * n_q (%lld query rows per sequence) is too large for one decode launch",
@@ -303,6 +304,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         }
         p.chunk = (int32_t)std::min<int64_t>(chunk, INT32_MAX / 2);
         p.max_split = 1;
+        p.n_groups = n_seq * d.n_head_kv;
         for (int i = 0; i < n_seq; i++) {
             const int32_t n = kv_len[b0 + i];
             p.seq[i].k = static_cast<const mx::half_t *>(k_caches[b0 + i]);

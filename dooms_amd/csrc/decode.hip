@@ -91,10 +91,15 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     __shared__ int s_last;
     __shared__ float2 s_cs[F32 ? HD / 2 : 1];  // fused step: (cos, sin) of each rotary pair's angle
 
-    const int s = blockIdx.x;
-    int y = blockIdx.y;
-    const int rt = y % p.n_rowtiles;
-    y /= p.n_rowtiles;
+    // Work item. The row tiles of one (sequence, kv head, split) read the same keys and values, so they run as
+    // consecutive workgroups of one XCD (workgroups are dealt to the 8 XCDs round-robin: ids 8 apart share one), where
+    // all but the first read hit that XCD's L2. With one row tile this is the identity.
+    const uint32_t T = p.n_rowtiles, id = blockIdx.x, k8 = id / 8;
+    const uint32_t grp = (k8 / T) * 8 + id % 8;  // (split, sequence, kv head) group
+    const int rt = k8 % T;
+    const int s = grp % p.max_split;
+    const int y = grp / p.max_split;
+    if (y >= p.n_groups) return;  // padding of the grid to whole XCD rounds
     const int g = y % p.n_head_kv;
     const int bl = y / p.n_head_kv;
     const DecodeSeq sq = p.seq[bl];
@@ -415,11 +420,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
 template <int HD, int RT, int NW>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
-    const int tiles = n_seq * p.n_head_kv * p.n_rowtiles;
+    // 1-D grid: groups of (split, sequence, kv head), 8 per round of XCDs, each group's row tiles on one XCD
+    const int64_t groups = (int64_t)p.max_split * n_seq * p.n_head_kv;
+    const dim3 grid((uint32_t)(((groups + 7) / 8) * 8 * p.n_rowtiles));
     if (p.f32)
-        hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW>), dim3(p.max_split, tiles), dim3(NW * kWave), 0, stream, p);
+        hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW>), grid, dim3(NW * kWave), 0, stream, p);
     else
-        hipLaunchKernelGGL((decode_kernel<HD, RT, false, NW>), dim3(p.max_split, tiles), dim3(NW * kWave), 0, stream, p);
+        hipLaunchKernelGGL((decode_kernel<HD, RT, false, NW>), grid, dim3(NW * kWave), 0, stream, p);
     return hipGetLastError();
 }
 
