@@ -67,6 +67,11 @@ def test_llama3_8b_decode_8192(device):
     run_decode(device, 3, 32, 8, 128, [8192], check_heads=[0, 1, 2, 3, 13, 30, 31])
 
 
+def test_llama3_8b_decode_128k(device):
+    # a 131072-token context: 32 splits of 4096 keys per kv head, each wave walking 16 blocks before the merge
+    run_decode(device, 76, 32, 8, 128, [131072], check_heads=[0, 9, 31])
+
+
 @pytest.mark.parametrize("batch", [4, 16])
 def test_llama3_8b_decode_batched(device, batch):
     lens = list(np.random.default_rng(300 + batch).integers(1024, 8193, size=batch))

@@ -169,6 +169,24 @@ def test_prefill_ws_routes(device, N, chunk, n_head, n_head_kv, hd):
     check_prefill(device, 400 + N, N, n_head, n_head_kv, hd, rows=rows, chunk=chunk, workspace="auto")
 
 
+@pytest.mark.parametrize("M", [16, 128, 200])
+def test_prefill_ws_long_context(device, M):
+    # the last M prompt rows at the end of a 131072-token context (Qwen2.5-7B shape): 16 and 128 rows take the split-KV
+    # route, 200 rows (1400 packed rows per kv head) the flash kernel
+    rng = np.random.default_rng(420 + M)
+    L, hd, heads = 131072, 128, [0, 6, 7, 27]
+    q = torch.from_numpy(normal_f16(rng, (M, 28 * hd))).to(device)
+    kn, vn = normal_f16(rng, (L, 4 * hd)), normal_f16(rng, (L, 4 * hd))
+    k, v = torch.from_numpy(kn).to(device), torch.from_numpy(vn).to(device)
+    out, lse = A.prefill(q, k, v, n_head=28, n_head_kv=4, head_dim=hd, p0=L - M, want_lse=True, workspace="auto")
+    torch.cuda.synchronize()
+    rows = [0, M // 2, M - 1]
+    ro, rl = ref_attention(q.cpu().numpy(), kn, vn, 28, 4, hd, 1 / np.sqrt(hd), p0=L - M, rows=rows, heads=heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    assert_close(out.cpu().numpy().astype(np.float64)[rows][:, cols], ro, hd, f"M={M}",
+                 lse.cpu().numpy()[rows][:, heads], rl)
+
+
 def test_prefill_ws_noncausal_and_extra_keys(device):
     # non-causal rows over n_kv keys, and a causal chunk with cache rows past its own (masked, not read)
     rng = np.random.default_rng(410)
