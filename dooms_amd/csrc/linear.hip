@@ -11,8 +11,9 @@
 // MI355X design:
 //   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). One workgroup per CU
 //     (1 to 8 waves, as the rows divide) stages the (normalized) input rows in LDS once; each wave owns 4 weight rows and
-//     streams them in 16-byte loads, 4 sweeps of 4 loads in flight per lane, the first ones issued before the staging;
-//     the dot products stay f32 and are reduced across the wave at the end.
+//     streams them in 16-byte loads, 4 sweeps of 4 loads in flight per lane. The input rows' loads go out first, in one
+//     batch, then the first sweeps of weight loads, so that the staging waits only for the input; the dot products
+//     stay f32 and are reduced across the wave at the end.
 //   * M > 8 (prompt): stage_kernel writes each input row once as half(x * gamma * scale) into the workspace (the
 //     reference stages the same values per tile); gemm_kernel, v_mfma_f32_32x32x16_f16 on 128 x 128 output tiles, K in
 //     steps of 64 through LDS (double buffer, rows padded to 72 halves so that the 16-byte operand reads of 16
@@ -107,19 +108,19 @@ constexpr int kGemvDepth = 4;      // 64-lane sweeps of 16-byte weight loads in 
 // L2 as it goes (the reference's kStageInput = false variant, metal_llama_decoder.mm:45-47).
 // The wave's first kGemvDepth sweeps of weight loads are issued before the input is staged, so the staging and its
 // barriers overlap the first HBM round trip.
-template <int MT, bool STAGE, bool OUT16>
+template <int MT, bool STAGE, bool OUT16, bool NORM>
 __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParams p) {
     extern __shared__ float xs[];  // [MT][K]: x (* gamma) of each input row, when staged
     __shared__ float red[MT][kGemvMaxWaves];
     __shared__ float s_scale[MT];
     const int K = p.K, M = p.M;
-    const bool norm = p.flags & kLinearNorm;
+    constexpr bool norm = NORM;  // p.flags & kLinearNorm
     const int nw = blockDim.x / kWave;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 
     // work item: (matrix, group of 4 rows) per wave
     const int groups = (p.N + kGemvRows - 1) / kGemvRows;
-    const int item = blockIdx.x * nw + wave;
+    const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * nw + wave);  // wave-uniform: scalar loads of p.w[mi]
     const bool active = item < groups * p.count;
     const int mi = active ? item / groups : 0;
     const int r0 = active ? (item % groups) * kGemvRows : 0;
@@ -134,30 +135,61 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
 #pragma unroll
         for (int i = 0; i < kGemvRows; i++) wv[j][i] = as_half8(load16(wr[i] + 8 * cc));
     };
-    if (active) {
-#pragma unroll
-        for (int j = 0; j < kGemvDepth; j++) load_sweep(j, lane + kWave * j);
-    }
 
-    // stage the rows and, with the norm, reduce their sums of squares (stage_input, llama_kernels.h:62-80)
+    // The input rows (and gamma) in batches: batch b covers the 16-byte chunks kk = (b XJ + j) blockDim + tid, j < XJ,
+    // of every input row. All of a batch's loads go out before any wait (clamped, unconditional), and batch 0 goes out
+    // ahead of the weight loads: loads complete in issue order, so its wait leaves the weights in flight.
+    constexpr int XJ = MT >= 4 ? 1 : 4 / MT;
+    const int K4 = K / 4;
+    const int nxb = (STAGE || NORM) ? (K4 + XJ * (int)blockDim.x - 1) / (XJ * (int)blockDim.x) : 0;
+    float4_t xv[MT][XJ], gv[XJ];
+    float ss[MT];
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
-        float ss = 0.f;
-        if (m < M) {
-            const float * xr = p.x + (int64_t)m * p.x_stride;
-            for (int k = threadIdx.x * 4; k < K; k += blockDim.x * 4) {
-                float4_t v = *reinterpret_cast<const float4_t *>(xr + k);
-                ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-                if constexpr (STAGE) {
-                    if (norm) v = v * *reinterpret_cast<const float4_t *>(p.gamma + k);
-                    *reinterpret_cast<float4_t *>(xs + m * K + k) = v;
-                }
+    for (int m = 0; m < MT; m++) ss[m] = 0.f;
+    auto xload = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < XJ; j++) {
+            const int kk = min((b * XJ + j) * (int)blockDim.x + (int)threadIdx.x, K4 - 1);
+            if constexpr (NORM) gv[j] = *reinterpret_cast<const float4_t *>(p.gamma + 4 * kk);
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                xv[m][j] = *reinterpret_cast<const float4_t *>(p.x + (int64_t)min(m, M - 1) * p.x_stride + 4 * kk);
+        }
+    };
+    // sums of squares (stage_input, llama_kernels.h:62-80) and the staged x (* gamma)
+    auto xstage = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < XJ; j++) {
+            const int kk = (b * XJ + j) * (int)blockDim.x + (int)threadIdx.x;
+            if (kk >= K4) continue;
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const float4_t v = xv[m][j];
+                if constexpr (NORM) ss[m] += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+                if constexpr (STAGE)
+                    if (m < M) *reinterpret_cast<float4_t *>(xs + m * K + 4 * kk) = NORM ? v * gv[j] : v;
             }
         }
-        if (norm) {
+    };
+    if constexpr (STAGE || NORM) xload(0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order: the input first, then the weights
+    // unconditional (an idle wave reads valid rows of matrix 0 and returns below): a branch here would make every
+    // later wait assume that the input loads are the newest ones
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += shfl_xor(ss, o);
-            if (lane == 0) red[m][wave] = ss;
+    for (int j = 0; j < kGemvDepth; j++) load_sweep(j, lane + kWave * j);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (STAGE || NORM) xstage(0);
+    for (int b = 1; b < nxb; b++) {  // inputs longer than one batch (the waits of these drain the weight loads too)
+        xload(b);
+        xstage(b);
+    }
+    if (norm) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            float t = ss[m];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) t += shfl_xor(t, o);
+            if (lane == 0) red[m][wave] = t;
         }
     }
     __syncthreads();
@@ -360,13 +392,17 @@ hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
     const dim3 grid((uint32_t)((items + nw - 1) / nw));
     const dim3 block((uint32_t)(nw * kWave));
     const size_t lds = (size_t)MT * p.K * sizeof(float);
-    const bool out16 = p.flags & kLinearOutF16;
-    if (lds <= kLinearGemvLds) {
-        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, true, true>), grid, block, lds, stream, p);
-        else hipLaunchKernelGGL((gemv_kernel<MT, true, false>), grid, block, lds, stream, p);
-    } else {
-        if (out16) hipLaunchKernelGGL((gemv_kernel<MT, false, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((gemv_kernel<MT, false, false>), grid, block, 0, stream, p);
+    const int v = (lds <= kLinearGemvLds ? 4 : 0) | ((p.flags & kLinearOutF16) ? 2 : 0) | ((p.flags & kLinearNorm) ? 1 : 0);
+    const size_t dyn = (v & 4) ? lds : 0;
+    switch (v) {
+        case 0: hipLaunchKernelGGL((gemv_kernel<MT, false, false, false>), grid, block, dyn, stream, p); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<MT, false, false, true>), grid, block, dyn, stream, p); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<MT, false, true, false>), grid, block, dyn, stream, p); break;
+        case 3: hipLaunchKernelGGL((gemv_kernel<MT, false, true, true>), grid, block, dyn, stream, p); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<MT, true, false, false>), grid, block, dyn, stream, p); break;
+        case 5: hipLaunchKernelGGL((gemv_kernel<MT, true, false, true>), grid, block, dyn, stream, p); break;
+        case 6: hipLaunchKernelGGL((gemv_kernel<MT, true, true, false>), grid, block, dyn, stream, p); break;
+        default: hipLaunchKernelGGL((gemv_kernel<MT, true, true, true>), grid, block, dyn, stream, p); break;
     }
     return hipGetLastError();
 }
