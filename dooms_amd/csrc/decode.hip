@@ -145,14 +145,14 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, xq[ks]);
         }
-    } else {
-        const half_t * qrow = p.q + (seq_row0 + st) * p.q_stride + (int64_t)sh * HD;
+    }
+    // f16 query rows: loaded by every lane (rows past the tile read the problem's first row, a valid address) and zeroed
+    // only after the first block's loads are out; a conditional load here would make the compiler drain it first
+    u32x4 qv[F32 ? 1 : KS];
+    if constexpr (!F32) {
+        const half_t * qrow = p.q + (seq_row0 + (srow_ok ? st : 0)) * p.q_stride + (int64_t)(srow_ok ? sh : g * G) * HD;
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (srow_ok) v = load16(qrow + 32 * ks + 8 * sgrp);
-            qb[ks] = as_half8(v);
-        }
+        for (int ks = 0; ks < KS; ks++) qv[ks] = load16(qrow + 32 * ks + 8 * sgrp);
     }
 
     // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
@@ -183,6 +183,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     int jb = j0 + kBlockKeys * wave;
     B cur, nxt;
     load_block(jb, cur);
+    if constexpr (!F32) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            asm volatile("" : "+v"(qv[ks])::"memory");  // used from here on, behind the block's loads
+            qb[ks] = as_half8(srow_ok ? qv[ks] : u32x4{0u, 0u, 0u, 0u});
+        }
+    }
     if constexpr (F32) {
         // the new key and value are used only from here on, so any wait for them leaves the block's loads in flight
 #pragma unroll
