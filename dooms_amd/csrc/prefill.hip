@@ -178,22 +178,39 @@ void prefill_kernel(PrefillParams p) {
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(x[ks]));
-    } else {
-        const char * qp = reinterpret_cast<const char *>(p.q) + (bq + (int64_t)qrow * p.q_stride + (int64_t)h * hstride) * ES;
+    }
+    // f16/f32/bf16 query rows: loaded by every lane (rows past the chunk read its last row, a valid address) and turned
+    // into the operand only once the first tile's loads are out, so that waiting for the query leaves them in flight
+    u32x4 qr[ROPE ? 1 : KS][NR];
+    auto q_operand = [&]() __attribute__((always_inline)) {
+        if constexpr (!ROPE) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            const int col = 16 * ks + 8 * hgrp;
-            u32x4 r[NR];
-#pragma unroll
-            for (int j = 0; j < NR; j++) r[j] = u32x4{0u, 0u, 0u, 0u};
-            if (qrow < p.n_q) ld8(qp, col, r);
-            qb[ks] = as_half8(half8(r, col));
+            for (int ks = 0; ks < KS; ks++) {
+                const int col = 16 * ks + 8 * hgrp;
+                const u32x4 hq = half8(qr[ks], col);
+                qb[ks] = as_half8(qrow < p.n_q ? hq : u32x4{0u, 0u, 0u, 0u});
+            }
         }
+    };
+    if constexpr (!ROPE) {
+        const char * qp = reinterpret_cast<const char *>(p.q) +
+                          (bq + (int64_t)min(qrow, p.n_q - 1) * p.q_stride + (int64_t)h * hstride) * ES;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) ld8(qp, 16 * ks + 8 * hgrp, qr[ks]);
     }
     if (nblk > 0) {
         load_tile(0);
+        if constexpr (!ROPE) {  // the query is used from here on (the compiler would otherwise hoist its use above)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int j = 0; j < NR; j++) asm volatile("" : "+v"(qr[ks][j])::"memory");
+        }
+        q_operand();
         store_tile(0);
         if (nblk > 1) load_tile(KB);
+    } else {
+        q_operand();
     }
     // Wait here for the query operand (and the prologue's loads): inside the loop the only loads in flight are then the
     // prefetch of a later block, whose registers the block's math does not read, so no wait inside the loop has to
