@@ -19,7 +19,7 @@ namespace mx {
 namespace {
 
 template <int HD>
-__global__ __launch_bounds__(256) void rope_store_kernel(RopeStoreParams p) {
+__global__ __launch_bounds__(1024) void rope_store_kernel(RopeStoreParams p) {
     const int t = blockIdx.x;
     const int pos = p.p0 + t;
     const float * row = p.qkv + (int64_t)t * p.qkv_stride;
@@ -66,7 +66,8 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeStoreParams p) {
 
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream) {
     const int pairs = ((p.q_out ? p.n_head : 0) + p.n_head_kv) * head_dim / 2;
-    const int threads = std::min(256, ((pairs + kWave - 1) / kWave) * kWave);
+    // one pair per thread where the row has at most 1024 (each further pass of the loop is another dependent round trip)
+    const int threads = std::min(1024, ((pairs + kWave - 1) / kWave) * kWave);
     if (head_dim == 64) hipLaunchKernelGGL((rope_store_kernel<64>), dim3(p.n_rows), dim3(threads), 0, stream, p);
     else hipLaunchKernelGGL((rope_store_kernel<128>), dim3(p.n_rows), dim3(threads), 0, stream, p);
     return hipGetLastError();
