@@ -50,6 +50,46 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(LinearParams p) {
     const float * row = p.x + (int64_t)blockIdx.x * p.x_stride;
     const int kp = (p.K + 63) / 64 * 64;  // staged rows are zero-padded to a multiple of 64 columns
     half_t * dst = p.xh + (int64_t)blockIdx.x * kp;
+    const int K4 = p.K / 4;
+    constexpr int SJ = 8;  // 16-byte pieces per thread held in registers
+    if (K4 <= SJ * kThreads) {
+        // the row (and gamma) loaded once, all pieces in flight together; the sum of squares and the conversion then
+        // work from registers
+        float4_t v[SJ], g[SJ];
+#pragma unroll
+        for (int j = 0; j < SJ; j++) {
+            const int kk = min(j * kThreads + (int)threadIdx.x, K4 - 1);
+            v[j] = *reinterpret_cast<const float4_t *>(row + 4 * kk);
+            if constexpr (NORM) g[j] = *reinterpret_cast<const float4_t *>(p.gamma + 4 * kk);
+        }
+        float s = 1.f;
+        if constexpr (NORM) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < SJ; j++)
+                if (j * kThreads + (int)threadIdx.x < K4)
+                    ss += v[j][0] * v[j][0] + v[j][1] * v[j][1] + v[j][2] * v[j][2] + v[j][3] * v[j][3];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += shfl_xor(ss, o);
+            if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+            __syncthreads();
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) t += red[w];
+            s = 1.f / __builtin_sqrtf(t / (float)p.K + p.eps);
+        }
+#pragma unroll
+        for (int j = 0; j < SJ; j++) {
+            const int kk = j * kThreads + (int)threadIdx.x;
+            if (kk >= K4) continue;
+            half4_t h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = (half_t)(NORM ? v[j][e] * (g[j][e] * s) : v[j][e]);
+            *reinterpret_cast<half4_t *>(dst + 4 * kk) = h;
+        }
+        for (int k = p.K + threadIdx.x * 8; k < kp; k += kThreads * 8) *reinterpret_cast<u32x4 *>(dst + k) = u32x4{0u, 0u, 0u, 0u};
+        return;
+    }
     float s = 1.f;
     if constexpr (NORM) {
         float ss = 0.f;
