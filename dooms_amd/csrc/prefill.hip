@@ -144,15 +144,16 @@ void prefill_kernel(PrefillParams p) {
     auto kchunk = [&](int b) { return 4 * (b / (KB / 16)) + lane / 16; };
     auto vrow = [&](int b) { return 16 * (b % (KB / 16)) + 4 * (lane / 16) + (lane % 16) / 4; };
     auto vchunk = [&](int b) { return 4 * (b / (KB / 16)) + lane % 4; };
-    auto load_tile = [&](int kb) {
+    auto load_tile_into = [&](int kb, u32x4 (&kr)[NI][NR], u32x4 (&vr)[NI][NR]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
             const int kkey = min(kb + krow(b), p.n_kv - 1), vkey = min(kb + vrow(b), p.n_kv - 1);
-            ld8(kg + (int64_t)kkey * p.kv_stride * ES, 8 * kchunk(b), kreg[i]);
-            ld8(vg + (int64_t)vkey * p.kv_stride * ES, 8 * vchunk(b), vreg[i]);
+            ld8(kg + (int64_t)kkey * p.kv_stride * ES, 8 * kchunk(b), kr[i]);
+            ld8(vg + (int64_t)vkey * p.kv_stride * ES, 8 * vchunk(b), vr[i]);
         }
     };
+    auto load_tile = [&](int kb) __attribute__((always_inline)) { load_tile_into(kb, kreg, vreg); };
     auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -198,9 +199,33 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) ld8(qp, 16 * ks + 8 * hgrp, qr[ks]);
     }
-    if (nblk > 0) {
+    if (nblk > 0 && W == 4) {
+        // the short-prompt plans: steps 0 and 1 go out together (step 1 into registers of its own, unconditionally:
+        // past the cache its rows are clamped to the last one and never used), so the prologue waits for one round
+        // trip instead of two (the 8-wave plan's long chunks keep the plain order)
+        u32x4 k1[NI][NR], v1[NI][NR];
         load_tile(0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile_into(KB, k1, v1);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (!ROPE) {  // the query is used from here on (the compiler would otherwise hoist its use above)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int j = 0; j < NR; j++) asm volatile("" : "+v"(qr[ks][j])::"memory");
+        }
+        q_operand();
+        store_tile(0);
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                kreg[i][j] = k1[i][j];
+                vreg[i][j] = v1[i][j];
+            }
+    } else if (nblk > 0) {
+        load_tile(0);
+        if constexpr (!ROPE) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++)
 #pragma unroll
