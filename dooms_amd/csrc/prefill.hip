@@ -166,6 +166,15 @@ void prefill_kernel(PrefillParams p) {
     // Q^T operand: lane holds Q[qrow][16 ks + 8 hgrp .. + 8]
     half8_t qb[KS];
     if constexpr (ROPE) {
+        // the rotary frequencies into LDS: compile-time indices make scalar loads of the kernel arguments, one LDS
+        // store each (a per-lane index into the arguments would be a vector load, waited for one by one)
+        __shared__ float s_freq[HD / 2];
+        float fr = 0.f;
+#pragma unroll
+        for (int i = 0; i < HD / 2; i++)
+            if (threadIdx.x == i) fr = p.rope_freq[i];
+        if (threadIdx.x < HD / 2) s_freq[threadIdx.x] = fr;
+        __syncthreads();
         float x[KS][8] = {};
         if (qrow < p.n_q) {
             const float * qp = p.qkv + bq + (int64_t)qrow * p.q_stride + (int64_t)h * HD + 8 * hgrp;
@@ -173,7 +182,7 @@ void prefill_kernel(PrefillParams p) {
             for (int ks = 0; ks < KS; ks++) load8f(qp + 16 * ks, x[ks]);
             rope_rotate<KS, 16>(x, 8 * hgrp, p.rope_mode, [&](int i) {
                 float sn, cs;
-                sincos_rope((float)qpos * p.rope_freq[i], sn, cs);
+                sincos_rope((float)qpos * s_freq[i], sn, cs);
                 return make_float2(cs, sn);
             });
         }
