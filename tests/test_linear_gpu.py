@@ -106,6 +106,14 @@ def test_eight_rows_unstaged_input_with_norm(device):
     run(device, 4, 8, 1024, 4096, norm=True, bias=True)  # 8 x 4096 f32 exceeds the 64 KB staging budget
 
 
+@pytest.mark.parametrize("M,N,K,norm", [(1, 256, 14336, True), (1, 4096, 14336, False), (4, 512, 8192, True),
+                                         (2, 96, 2080, True)])
+def test_input_staged_in_several_batches(device, M, N, K, norm):
+    # input rows longer than one batch of the staging loads (a workgroup of one wave holds 4 (M = 1) or 2 (M = 2)
+    # 16-byte pieces per row per thread per batch); the FFN-down shape accumulates into the residual
+    run(device, 20 + M + K, M, N, K, norm=norm, accumulate=not norm)
+
+
 # ---- prompt chunks (matmul): the MFMA GEMM ----
 def test_qwen05b_prompt_qkv(device):
     run(device, 5, 512, 1152, 896, norm=True, bias=True, rows=list(range(0, 512, 5)) + [511])
