@@ -66,6 +66,9 @@ int32_t hip_status(hipError_t e, const char * what) {
 // Decode split plan. Splits are whole multiples of kDecodeChunkQuantum keys, and
 //   * at least kMinChunk keys and at most kMaxSplits splits per sequence: every extra split lengthens the in-kernel
 //     merge (measured: 64 splits of an 8192-key Llama-3-8B row cost ~5 us more than 32);
+//   * or, when that leaves fewer than kFewWorkgroups workgroups, splits of 128 keys: Llama-3-8B at 700 keys (24 -> 48
+//     workgroups) 9.75 -> 8.9 us, Qwen2.5-0.5B at 900 keys 7.45 -> 7.0 us; with 120 workgroups (Whisper cross-attention,
+//     20 heads over 1500 frames) the smaller chunk was 15 % slower;
 //   * then as small as possible while the launch stays within workgroup_cap() workgroups (measured on MI355X for
 //     Llama-3-8B batches of 4 and 16: 1536 streams best; two workgroups per CU are resident at once, 512 in all).
 //   * but when the longest sequence is short (keys x head_dim <= kOneSplitWork: at most 20 KB of K and V for each of
@@ -73,7 +76,7 @@ int32_t hip_status(hipError_t e, const char * what) {
 //     Qwen2.5-0.5B at 513 keys 7.6 -> 6.8 us, Whisper self-attention at 449 keys 8.3 -> 7.7 us; but Qwen2.5-0.5B at
 //     700 keys 7.5 -> 8.1 us and Llama-3-8B (hd 128) at 600-768 keys 9.8 -> 13.6 us, hence the bound.
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
-constexpr int kMinChunk = 256, kMaxSplits = 32, kOneSplitWork = 40960;
+constexpr int kMinChunk = 256, kMaxSplits = 32, kOneSplitWork = 40960, kFewWorkgroups = 64;
 int workgroup_cap() {
     const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
     const int v = s ? std::atoi(s) : 0;
@@ -286,12 +289,15 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
         auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
         int64_t chunk = std::max<int64_t>(round_up(kMinChunk), round_up((lmax + kMaxSplits - 1) / kMaxSplits));
-        if (lmax * d.head_dim <= kOneSplitWork) chunk = round_up(lmax);  // short caches: one split, no merge
         auto launch_wgs = [&](int64_t c) {
             int64_t n = 0;
             for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
             return n * d.n_head_kv * s.n_rowtiles;
         };
+        // few workgroups at the minimum chunk: halve it, so that twice as many CUs stream the keys
+        if (launch_wgs(chunk) < kFewWorkgroups)
+            chunk = std::max<int64_t>(quantum, round_up((lmax + kMaxSplits - 1) / kMaxSplits));
+        if (lmax * d.head_dim <= kOneSplitWork) chunk = round_up(lmax);  // short caches: one split, no merge
         const int64_t cap = workgroup_cap();
         if (launch_wgs(chunk) > cap) {  // smallest chunk within the cap: bisect over multiples of the quantum
             int64_t lo = chunk / quantum, hi = round_up(lmax) / quantum;
