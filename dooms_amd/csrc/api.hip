@@ -178,7 +178,7 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.p0 = d.p0;
     p.n_kv = (int32_t)n_kv;
     p.causal = d.causal;
-    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv);
+    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim);
     p.n_qtiles = (d.n_q + rows - 1) / rows;
     p.scale_log2 = d.scale * 1.4426950408889634f;
     p.rope = rope != nullptr;
@@ -431,7 +431,7 @@ MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void
     p.n_q = p.n_kv = d.n_tok;
     p.p0 = 0;
     p.causal = 0;
-    const int rpw = mx::prefill_rows_per_workgroup(d.n_tok, d.heads * d.batch, d.n_tok);
+    const int rpw = mx::prefill_rows_per_workgroup(d.n_tok, d.heads * d.batch, d.n_tok, s.hdp);
     p.n_qtiles = (d.n_tok + rpw - 1) / rpw;
     p.scale_log2 = d.scale * 1.4426950408889634f;
     p.rope_mode = 2;

@@ -121,7 +121,7 @@ int decode_rows_per_tile(int rows);
 hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, int waves, hipStream_t stream);
 hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 
-int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv);  // query rows one prefill workgroup covers
+int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim);  // query rows one prefill workgroup covers
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);

@@ -471,21 +471,27 @@ void prefill_kernel(PrefillParams p) {
 // workgroups of 4 waves, two per row tile splitting the key blocks (KSP = 2): one round on the CUs, half the chain of
 // dependent blocks per wave, but twice the K/V bytes through the load path per step. Measured: the Qwen2.5-0.5B
 // 512-token prompt 12.0 -> 10.8 us per layer, a 16-row chunk at 30k keys (28 heads, hd 128) 629 -> 559 us; a
-// 300-token Llama-3-8B prompt (5 blocks) ran 7 % slower split, hence the 512-key floor.
+// 300-token Llama-3-8B prompt (5 blocks) ran 7 % slower split, hence the 512-key floor. At head dim 64 (half the
+// K/V bytes per key) and with the 128-row workgroups filling at most a quarter of the CUs, the split pays from 128
+// keys: Qwen2.5-0.5B prompts of 128, 256 and 384 tokens 6.06 -> 5.9, 8.2 -> 7.5 and 10.0 -> 9.3 us per layer (a
+// 448-token prompt of 20 heads, 80 such workgroups, ran 9 % slower split).
 // Plans: 8 = 8 waves x 32 rows, 4 = 4 waves x 32 rows, 2 = 4 waves over 2 row tiles x 2 key halves (64 rows).
 constexpr int kCUs = 256;
-int prefill_plan(int n_q, int n_head, int n_kv) {
+int prefill_plan(int n_q, int n_head, int n_kv, int head_dim) {
     const char * s = std::getenv("MX_PREFILL_PLAN");  // tuning and test override, read per call
     const int forced = s ? std::atoi(s) : 0;
     if (forced == 2 || forced == 4 || forced == 8) return forced;
     const int64_t wg8 = (int64_t)((n_q + 255) / 256) * n_head, wg4 = (int64_t)((n_q + 127) / 128) * n_head;
     if (2 * wg4 <= kCUs && n_kv >= 8 * kBK) return 2;
+    if (4 * wg4 <= kCUs && head_dim <= 64 && n_kv >= 2 * kBK) return 2;
     const double cost8 = (double)((wg8 + kCUs - 1) / kCUs) * 256 * 0.8;
     const double cost4 = (double)((wg4 + kCUs - 1) / kCUs) * 128;
     return cost8 <= cost4 ? 8 : 4;
 }
 
-int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv) { return 32 * prefill_plan(n_q, n_head, n_kv); }
+int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim) {
+    return 32 * prefill_plan(n_q, n_head, n_kv, head_dim);
+}
 
 // ---- the IR self-attention's operand packing (row f4): one thread per 8 consecutive padded head dims ----
 __global__ __launch_bounds__(256) void self_attn_pack_kernel(SelfAttnPackParams p) {
@@ -596,7 +602,7 @@ void launch_prefill_t(const PrefillParams & p, int plan, int n_batch, int sa, hi
 
 hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, int sa, hipStream_t stream) {
     const bool pos = p.scale_log2 > 0.f;
-    const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv);
+    const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv, head_dim);
     if (p.n_qtiles != (p.n_q + 32 * plan - 1) / (32 * plan)) return hipErrorInvalidValue;  // planned with other inputs
     if (head_dim == 64) {
         if (pos) launch_prefill_t<64, true>(p, plan, n_batch, sa, stream);
