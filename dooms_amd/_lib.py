@@ -31,13 +31,19 @@ ROPE_NEOX = 1    # split halves (i, i + head_dim / 2): qwen2
 ROPE_NONE = 2    # no rotation: Whisper
 
 
+class MxAttnTuning(ctypes.Structure):
+    """mx_attn_tuning (include/mx_attn.h): 0 in a field keeps the library's plan."""
+    _fields_ = [("decode_splits", ctypes.c_int32), ("decode_waves", ctypes.c_int32),
+                ("decode_max_workgroups", ctypes.c_int32), ("prefill_plan", ctypes.c_int32)]
+
+
 class MxAttnDesc(ctypes.Structure):
     """mx_attn_desc (include/mx_attn.h)."""
     _fields_ = [
         ("n_head", ctypes.c_int32), ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("n_q", ctypes.c_int32), ("p0", ctypes.c_int32), ("n_kv", ctypes.c_int32), ("causal", ctypes.c_int32),
         ("reserved", ctypes.c_int32), ("q_stride", ctypes.c_int64), ("kv_stride", ctypes.c_int64),
-        ("out_stride", ctypes.c_int64), ("scale", ctypes.c_float),
+        ("out_stride", ctypes.c_int64), ("scale", ctypes.c_float), ("tuning", ctypes.POINTER(MxAttnTuning)),
     ]
 
 
@@ -56,7 +62,8 @@ class MxLinearDesc(ctypes.Structure):
 class MxSelfAttnDesc(ctypes.Structure):
     """mx_self_attn_desc (include/mx_attn.h)."""
     _fields_ = [("batch", ctypes.c_int32), ("n_tok", ctypes.c_int32), ("heads", ctypes.c_int32),
-                ("embed", ctypes.c_int32), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float)]
+                ("embed", ctypes.c_int32), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float),
+                ("tuning", ctypes.POINTER(MxAttnTuning))]
 
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
@@ -132,11 +139,23 @@ def check(code: int) -> None:
         raise MxAttnError(code, last_error())
 
 
+def make_tuning(tuning):
+    """An MxAttnTuning from None, an MxAttnTuning or a dict of its fields; None stays None."""
+    if tuning is None or isinstance(tuning, MxAttnTuning):
+        return tuning
+    return MxAttnTuning(**tuning)
+
+
 def make_desc(n_head, n_head_kv, head_dim, n_q, q_stride, kv_stride, out_stride, scale, p0=0, n_kv=0, causal=1,
-              reserved=0) -> MxAttnDesc:
-    return MxAttnDesc(n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim, n_q=n_q, p0=p0, n_kv=n_kv,
-                      causal=causal, reserved=reserved, q_stride=q_stride, kv_stride=kv_stride,
-                      out_stride=out_stride, scale=scale)
+              reserved=0, tuning=None) -> MxAttnDesc:
+    d = MxAttnDesc(n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim, n_q=n_q, p0=p0, n_kv=n_kv,
+                   causal=causal, reserved=reserved, q_stride=q_stride, kv_stride=kv_stride,
+                   out_stride=out_stride, scale=scale)
+    t = make_tuning(tuning)
+    if t is not None:
+        d.tuning = ctypes.pointer(t)
+        d._tuning_keepalive = t  # the struct must outlive every call that passes this descriptor
+    return d
 
 
 def prefill_raw(desc: MxAttnDesc, q: int, k: int, v: int, out: int, lse: int, stream: int) -> int:

@@ -3,11 +3,33 @@
 Every call goes through libmx_attn.so; there is no CPU or PyTorch fallback. Tensors must be CUDA (HIP) float16 with a
 unit stride along the feature dimension; row strides are taken from the tensors.
 """
+import contextlib
 import math
 
 import torch
 
 from . import _lib
+
+# Tuning that calls without their own `tuning=` argument pass in their descriptors (see tuning()); None: the library's
+# plans.
+_default_tuning = None
+
+
+@contextlib.contextmanager
+def tuning(**fields):
+    """Within the block, calls that do not pass `tuning=` use an mx_attn_tuning with these fields (decode_splits,
+    decode_waves, decode_max_workgroups, prefill_plan); the library's plan for the others."""
+    global _default_tuning
+    saved = _default_tuning
+    _default_tuning = dict(fields)
+    try:
+        yield
+    finally:
+        _default_tuning = saved
+
+
+def _tuning(t):
+    return _default_tuning if t is None else t
 
 
 def _stream() -> int:
@@ -25,7 +47,7 @@ def _rows(t: torch.Tensor, name: str, dtype=torch.float16) -> torch.Tensor:
 
 
 def prefill(q, k_cache, v_cache, *, n_head, n_head_kv, head_dim, p0=0, causal=True, n_kv=None, scale=None,
-            out=None, lse=None, want_lse=False, workspace=None):
+            out=None, lse=None, want_lse=False, workspace=None, tuning=None):
     """mx_attn_prefill: q [n_q][>= n_head*hd], caches [n_kv][>= n_head_kv*hd]. Returns (out, lse or None).
     workspace: "auto" (sized and zeroed here) or a zeroed uint8 device tensor runs mx_attn_prefill_ws, which takes the
     split-KV kernel for chunks of few rows; None runs mx_attn_prefill."""
@@ -41,7 +63,7 @@ def prefill(q, k_cache, v_cache, *, n_head, n_head_kv, head_dim, p0=0, causal=Tr
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
     d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, q.stride(0), k_cache.stride(0), out.stride(0), scale,
-                       p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0)
+                       p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0, tuning=_tuning(tuning))
     if workspace is None:
         _lib.check(_lib.prefill_raw(d, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
                                     lse.data_ptr() if lse is not None else 0, _stream()))
@@ -68,7 +90,7 @@ def new_workspace(nbytes: int, device) -> torch.Tensor:
 
 
 def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1, causal=False, scale=None,
-           out=None, lse=None, want_lse=False, workspace=None):
+           out=None, lse=None, want_lse=False, workspace=None, tuning=None):
     """mx_attn_decode (float16 q) or mx_attn_decode_f32 (float32 q and output): q [batch*n_q][>= n_head*hd];
     k_caches/v_caches lists of [>= kv_len[b]][>= n_head_kv*hd] float16 tensors (entries may repeat); kv_len list of
     ints. Returns (out, lse or None)."""
@@ -90,7 +112,7 @@ def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1,
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
     d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, q.stride(0), kv_stride, out.stride(0), scale,
-                       causal=1 if causal else 0)
+                       causal=1 if causal else 0, tuning=_tuning(tuning))
     if workspace is None:
         workspace = new_workspace(_lib.decode_workspace_bytes(d, batch, max(kv_len)), q.device)
     _lib.check((_lib.decode_f32_raw if f32 else _lib.decode_raw)(d, list(kv_len), q.data_ptr(), [t.data_ptr() for t in k_caches],
@@ -101,7 +123,7 @@ def decode(q, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, n_q=1,
 
 
 def decode_rope(qkv, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim, rope_mode, rope_base=10000.0,
-                scale=None, out=None, lse=None, want_lse=False, workspace=None):
+                scale=None, out=None, lse=None, want_lse=False, workspace=None, tuning=None):
     """mx_attn_decode_rope, the fused decode step: qkv f32 [batch][>= (n_head + 2 n_head_kv) hd] holds each sequence's
     new token unrotated (q | k | v); the token goes to position kv_len[b] - 1 of k_caches[b] / v_caches[b] (f16,
     written in place). Returns (out f32 [batch][n_head hd], lse or None)."""
@@ -121,7 +143,8 @@ def decode_rope(qkv, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim,
         lse = torch.empty(batch, n_head, dtype=torch.float32, device=qkv.device)
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
-    d = _lib.make_desc(n_head, n_head_kv, head_dim, 1, qkv.stride(0), kv_stride, out.stride(0), scale, causal=0)
+    d = _lib.make_desc(n_head, n_head_kv, head_dim, 1, qkv.stride(0), kv_stride, out.stride(0), scale, causal=0,
+                       tuning=_tuning(tuning))
     if workspace is None:
         workspace = new_workspace(_lib.decode_workspace_bytes(d, batch, max(kv_len)), qkv.device)
     _lib.check(_lib.decode_rope_raw(d, rope_mode, rope_base, list(kv_len), qkv.data_ptr(),
@@ -132,7 +155,8 @@ def decode_rope(qkv, k_caches, v_caches, kv_len, *, n_head, n_head_kv, head_dim,
 
 
 def prefill_rope(qkv, k_cache, v_cache, *, n_head, n_head_kv, head_dim, rope_mode, rope_base=10000.0, p0=0,
-                 causal=True, n_kv=None, scale=None, out=None, lse=None, want_lse=False, workspace=None):
+                 causal=True, n_kv=None, scale=None, out=None, lse=None, want_lse=False, workspace=None,
+                 tuning=None):
     """mx_attn_prefill_rope: qkv f32 [n_q][>= (n_head + 2 n_head_kv) hd] unrotated rows at positions p0 ..; their keys
     and values are written (rotated, f16) into rows p0 .. of k_cache / v_cache, then the chunk attends.
     Returns (out f32 [n_q][n_head hd], lse or None). workspace ("auto" or a zeroed uint8 device tensor) runs
@@ -149,7 +173,7 @@ def prefill_rope(qkv, k_cache, v_cache, *, n_head, n_head_kv, head_dim, rope_mod
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
     d = _lib.make_desc(n_head, n_head_kv, head_dim, n_q, qkv.stride(0), k_cache.stride(0), out.stride(0), scale,
-                       p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0)
+                       p0=p0, n_kv=0 if n_kv is None else n_kv, causal=1 if causal else 0, tuning=_tuning(tuning))
     if workspace is None:
         _lib.check(_lib.prefill_rope_raw(d, rope_mode, rope_base, qkv.data_ptr(), k_cache.data_ptr(),
                                          v_cache.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else 0,
@@ -204,7 +228,7 @@ def linear(x, weights, *, out=None, gamma=None, bias=None, eps=1e-5, accumulate=
 _SA_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
 
 
-def self_attention(qkv, *, heads, scale=None, out=None):
+def self_attention(qkv, *, heads, scale=None, out=None, tuning=None):
     """mx_self_attention, the IR's SelfAttention op: qkv [B][N][3E] contiguous (f32, f16 or bf16) -> y [B][N][E] of the
     same dtype. scale defaults to head_dim^-0.5. The workspace (if the shape needs one) comes from torch's allocator."""
     if not qkv.is_cuda:
@@ -218,6 +242,9 @@ def self_attention(qkv, *, heads, scale=None, out=None):
     if scale is None:
         scale = (E // heads) ** -0.5 if heads >= 1 and E % heads == 0 else 1.0
     d = _lib.MxSelfAttnDesc(batch=B, n_tok=N, heads=heads, embed=E, dtype=_SA_DTYPES[qkv.dtype], scale=scale)
+    t = _lib.make_tuning(_tuning(tuning))
+    if t is not None:
+        d.tuning = _lib.ctypes.pointer(t)
     if out is None:
         out = torch.empty(B, N, E, dtype=qkv.dtype, device=qkv.device)
     nbytes = _lib.self_attention_workspace_bytes(d)  # 0 also for an invalid descriptor, which the call reports

@@ -33,6 +33,19 @@ int32_t fail(int32_t code, const char * fmt, ...) {
 
 bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int32_t check_tuning(const mx_attn_tuning * t) {
+    if (!t) return MX_ATTN_OK;
+    if (t->decode_splits < 0 || t->decode_splits > 32)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_splits (%d) must be 0 (planned) or 1..32", t->decode_splits);
+    if (t->decode_waves != 0 && t->decode_waves != 4 && t->decode_waves != 8)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_waves (%d) must be 0 (planned), 4 or 8", t->decode_waves);
+    if (t->decode_max_workgroups < 0)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_max_workgroups (%d) must be >= 0", t->decode_max_workgroups);
+    if (t->prefill_plan != 0 && t->prefill_plan != 2 && t->prefill_plan != 4 && t->prefill_plan != 8)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->prefill_plan (%d) must be 0 (planned), 2, 4 or 8", t->prefill_plan);
+    return MX_ATTN_OK;
+}
+
 // Checks shared by prefill and decode.
 int32_t check_desc(const mx_attn_desc * d) {
     if (!d) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
@@ -55,7 +68,7 @@ int32_t check_desc(const mx_attn_desc * d) {
         return fail(MX_ATTN_INVALID_ARGUMENT, "kv_stride (%lld) < n_head_kv * head_dim (%lld)", (long long)d->kv_stride, (long long)kvw);
     if (d->q_stride % 8 || d->kv_stride % 8 || d->out_stride % 8)
         return fail(MX_ATTN_INVALID_ARGUMENT, "strides must be multiples of 8 elements (16-byte rows)");
-    return MX_ATTN_OK;
+    return check_tuning(d->tuning);
 }
 
 int32_t hip_status(hipError_t e, const char * what) {
@@ -77,18 +90,14 @@ int32_t hip_status(hipError_t e, const char * what) {
 //     700 keys 7.5 -> 8.1 us and Llama-3-8B (hd 128) at 600-768 keys 9.8 -> 13.6 us, hence the bound.
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
 constexpr int kMinChunk = 256, kMaxSplits = 32, kOneSplitWork = 40960, kFewWorkgroups = 64;
-int workgroup_cap() {
-    const char * s = std::getenv("MX_ATTN_DECODE_WGS");  // tuning override, read per call
-    const int v = s ? std::atoi(s) : 0;
-    return v > 0 ? v : 1536;
+int workgroup_cap(const mx_attn_tuning * t) {
+    return t && t->decode_max_workgroups > 0 ? t->decode_max_workgroups : 1536;
 }
 
 // Waves per workgroup: 8 when the launch has fewer workgroups than the chip has CUs (short or few sequences: each wave
 // then walks half as many 32-key blocks one after another, and the CUs are idle anyway), else 4.
-int decode_waves(int64_t wgs) {
-    const char * s = std::getenv("MX_ATTN_DECODE_WAVES");  // tuning override, read per call
-    const int v = s ? std::atoi(s) : 0;
-    if (v == 4 || v == 8) return v;
+int decode_waves(const mx_attn_tuning * t, int64_t wgs) {
+    if (t && t->decode_waves) return t->decode_waves;
     return wgs <= 256 ? 8 : 4;
 }
 
@@ -178,7 +187,8 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.p0 = d.p0;
     p.n_kv = (int32_t)n_kv;
     p.causal = d.causal;
-    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim);
+    p.plan = d.tuning ? d.tuning->prefill_plan : 0;
+    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim, p.plan);
     p.n_qtiles = (d.n_q + rows - 1) / rows;
     p.scale_log2 = d.scale * 1.4426950408889634f;
     p.rope = rope != nullptr;
@@ -298,8 +308,11 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         if (launch_wgs(chunk) < kFewWorkgroups)
             chunk = std::max<int64_t>(quantum, round_up((lmax + kMaxSplits - 1) / kMaxSplits));
         if (lmax * d.head_dim <= kOneSplitWork) chunk = round_up(lmax);  // short caches: one split, no merge
-        const int64_t cap = workgroup_cap();
-        if (launch_wgs(chunk) > cap) {  // smallest chunk within the cap: bisect over multiples of the quantum
+        const int64_t cap = workgroup_cap(d.tuning);
+        if (d.tuning && d.tuning->decode_splits > 0) {
+            // the caller's split count (of the longest sequence): never more than one split per quantum of keys
+            chunk = round_up((lmax + d.tuning->decode_splits - 1) / d.tuning->decode_splits);
+        } else if (launch_wgs(chunk) > cap) {  // smallest chunk within the cap: bisect over multiples of the quantum
             int64_t lo = chunk / quantum, hi = round_up(lmax) / quantum;
             while (lo < hi) {
                 const int64_t mid = (lo + hi) / 2;
@@ -320,7 +333,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
             p.max_split = std::max(p.max_split, p.seq[i].n_split);
         }
         for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
-        const int waves = decode_waves(launch_wgs(p.chunk));
+        const int waves = decode_waves(d.tuning, launch_wgs(p.chunk));
         if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, waves, st), "decode launch")) return rc;
     }
     return MX_ATTN_OK;
@@ -361,6 +374,7 @@ int32_t check_self_attn(const mx_self_attn_desc * d) {
         return fail(MX_ATTN_INVALID_ARGUMENT, "self_attention: embedding %d is not divisible by %d heads", d->embed, d->heads);
     if (d->dtype < MX_ATTN_F32 || d->dtype > MX_ATTN_BF16) return fail(MX_ATTN_INVALID_ARGUMENT, "dtype %d is not f32, f16 or bf16", d->dtype);
     if (!std::isfinite(d->scale)) return fail(MX_ATTN_INVALID_ARGUMENT, "self_attention: scale must be finite");
+    if (int32_t rc = check_tuning(d->tuning)) return rc;
     if (d->embed / d->heads > mx::kMaxHeadDim)
         return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is above %d", d->embed / d->heads, mx::kMaxHeadDim);
     if ((int64_t)d->batch * d->n_tok * 3 * d->embed > ((int64_t)1 << 40)) return fail(MX_ATTN_INVALID_ARGUMENT, "qkv is too large");
@@ -431,7 +445,8 @@ MX_ATTN_API int32_t mx_self_attention(const mx_self_attn_desc * desc, const void
     p.n_q = p.n_kv = d.n_tok;
     p.p0 = 0;
     p.causal = 0;
-    const int rpw = mx::prefill_rows_per_workgroup(d.n_tok, d.heads * d.batch, d.n_tok, s.hdp);
+    p.plan = d.tuning ? d.tuning->prefill_plan : 0;
+    const int rpw = mx::prefill_rows_per_workgroup(d.n_tok, d.heads * d.batch, d.n_tok, s.hdp, p.plan);
     p.n_qtiles = (d.n_tok + rpw - 1) / rpw;
     p.scale_log2 = d.scale * 1.4426950408889634f;
     p.rope_mode = 2;

@@ -250,9 +250,14 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 #pragma unroll
                     for (int ks = 0; ks < KS; ks++)
                         if (k_lane_new && mt == mt_new) cur.k[mt][ks] = kn[ks];
+                // Key slots past L - 1 were clamped to row L - 1, whose memory holds what the cache had before this
+                // step (and which the row-tile-0 workgroup is overwriting). Their scores are masked, but a stale
+                // Inf/NaN there would survive the p = 0 product, so their value operand is zero instead.
 #pragma unroll
-                for (int i = 0; i < NLV; i++)
+                for (int i = 0; i < NLV; i++) {
                     if (v_lane_new && i == i_new) cur.v[i] = vn;
+                    else if (jb + KPL * i + vslot > L - 1) cur.v[i] = u32x4{0u, 0u, 0u, 0u};
+                }
             }
         }
         // S^T = K Q^T, 2 tiles of 16 keys: lane holds keys 16 mt + 4 sgrp + v of row srow

@@ -66,6 +66,7 @@ struct PrefillParams {
     // the IR self-attention's rows read in place (kernel variants for f32, bf16 or f16 rows): head_dim of the rows
     // (<= the kernel's, a multiple of 8; columns past it are zeros) and the elements between consecutive heads
     int32_t hdv, head_stride;
+    int32_t plan;  // workgroup plan fixed by the caller (8, 4 or 2), or 0: prefill_plan's choice
     float rope_freq[kMaxHeadDim / 2];
 };
 
@@ -121,7 +122,8 @@ int decode_rows_per_tile(int rows);
 hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, int waves, hipStream_t stream);
 hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 
-int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim);  // query rows one prefill workgroup covers
+// query rows one prefill workgroup covers (forced: a plan fixed by the caller, or 0)
+int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim, int forced);
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);

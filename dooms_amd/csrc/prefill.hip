@@ -26,7 +26,6 @@
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
-#include <cstdlib>
 
 namespace mx {
 
@@ -477,9 +476,7 @@ void prefill_kernel(PrefillParams p) {
 // 448-token prompt of 20 heads, 80 such workgroups, ran 9 % slower split).
 // Plans: 8 = 8 waves x 32 rows, 4 = 4 waves x 32 rows, 2 = 4 waves over 2 row tiles x 2 key halves (64 rows).
 constexpr int kCUs = 256;
-int prefill_plan(int n_q, int n_head, int n_kv, int head_dim) {
-    const char * s = std::getenv("MX_PREFILL_PLAN");  // tuning and test override, read per call
-    const int forced = s ? std::atoi(s) : 0;
+int prefill_plan(int n_q, int n_head, int n_kv, int head_dim, int forced) {
     if (forced == 2 || forced == 4 || forced == 8) return forced;
     const int64_t wg8 = (int64_t)((n_q + 255) / 256) * n_head, wg4 = (int64_t)((n_q + 127) / 128) * n_head;
     if (2 * wg4 <= kCUs && n_kv >= 8 * kBK) return 2;
@@ -489,8 +486,8 @@ int prefill_plan(int n_q, int n_head, int n_kv, int head_dim) {
     return cost8 <= cost4 ? 8 : 4;
 }
 
-int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim) {
-    return 32 * prefill_plan(n_q, n_head, n_kv, head_dim);
+int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim, int forced) {
+    return 32 * prefill_plan(n_q, n_head, n_kv, head_dim, forced);
 }
 
 // ---- the IR self-attention's operand packing (row f4): one thread per 8 consecutive padded head dims ----
@@ -602,7 +599,7 @@ void launch_prefill_t(const PrefillParams & p, int plan, int n_batch, int sa, hi
 
 hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, int sa, hipStream_t stream) {
     const bool pos = p.scale_log2 > 0.f;
-    const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv, head_dim);
+    const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv, head_dim, p.plan);
     if (p.n_qtiles != (p.n_q + 32 * plan - 1) / (32 * plan)) return hipErrorInvalidValue;  // planned with other inputs
     if (head_dim == 64) {
         if (pos) launch_prefill_t<64, true>(p, plan, n_batch, sa, stream);

@@ -94,6 +94,9 @@ struct LlamaAttentionConfig {  // the attention fields of LlamaDecoderConfig (me
     int32_t head_dim = 0;    // 64 or 128
     float rope_base = 10000.f;  // rotary frequency base (rope.freq_base)
     bool rope_neox = false;     // rotary pairs (i, i + head_dim / 2) (qwen2) instead of (2i, 2i + 1) (llama)
+    // Launch plans fixed for measuring, as the reference's prefill_tile (metal_llama_decoder.h:35-37); all 0: the
+    // library's plans. Not model metadata.
+    mx_attn_tuning tuning{};
 };
 
 class LlamaAttention {
@@ -213,6 +216,7 @@ private:
         d.kv_stride = kv_width();
         d.out_stride = out_stride ? out_stride : q_width();
         d.scale = 1.0f / std::sqrt((float)cfg_.head_dim);
+        d.tuning = &cfg_.tuning;
         return d;
     }
     LlamaAttentionConfig cfg_;
@@ -231,6 +235,10 @@ struct WhisperAttentionConfig {  // the attention fields of WhisperDecoderConfig
     int32_t n_text_ctx = 0;   // self-attention cache positions (448)
     int32_t n_audio_ctx = 0;  // cross-attention positions (1500)
     int32_t max_rows = 8;     // query rows per call: prompt rows, or beams for cross-attention
+    // cross-attention: splits of the audio positions (the reference's cross_splits, whisper_text_decoder.h:25);
+    // 0: the library's plan
+    int32_t cross_splits = 0;
+    mx_attn_tuning tuning{};  // the other plans (its decode_splits applies to self-attention); all 0: the library's
 };
 
 class WhisperAttention {
@@ -239,6 +247,7 @@ public:
                          uint16_t * cross_v, hipStream_t stream, std::unique_ptr<WhisperAttention> & out) {
         if (c.n_layer < 1 || c.n_state < 1 || c.n_head < 1 || c.n_text_ctx < 1 || c.n_audio_ctx < 1 || c.max_rows < 1)
             return {Code::InvalidArgument, "sizes must be >= 1"};
+        if (c.cross_splits < 0 || c.cross_splits > 32) return {Code::InvalidArgument, "cross_splits must be in [0, 32]"};
         if (c.n_state % c.n_head) return {Code::InvalidArgument, "n_state must be a multiple of n_head"};
         const int32_t hd = c.n_state / c.n_head;
         if (hd != 64 && hd != 128) return {Code::Unsupported, "head_dim " + std::to_string(hd) + " is not supported (64 or 128)"};
@@ -275,7 +284,7 @@ public:
     }
     // M query rows (greedy 1, or one per beam) over the layer's n_audio_ctx encoder keys/values.
     Status cross_attention(int32_t layer, const uint16_t * q, uint16_t * out, int32_t M) {
-        return run(layer, q, out, M, cfg_.n_audio_ctx, 0, cross_k(layer), cross_v(layer));
+        return run(layer, q, out, M, cfg_.n_audio_ctx, 0, cross_k(layer), cross_v(layer), true);
     }
 
     // The same three calls on the reference's f32 buffers (metal_whisper_decoder.mm:167-225): qkv rows are
@@ -305,6 +314,7 @@ public:
         if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
         if (M < 1 || M > cfg_.max_rows) return {Code::InvalidArgument, "rows must be in [1, max_rows]"};
         mx_attn_desc d = desc(M, 0);
+        d.tuning = &cross_tuning_;
         const int32_t n = cfg_.n_audio_ctx;
         const uint16_t * k = cross_k(layer);
         const uint16_t * v = cross_v(layer);
@@ -313,7 +323,9 @@ public:
 
 private:
     WhisperAttention(const WhisperAttentionConfig & c, uint16_t * sk, uint16_t * sv, uint16_t * ck, uint16_t * cv, hipStream_t s)
-        : cfg_(c), sk_(sk), sv_(sv), ck_(ck), cv_(cv), stream_(s) {}
+        : cfg_(c), sk_(sk), sv_(sv), ck_(ck), cv_(cv), stream_(s), cross_tuning_(c.tuning) {
+        cross_tuning_.decode_splits = c.cross_splits;
+    }
     mx_attn_desc desc(int32_t n_q, int32_t causal) const {
         mx_attn_desc d{};
         d.n_head = cfg_.n_head;
@@ -323,13 +335,15 @@ private:
         d.causal = causal;
         d.q_stride = d.kv_stride = d.out_stride = cfg_.n_state;
         d.scale = 1.0f / std::sqrt((float)head_dim());
+        d.tuning = &cfg_.tuning;
         return d;
     }
     Status run(int32_t layer, const uint16_t * q, uint16_t * out, int32_t M, int32_t n_keys, int32_t causal, const uint16_t * k,
-               const uint16_t * v) {
+               const uint16_t * v, bool cross = false) {
         if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
         if (M < 1 || M > cfg_.max_rows) return {Code::InvalidArgument, "rows must be in [1, max_rows]"};
         mx_attn_desc d = desc(M, causal);
+        if (cross) d.tuning = &cross_tuning_;
         return Status::from(mx_attn_decode(&d, 1, &n_keys, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
     }
     WhisperAttentionConfig cfg_;
@@ -338,6 +352,7 @@ private:
     uint16_t * ck_;
     uint16_t * cv_;
     hipStream_t stream_;
+    mx_attn_tuning cross_tuning_;
     Workspace ws_;
 };
 

@@ -87,7 +87,7 @@ private:
     SelfAttentionOp(int32_t heads, float scale, DType dtype, hipStream_t stream)
         : heads_(heads), scale_(scale), dtype_(dtype), stream_(stream) {}
     mx_self_attn_desc desc(int32_t batch, int32_t tokens, int32_t embed) const {
-        mx_self_attn_desc d;
+        mx_self_attn_desc d{};
         d.batch = batch;
         d.n_tok = tokens;
         d.heads = heads_;

@@ -49,7 +49,7 @@ extern "C" {
 #endif
 
 #define MX_ATTN_API __attribute__((visibility("default")))
-#define MX_ATTN_ABI_VERSION 1
+#define MX_ATTN_ABI_VERSION 2
 
 /* Return codes: the numbering of dooms_code (include/dooms/dooms_c.h:24-33). */
 #define MX_ATTN_OK 0
@@ -60,6 +60,21 @@ extern "C" {
 
 /* A HIP stream (hipStream_t); NULL is the legacy default stream. */
 typedef void * mx_attn_stream;
+
+/*
+ * Launch-plan choices a decoder may fix in its configuration instead of taking the library's plan: the counterpart of
+ * the reference's per-decoder tuning fields WhisperDecoderConfig::cross_splits (src/backend/whisper_text_decoder.h:25)
+ * and LlamaDecoderConfig::prefill_tile (src/backend/metal/metal_llama_decoder.h:37). Every field's 0 means "the
+ * library's plan"; results agree within the tolerance whatever the plan (only the summation order changes). The
+ * library reads no environment variable: these fields are the only way to change a plan.
+ */
+typedef struct mx_attn_tuning {
+    int32_t decode_splits;         /* decode: splits of each sequence's keys, 1..32 (cross_splits); 0: planned */
+    int32_t decode_waves;          /* decode: waves per workgroup, 4 or 8; 0: planned */
+    int32_t decode_max_workgroups; /* decode: workgroup cap of one launch for the split plan, >= 1; 0: 1536 */
+    int32_t prefill_plan;          /* flash prefill workgroups (prefill_tile): 8 = 8 waves x 32 query rows, 4 = 4 waves x
+                                      32 rows, 2 = 4 waves over 2 row tiles splitting each tile's key blocks; 0: planned */
+} mx_attn_tuning;
 
 /*
  * One attention problem: a superset of the reference's AttnParams (llama_kernels.h:496-507) without the rotary fields,
@@ -78,6 +93,7 @@ typedef struct mx_attn_desc {
     int64_t kv_stride;   /* elements between cache rows   (>= n_head_kv * head_dim) */
     int64_t out_stride;  /* elements between output rows  (>= n_head * head_dim) */
     float scale;         /* score scale, normally 1 / sqrt(head_dim); 0 is valid (uniform attention) */
+    const mx_attn_tuning * tuning;  /* NULL: the library's plans; else read during the call only */
 } mx_attn_desc;
 
 /* MX_ATTN_ABI_VERSION of the library. */
@@ -254,6 +270,7 @@ typedef struct mx_self_attn_desc {
     int32_t embed;   /* E, a multiple of heads (infer_self_attention, src/ir/shape_infer.cpp:156-171); head_dim <= 128 */
     int32_t dtype;   /* MX_ATTN_F32, MX_ATTN_F16 or MX_ATTN_BF16: of qkv and of y (the op keeps the input's dtype) */
     float scale;     /* finite; multiplies q k^T before the softmax (0: uniform attention) */
+    const mx_attn_tuning * tuning;  /* NULL, or prefill_plan fixes the workgroup plan (the decode fields are unused) */
 } mx_self_attn_desc;
 
 /*

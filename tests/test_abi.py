@@ -32,7 +32,7 @@ def exported():
 
 
 def test_library_loads():
-    assert _lib.lib().mx_attn_abi_version() == 1
+    assert _lib.lib().mx_attn_abi_version() == 2
 
 
 def test_exports_exactly_the_header():
@@ -45,13 +45,17 @@ def test_desc_layout_matches_c(tmp_path):
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mx_attn.h"\n'
                    'int main(void){printf("%zu %zu %zu %zu %zu\\n", sizeof(mx_attn_desc), offsetof(mx_attn_desc, reserved),'
                    ' offsetof(mx_attn_desc, q_stride), offsetof(mx_attn_desc, out_stride), offsetof(mx_attn_desc, scale));'
+                   'printf("%zu %zu %zu %zu\\n", offsetof(mx_attn_desc, tuning), sizeof(mx_attn_tuning),'
+                   ' offsetof(mx_attn_tuning, prefill_plan), offsetof(mx_self_attn_desc, tuning));'
                    'return 0;}\n')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
                    check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     D = _lib.MxAttnDesc
-    assert got == [ctypes.sizeof(D), D.reserved.offset, D.q_stride.offset, D.out_stride.offset, D.scale.offset]
+    T, S = _lib.MxAttnTuning, _lib.MxSelfAttnDesc
+    assert got == [ctypes.sizeof(D), D.reserved.offset, D.q_stride.offset, D.out_stride.offset, D.scale.offset,
+                   D.tuning.offset, ctypes.sizeof(T), T.prefill_plan.offset, S.tuning.offset]
 
 
 def desc(**kw):
@@ -89,6 +93,11 @@ def decode(d, lens=(100,), kp=None, vp=None, q=A, out=A, lse=0, ws=A, ws_bytes=1
     (dict(kv_stride=1016), _lib.INVALID_ARGUMENT, "kv_stride"),
     (dict(out_stride=100), _lib.INVALID_ARGUMENT, "out_stride"),
     (dict(q_stride=4100), _lib.INVALID_ARGUMENT, "multiples of 8"),
+    (dict(tuning=dict(decode_splits=33)), _lib.INVALID_ARGUMENT, "decode_splits"),
+    (dict(tuning=dict(decode_splits=-1)), _lib.INVALID_ARGUMENT, "decode_splits"),
+    (dict(tuning=dict(decode_waves=6)), _lib.INVALID_ARGUMENT, "decode_waves"),
+    (dict(tuning=dict(decode_max_workgroups=-2)), _lib.INVALID_ARGUMENT, "decode_max_workgroups"),
+    (dict(tuning=dict(prefill_plan=3)), _lib.INVALID_ARGUMENT, "prefill_plan"),
 ])
 def test_descriptor_checks(kw, code, msg):
     for call in (lambda d: prefill(d), lambda d: decode(d)):

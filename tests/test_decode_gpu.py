@@ -150,7 +150,7 @@ def test_scale_zero_is_mean_of_v(device):
     np.testing.assert_allclose(got[0, hd:], mean, atol=2e-3)
 
 
-def test_split_count_invariance(device, monkeypatch):
+def test_split_count_invariance(device):
     # the merge must not depend on how the keys are split (test_whisper.cpp:255-270 checks cross_splits 1, 7, 64)
     rng = np.random.default_rng(74)
     L, hd = 4000, 128
@@ -158,9 +158,9 @@ def test_split_count_invariance(device, monkeypatch):
     k = torch.from_numpy(normal_f16(rng, (L, 8 * hd))).to(device)
     v = torch.from_numpy(normal_f16(rng, (L, 8 * hd))).to(device)
     outs = []
-    for wgs in ["1", "7", "64", "100000"]:
-        monkeypatch.setenv("MX_ATTN_DECODE_WGS", wgs)
-        o, l = A.decode(q, [k], [v], [L], n_head=32, n_head_kv=8, head_dim=hd, want_lse=True)
+    plans = [dict(decode_max_workgroups=w) for w in (1, 7, 64, 100000)] + [dict(decode_splits=s) for s in (1, 7, 32)]
+    for t in plans:
+        o, l = A.decode(q, [k], [v], [L], n_head=32, n_head_kv=8, head_dim=hd, want_lse=True, tuning=t)
         outs.append((o.cpu().numpy().astype(np.float64), l.cpu().numpy()))
     for o, l in outs[1:]:
         assert np.abs(o - outs[0][0]).max() <= 2e-3
@@ -229,19 +229,19 @@ def test_f32_llama3_8b_batch3(device):
     run_decode_f32(device, 43, 32, 8, 128, [1, 700, 5000], check_heads=[0, 13, 31])
 
 
-@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("case", ["qwen513", "llama_b4", "whisper_cross_b5", "causal_rows", "gqa16_hd128"])
-def test_waves_per_workgroup(device, monkeypatch, waves, case):
+def test_waves_per_workgroup(device, waves, case):
     # both workgroup shapes (4 or 8 waves; the library picks 8 when a launch fits the CUs in one round) on every tile
     # size: rows per tile 4 (GQA 4), 8 (GQA 7, beam 5), 16 (causal rows, GQA 16)
-    monkeypatch.setenv("MX_ATTN_DECODE_WAVES", waves)
-    if case == "qwen513":
-        run_decode(device, 1, 14, 2, 64, [513])
-    elif case == "llama_b4":
-        run_decode(device, 34, 32, 8, 128, [6841, 1638, 33, 2721], check_heads=[0, 5, 31])
-    elif case == "whisper_cross_b5":
-        run_decode(device, 95, 20, 20, 64, [1500] * 5, n_q=1, shared_cache=True, check_heads=[0, 7, 19])
-    elif case == "causal_rows":
-        run_decode(device, 108, 14, 2, 64, [300], n_q=8, causal=True)
-    else:
-        run_decode(device, 114, 16, 1, 128, [777])
+    with A.tuning(decode_waves=waves):
+        if case == "qwen513":
+            run_decode(device, 1, 14, 2, 64, [513])
+        elif case == "llama_b4":
+            run_decode(device, 34, 32, 8, 128, [6841, 1638, 33, 2721], check_heads=[0, 5, 31])
+        elif case == "whisper_cross_b5":
+            run_decode(device, 95, 20, 20, 64, [1500] * 5, n_q=1, shared_cache=True, check_heads=[0, 7, 19])
+        elif case == "causal_rows":
+            run_decode(device, 108, 14, 2, 64, [300], n_q=8, causal=True)
+        else:
+            run_decode(device, 114, 16, 1, 128, [777])

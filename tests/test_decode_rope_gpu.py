@@ -30,13 +30,21 @@ def half_ulps(a, b):
 
 
 def run_rope(device, seed, n_head, n_head_kv, hd, kv_lens, mode, base, spare=3, qkv_pad=0, kv_pad=0,
-             check_heads=None):
+             check_heads=None, poison=False):
     rng = np.random.default_rng(seed)
     batch = len(kv_lens)
     qw, kvw = n_head * hd, n_head_kv * hd
     qkv = rng.standard_normal((batch, qw + 2 * kvw + qkv_pad), dtype=np.float32)
     kc = [rng.standard_normal((L + spare, kvw + kv_pad), dtype=np.float32).astype(np.float16) for L in kv_lens]
     vc = [rng.standard_normal((L + spare, kvw + kv_pad), dtype=np.float32).astype(np.float16) for L in kv_lens]
+    if poison:
+        # the row the step appends and the spare rows behind it hold Inf and NaN half patterns (fresh or pooled
+        # memory): the kernel must not let any of them reach the output
+        pats = np.array([0x7C00, 0xFC00, 0x7E00, 0xFFFF, 0x7C01], dtype=np.uint16)
+        for b, L in enumerate(kv_lens):
+            for c in (kc[b], vc[b]):
+                tail = c[L - 1:].view(np.uint16)
+                tail[...] = pats[np.arange(tail.size).reshape(tail.shape) % len(pats)]
     dk = [torch.from_numpy(k).to(device) for k in kc]
     dv = [torch.from_numpy(v).to(device) for v in vc]
     scale = 1.0 / np.sqrt(hd)
@@ -106,8 +114,23 @@ def test_rope_decode_rejects_shared_cache(device):
 
 
 # the new position in every wave of both workgroup shapes (4 or 8 waves of 32-key blocks per split)
-@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("L", [33, 100, 129, 200, 257, 8192])
-def test_rope_decode_waves_per_workgroup(device, monkeypatch, waves, L):
-    monkeypatch.setenv("MX_ATTN_DECODE_WAVES", waves)
-    run_rope(device, 500 + L, 32, 8, 128, [L], 0, 500000.0, check_heads=[0, 5, 17, 31] if L > 4000 else None)
+def test_rope_decode_waves_per_workgroup(device, waves, L):
+    with A.tuning(decode_waves=waves):
+        run_rope(device, 500 + L, 32, 8, 128, [L], 0, 500000.0, check_heads=[0, 5, 17, 31] if L > 4000 else None)
+
+
+# The appended row and the rows past it start as Inf / NaN: masked key slots of the last block are clamped to the new
+# row, and nothing read from that row's memory (stale, and being overwritten) may reach the output.
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("L", [1, 2, 33, 129, 8192])
+def test_rope_decode_poisoned_tail(device, waves, L):
+    with A.tuning(decode_waves=waves):
+        run_rope(device, 900 + L, 32, 8, 128, [L], 0, 500000.0, spare=40, poison=True,
+                 check_heads=[0, 5, 17, 31] if L > 4000 else None)
+
+
+@pytest.mark.parametrize("L", [1, 2, 65, 513])
+def test_rope_decode_poisoned_tail_hd64(device, L):
+    run_rope(device, 950 + L, 14, 2, 64, [L], 1, 1000000.0, spare=40, poison=True)

@@ -143,20 +143,20 @@ def test_equal_keys_mean_of_v(device):
 
 # every workgroup plan (8 or 4 waves of 32-row tiles, or 4 waves over two 32-row tiles each split over two key halves)
 # on the same problems: chunk offsets, non-causal, zero/negative scales, ragged ends, both head dims
-@pytest.mark.parametrize("plan", ["2", "4", "8"])
+@pytest.mark.parametrize("plan", [2, 4, 8])
 @pytest.mark.parametrize("case", ["gqa_hd128_chunks", "mha_hd64_noncausal", "neg_scale", "ragged_257", "one_block"])
-def test_workgroup_plans(device, monkeypatch, plan, case):
-    monkeypatch.setenv("MX_PREFILL_PLAN", plan)
-    if case == "gqa_hd128_chunks":
-        check_prefill(device, 200, 900, 8, 2, 128, rows=list(range(0, 900, 5)) + [899], chunk=300)
-    elif case == "mha_hd64_noncausal":
-        check_prefill(device, 201, 333, 6, 6, 64, causal=False)
-    elif case == "neg_scale":
-        check_prefill(device, 202, 400, 4, 2, 64, scale=-0.3)
-    elif case == "ragged_257":
-        check_prefill(device, 203, 257, 4, 1, 128)
-    else:
-        check_prefill(device, 204, 60, 4, 2, 64)
+def test_workgroup_plans(device, plan, case):
+    with A.tuning(prefill_plan=plan):
+        if case == "gqa_hd128_chunks":
+            check_prefill(device, 200, 900, 8, 2, 128, rows=list(range(0, 900, 5)) + [899], chunk=300)
+        elif case == "mha_hd64_noncausal":
+            check_prefill(device, 201, 333, 6, 6, 64, causal=False)
+        elif case == "neg_scale":
+            check_prefill(device, 202, 400, 4, 2, 64, scale=-0.3)
+        elif case == "ragged_257":
+            check_prefill(device, 203, 257, 4, 1, 128)
+        else:
+            check_prefill(device, 204, 60, 4, 2, 64)
 
 
 # mx_attn_prefill_ws: chunks of few rows on the split-KV decode kernel (n_q x group <= 512), larger ones on the flash

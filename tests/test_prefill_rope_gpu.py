@@ -107,11 +107,11 @@ def test_prompt_in_chunks_matches_one_call(device):
 
 
 # the reference's prompt path under every workgroup plan (see test_prefill_gpu.test_workgroup_plans)
-@pytest.mark.parametrize("plan", ["2", "4", "8"])
-def test_workgroup_plans(device, monkeypatch, plan):
-    monkeypatch.setenv("MX_PREFILL_PLAN", plan)
-    run_prefill_rope(device, 300, 14, 2, 64, 300, 170, 1, 1000000.0)
-    run_prefill_rope(device, 301, 8, 2, 128, 200, 0, 0, 500000.0)
+@pytest.mark.parametrize("plan", [2, 4, 8])
+def test_workgroup_plans(device, plan):
+    with A.tuning(prefill_plan=plan):
+        run_prefill_rope(device, 300, 14, 2, 64, 300, 170, 1, 1000000.0)
+        run_prefill_rope(device, 301, 8, 2, 128, 200, 0, 0, 500000.0)
 
 
 # mx_attn_prefill_rope_ws: chunks of few rows take the split-KV kernel (keys/values cached and queries rotated by

@@ -103,8 +103,8 @@ def test_errors_leave_output_untouched():
 
 
 # the batched launch under every prefill workgroup plan (the batch runs along the grid's second dimension)
-@pytest.mark.parametrize("plan", ["2", "4", "8"])
+@pytest.mark.parametrize("plan", [2, 4, 8])
 @pytest.mark.parametrize("B,N,H,D,dtype", [(1, 210, 16, 80, "f32"), (3, 300, 4, 64, "f16"), (2, 400, 2, 128, "bf16")])
-def test_workgroup_plans(monkeypatch, plan, B, N, H, D, dtype):
-    monkeypatch.setenv("MX_PREFILL_PLAN", plan)
-    run(B, N, H, D, dtype)
+def test_workgroup_plans(plan, B, N, H, D, dtype):
+    with A.tuning(prefill_plan=plan):
+        run(B, N, H, D, dtype)
