@@ -20,19 +20,34 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every HIP source into dooms_amd/libmx_attn.so; returns its path. Raises on a compile error."""
-    cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-           *[os.path.join(CSRC, s) for s in SOURCES], "-lhipblaslt", "-o", LIB + ".tmp"]
+def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    msg = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{msg}")
-    if verbose and msg.strip():
-        print(msg, file=sys.stderr)
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+    return r.returncode, "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
+
+
+def build(verbose: bool = False, out: str = LIB, defines=()) -> str:
+    """Compiles every HIP source (one hipcc per source, in parallel) and links dooms_amd/libmx_attn.so; returns its
+    path. Raises on a compile error. `out` and `defines` (extra -D macros) serve experiments that build variants."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = os.path.join(os.path.dirname(out), "_build")
+    os.makedirs(objdir, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC, *[f"-D{d}" for d in defines]]
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    jobs = [[HIPCC, *compile_flags, *inc, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        results = list(ex.map(_run, jobs))
+    msgs = "\n".join(m for _, m in results if m.strip())
+    if any(rc != 0 for rc, _ in results):
+        raise RuntimeError(f"hipcc failed:\n{msgs}")
+    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-lhipblaslt", "-o", out + ".tmp"])
+    if rc != 0:
+        raise RuntimeError(f"link failed ({rc}):\n{msg}")
+    if verbose and (msgs + msg).strip():
+        print(msgs + msg, file=sys.stderr)
+    os.replace(out + ".tmp", out)
+    return out
 
 
 TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host_attention.cpp")

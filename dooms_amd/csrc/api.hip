@@ -76,29 +76,32 @@ int32_t hip_status(hipError_t e, const char * what) {
     return fail(MX_ATTN_INTERNAL, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Decode split plan. Splits are whole multiples of kDecodeChunkQuantum keys, and
-//   * at least kMinChunk keys and at most kMaxSplits splits per sequence: every extra split lengthens the in-kernel
-//     merge (measured: 64 splits of an 8192-key Llama-3-8B row cost ~5 us more than 32);
-//   * or, when that leaves fewer than kFewWorkgroups workgroups, splits of 128 keys: Llama-3-8B at 700 keys (24 -> 48
-//     workgroups) 9.75 -> 8.9 us, Qwen2.5-0.5B at 900 keys 7.45 -> 7.0 us; with 120 workgroups (Whisper cross-attention,
-//     20 heads over 1500 frames) the smaller chunk was 15 % slower;
+// Decode split plan. Splits are whole multiples of kDecodeChunkQuantum (128) keys, and
+//   * as short as that allows with at most kMaxSplits splits per sequence: every wave of a 4-wave workgroup then
+//     walks one 32-key block (more splits lengthen the in-kernel merge: 64 splits of an 8192-key Llama-3-8B row cost
+//     ~5 us more than 32);
 //   * then as small as possible while the launch stays within workgroup_cap() workgroups (measured on MI355X for
 //     Llama-3-8B batches of 4 and 16: 1536 streams best; two workgroups per CU are resident at once, 512 in all).
-//   * but when the longest sequence is short (keys x head_dim <= kOneSplitWork: at most 20 KB of K and V for each of
-//     the 8 waves), one split per sequence: the waves of its workgroup walk the keys and no merge follows. Measured:
-//     Qwen2.5-0.5B at 513 keys 7.6 -> 6.8 us, Whisper self-attention at 449 keys 8.3 -> 7.7 us; but Qwen2.5-0.5B at
-//     700 keys 7.5 -> 8.1 us and Llama-3-8B (hd 128) at 600-768 keys 9.8 -> 13.6 us, hence the bound.
+// With every split counter on a line of its own (kCounterStride), splitting pays down to the shortest caches: one
+// split per sequence (no merge) no longer wins anywhere measured, e.g. Qwen2.5-0.5B at 513 keys 7.0 us as one split
+// of 8 waves vs 6.5 us as 5 splits of 4 waves, Whisper self-attention at 449 keys 7.1 -> 6.7 us; and 128-key splits
+// beat 256-key ones at every size measured below 32 x 256 keys (Whisper cross-attention over 1500 frames: 7.8 ->
+// 7.25 us, Llama-3-8B at 1024 keys 8.9 -> 8.1 us).
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
-constexpr int kMinChunk = 256, kMaxSplits = 32, kOneSplitWork = 40960, kFewWorkgroups = 64;
+constexpr int kMaxSplits = 32;
 int workgroup_cap(const mx_attn_tuning * t) {
     return t && t->decode_max_workgroups > 0 ? t->decode_max_workgroups : 1536;
 }
 
-// Waves per workgroup: 8 when the launch has fewer workgroups than the chip has CUs (short or few sequences: each wave
-// then walks half as many 32-key blocks one after another, and the CUs are idle anyway), else 4.
-int decode_waves(const mx_attn_tuning * t, int64_t wgs) {
+// Waves per workgroup: 8 when splits of at least 256 keys give each of them a 32-key block and the launch runs in one
+// round on the CUs (at most 256 workgroups), each wave then walking half as many blocks (Llama-3-8B at 8192 keys, 256
+// workgroups, 15.1 -> 14.4 us; Qwen2.5-7B at 32768 keys, 128 workgroups of 1024 keys, 32.2 -> 29.0 us); else 4: with
+// 128-key splits the 4-wave workgroup's merge is cheaper (Whisper cross-attention 7.8 -> 7.25 us; Llama-3-8B at 1024
+// keys 8.8 -> 8.1 us), and with more workgroups 8-wave ones would not all be resident at once (Llama-3-8B batch 4:
+// 26.0 -> 20.6 us).
+int decode_waves(const mx_attn_tuning * t, int64_t chunk, int64_t wgs) {
     if (t && t->decode_waves) return t->decode_waves;
-    return wgs <= 256 ? 8 : 4;
+    return chunk >= 256 && wgs <= 256 ? 8 : 4;
 }
 
 struct DecodeShape {
@@ -127,7 +130,7 @@ WsLayout decode_ws_layout(const mx_attn_desc * d, int32_t batch, int32_t max_kv_
     const int64_t max_split = std::min<int64_t>(kMaxSplits, ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum);
     WsLayout w{0, 0};
     if (max_split <= 1) return w;  // one split per sequence: no partials, no counters
-    w.counter_bytes = (size_t)((seqs * d->n_head_kv * s.n_rowtiles * 4 + 255) / 256 * 256);
+    w.counter_bytes = (size_t)(seqs * d->n_head_kv * s.n_rowtiles * mx::kCounterStride * 4);
     w.part_bytes = (size_t)(seqs * d->n_head_kv * s.n_rowtiles * max_split * s.rt * (d->head_dim + 4) * (int64_t)sizeof(float));
     return w;
 }
@@ -298,16 +301,12 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         int64_t lmax = 0;
         for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
         auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
-        int64_t chunk = std::max<int64_t>(round_up(kMinChunk), round_up((lmax + kMaxSplits - 1) / kMaxSplits));
+        int64_t chunk = round_up((lmax + kMaxSplits - 1) / kMaxSplits);
         auto launch_wgs = [&](int64_t c) {
             int64_t n = 0;
             for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
             return n * d.n_head_kv * s.n_rowtiles;
         };
-        // few workgroups at the minimum chunk: halve it, so that twice as many CUs stream the keys
-        if (launch_wgs(chunk) < kFewWorkgroups)
-            chunk = std::max<int64_t>(quantum, round_up((lmax + kMaxSplits - 1) / kMaxSplits));
-        if (lmax * d.head_dim <= kOneSplitWork) chunk = round_up(lmax);  // short caches: one split, no merge
         const int64_t cap = workgroup_cap(d.tuning);
         if (d.tuning && d.tuning->decode_splits > 0) {
             // the caller's split count (of the longest sequence): never more than one split per quantum of keys
@@ -333,7 +332,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
             p.max_split = std::max(p.max_split, p.seq[i].n_split);
         }
         for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
-        const int waves = decode_waves(d.tuning, launch_wgs(p.chunk));
+        const int waves = decode_waves(d.tuning, p.chunk, launch_wgs(p.chunk));
         if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, waves, st), "decode launch")) return rc;
     }
     return MX_ATTN_OK;

@@ -375,7 +375,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t done = __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t done = __hip_atomic_fetch_add(p.counters + tile * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = done == (uint32_t)(sq.n_split - 1);
     }
     __syncthreads();
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         store_pair<F32>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 * inv, a1 * inv);
         if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
     }
-    if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int HD, int RT, int NW>

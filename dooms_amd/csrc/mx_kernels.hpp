@@ -14,6 +14,9 @@ constexpr int kMaxHeadDim = 128;
 constexpr int kMaxSeqPerLaunch = 32;
 // Keys per split are a multiple of this (4 waves x 32-key blocks), and never fewer.
 constexpr int kDecodeChunkQuantum = 128;
+// Split counters kCounterStride uint32 (256 bytes) apart: each on a line of its own, so that the atomics of different
+// tiles do not serialize on one line.
+constexpr int kCounterStride = 64;
 
 struct DecodeSeq {
     const half_t * k;
