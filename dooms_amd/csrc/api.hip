@@ -116,21 +116,32 @@ DecodeShape decode_shape(const mx_attn_desc * d) {
     return s;
 }
 
-// Workspace layout: the split counters (one uint32 per (sequence of a launch, kv head, row tile)), padded to 256 bytes,
-// then the partials. Launches of more than kMaxSeqPerLaunch sequences run one after another on the stream and reuse
-// both (every launch leaves the counters at 0).
+// Workspace layout: kMaxTilesPerLaunch split counters (one per (sequence of a launch, kv head, row tile), each on a
+// 256-byte line of its own) at a fixed place, then the partials. The counters must be zero when a call starts, and
+// every call leaves the ones it used at zero; the partials are left as they are. So the counter region has the same
+// place and size in every call, whatever its shape: a call of another shape on the same workspace must never write
+// partials where a counter lies. Launches of more sequences than fit run one after another and reuse both.
+constexpr int64_t kMaxTilesPerLaunch = 2048;
+constexpr size_t kCounterRegion = (size_t)kMaxTilesPerLaunch * mx::kCounterStride * 4;  // 512 KiB
+
+// Sequences one decode launch takes (0: a sequence alone has more tiles than a launch holds).
+int64_t decode_seqs_per_launch(const mx_attn_desc * d, int64_t n_rowtiles) {
+    const int64_t tiles_per_seq = (int64_t)d->n_head_kv * n_rowtiles;
+    return std::min<int64_t>(mx::kMaxSeqPerLaunch, kMaxTilesPerLaunch / tiles_per_seq);
+}
+
 struct WsLayout {
     size_t counter_bytes, part_bytes;
 };
 
 WsLayout decode_ws_layout(const mx_attn_desc * d, int32_t batch, int32_t max_kv_len) {
     const DecodeShape s = decode_shape(d);
-    const int64_t seqs = std::min<int64_t>(batch, mx::kMaxSeqPerLaunch);
+    const int64_t seqs = std::min<int64_t>(batch, std::max<int64_t>(1, decode_seqs_per_launch(d, s.n_rowtiles)));
     // the split plan never makes more than kMaxSplits splits of a sequence, nor more than one per quantum of keys
     const int64_t max_split = std::min<int64_t>(kMaxSplits, ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum);
     WsLayout w{0, 0};
     if (max_split <= 1) return w;  // one split per sequence: no partials, no counters
-    w.counter_bytes = (size_t)(seqs * d->n_head_kv * s.n_rowtiles * mx::kCounterStride * 4);
+    w.counter_bytes = kCounterRegion;
     w.part_bytes = (size_t)(seqs * d->n_head_kv * s.n_rowtiles * max_split * s.rt * (d->head_dim + 4) * (int64_t)sizeof(float));
     return w;
 }
@@ -262,13 +273,12 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     const WsLayout wl = decode_ws_layout(desc, batch, max_len);
 
     const DecodeShape s = decode_shape(desc);
-    // one launch holds at most 65535 (sequence, kv head, row tile) tiles, so its 1-D grid of up to 32 splits per tile
-    // stays far inside the grid's range
-    const int64_t tiles_per_seq = (int64_t)d.n_head_kv * s.n_rowtiles;
-    if (tiles_per_seq > 65535)
+    // one launch holds at most kMaxTilesPerLaunch (sequence, kv head, row tile) tiles (so its 1-D grid of up to 32
+    // splits per tile stays far inside the grid's range)
+    const int32_t seq_per_launch = (int32_t)decode_seqs_per_launch(desc, s.n_rowtiles);
+    if (seq_per_launch < 1)
         return fail(MX_ATTN_UNSUPPORTED, "n_head * n_q (%lld query rows per sequence) is too large for one decode launch",
                     (long long)d.n_head * d.n_q);
-    const int32_t seq_per_launch = (int32_t)std::min<int64_t>(mx::kMaxSeqPerLaunch, 65535 / tiles_per_seq);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     for (int32_t b0 = 0; b0 < batch; b0 += seq_per_launch) {
         const int n_seq = std::min<int32_t>(seq_per_launch, batch - b0);
@@ -351,6 +361,7 @@ int64_t prefill_split_keys(const mx_attn_desc & d);
 bool prefill_split_route(const mx_attn_desc & d) {
     if (d.n_q < 1) return false;
     const int64_t rows = (int64_t)d.n_q * (d.n_head / d.n_head_kv);
+    if (decode_seqs_per_launch(&d, decode_shape(&d).n_rowtiles) < 1) return false;
     return rows <= kPrefillSplitRows ||
            (rows <= kPrefillSplitRowsLong && prefill_split_keys(d) >= kPrefillSplitKeysPerRow * d.n_q);
 }

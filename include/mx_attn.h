@@ -161,7 +161,8 @@ MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc);
  * With causal = 1 query row t of sequence b attends keys 0 .. kv_len[b] - n_q + t (the decoder's prompt rows appended
  * at the end of the cache, as the reference's per-query kernel with p0 = kv_len - n_q); with causal = 0 every row
  * attends all kv_len[b] keys (cross-attention, or one decode row). desc->p0 and desc->n_kv are ignored.
- * MX_ATTN_UNSUPPORTED when one sequence has more than ~1M query rows (n_head * n_q; a prompt that size is a prefill).
+ * MX_ATTN_UNSUPPORTED when one sequence has more than 2048 (kv head, 16-row tile) pairs, n_head * n_q beyond about
+ * 32768 query rows (a prompt that size is a prefill).
  */
 MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const uint16_t * q,
                                    const uint16_t * const * k_caches, const uint16_t * const * v_caches, uint16_t * out,

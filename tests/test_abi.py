@@ -133,8 +133,9 @@ def test_decode_checks():
     assert decode(d, lens=(5000,), ws=0) == _lib.INVALID_ARGUMENT and "workspace is null" in _lib.last_error()
     assert decode(d, lens=(5000,), ws=A + 16) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
     assert decode(desc(n_q=0), lens=(5,)) == _lib.OK
-    # (kv head, row tile) pairs of one sequence beyond the grid's 65535: refused before anything is enqueued
+    # (kv head, row tile) pairs of one sequence beyond the 2048 one launch holds: refused before anything is enqueued
     assert decode(desc(n_q=40000, causal=0), lens=(100,)) == _lib.UNSUPPORTED and "too large" in _lib.last_error()
+    assert decode(desc(n_q=1025, causal=0), lens=(100,)) == _lib.UNSUPPORTED  # 8 kv heads x 257 tiles of 16 rows
 
 
 def rope_decode(d, mode=0, base=500000.0, lens=(100,), kp=None, vp=None, qkv=A, rope=True):
@@ -188,10 +189,10 @@ def test_workspace_size():
     assert ws(1, 1) == 0 and ws(1, 128) == 0  # one split: no partials
     assert ws(1, 129) > 0
     assert ws(1, 8192) <= ws(1, 8193) <= ws(4, 8193) <= ws(32, 8193) == ws(100, 8193)  # launches of 32 reuse it
-    # a 256-byte line per split counter (8 kv heads, one row tile), plus min(8192/128, 32) = 32 splits x 8 kv heads x
-    # 4 rows x (128 + 4) floats
-    assert ws(1, 8192) == 8 * 256 + 32 * 8 * 4 * 132 * 4
-    assert ws(1, 4096) == ws(1, 8192) and ws(1, 2048) == 8 * 256 + 16 * 8 * 4 * 132 * 4
+    # the fixed counter region (2048 lines of 256 bytes), plus min(8192/128, 32) = 32 splits x 8 kv heads x 4 rows x
+    # (128 + 4) floats
+    assert ws(1, 8192) == 2048 * 256 + 32 * 8 * 4 * 132 * 4
+    assert ws(1, 4096) == ws(1, 8192) and ws(1, 2048) == 2048 * 256 + 16 * 8 * 4 * 132 * 4
     assert _lib.decode_workspace_bytes(desc(n_head=3, n_head_kv=2), 1, 1000) == 0
     assert "multiple" in _lib.last_error()
 
@@ -200,9 +201,9 @@ def test_prefill_ws_checks():
     # the split-KV route for chunks of few rows: a decode workspace sized for the chunk's rows over p0 + n_q keys
     d16 = desc(n_head=28, n_head_kv=4, n_q=16, p0=30000, q_stride=3584, kv_stride=512, out_stride=3584)
     n = _lib.prefill_workspace_bytes(d16)  # 16 x 7 rows: 7 row tiles of 16 per kv head
-    # the decode workspace (28 counter lines, 32 splits of partials), then room for the rotated f32 query rows of the
+    # the decode workspace (the counter region, 32 splits of partials), then room for the rotated f32 query rows of the
     # rope call
-    assert n == 28 * 256 + 32 * 4 * 7 * 16 * 132 * 4 + 16 * 28 * 128 * 4
+    assert n == 2048 * 256 + 32 * 4 * 7 * 16 * 132 * 4 + 16 * 28 * 128 * 4
     big = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584)
     assert _lib.prefill_workspace_bytes(big) == 0  # the flash kernel, no workspace
     assert _lib.prefill_workspace_bytes(desc(n_head=3, n_head_kv=2)) == 0 and "multiple" in _lib.last_error()

@@ -245,3 +245,26 @@ def test_waves_per_workgroup(device, waves, case):
             run_decode(device, 108, 14, 2, 64, [300], n_q=8, causal=True)
         else:
             run_decode(device, 114, 16, 1, 128, [777])
+
+
+def test_workspace_shared_across_shapes(device):
+    """One workspace (sized for the largest call) serving calls of different shapes in turn, as a decoder's workspace
+    serves decode steps, batches and prompt chunks: a call's partials must never land where another call's split
+    counters lie. Every call is compared bit for bit with the same call on a fresh workspace."""
+    rng = np.random.default_rng(2024)
+    calls = [(32, 8, 128, [8192], 1, False), (32, 8, 128, [6841, 1638, 4000, 2721], 1, False),
+             (28, 4, 128, [3000], 64, True), (32, 8, 128, [700], 1, False), (14, 2, 64, [2000, 513], 1, False),
+             (32, 8, 128, [5000] * 6, 1, False), (28, 4, 128, [3000], 64, True)]
+    need = max(A.decode_workspace_bytes(n_head=nh, n_head_kv=nkv, head_dim=hd, n_q=nq, batch=len(lens),
+                                        max_kv_len=max(lens), causal=c) for nh, nkv, hd, lens, nq, c in calls)
+    shared = A.new_workspace(need, device)
+    for nh, nkv, hd, lens, nq, c in calls:
+        q = torch.from_numpy(normal_f16(rng, (len(lens) * nq, nh * hd))).to(device)
+        k = [torch.from_numpy(normal_f16(rng, (L, nkv * hd))).to(device) for L in lens]
+        v = [torch.from_numpy(normal_f16(rng, (L, nkv * hd))).to(device) for L in lens]
+        kw = dict(n_head=nh, n_head_kv=nkv, head_dim=hd, n_q=nq, causal=c, want_lse=True)
+        got, gl = A.decode(q, k, v, lens, workspace=shared, **kw)
+        ref, rl = A.decode(q, k, v, lens, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"{nh}/{nkv} {lens} n_q {nq}"
+        assert torch.equal(gl.view(torch.int32), rl.view(torch.int32))
