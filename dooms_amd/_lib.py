@@ -22,7 +22,7 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
 # Every symbol include/mx_attn.h declares.
 EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_prefill_ws",
            "mx_attn_prefill_workspace_bytes", "mx_attn_prefill_rope", "mx_attn_prefill_rope_ws", "mx_attn_decode",
-           "mx_attn_decode_f32", "mx_attn_decode_rope", "mx_linear", "mx_linear_workspace_bytes",
+           "mx_attn_decode_f32", "mx_attn_decode_noalloc", "mx_attn_decode_rope", "mx_linear", "mx_linear_workspace_bytes",
            "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init", "mx_self_attention",
            "mx_self_attention_workspace_bytes")
 
@@ -105,6 +105,9 @@ def lib() -> ctypes.CDLL:
         L.mx_attn_decode.restype = ctypes.c_int32
         L.mx_attn_decode.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), P,
                                      ctypes.POINTER(P), ctypes.POINTER(P), P, P, P, ctypes.c_size_t, P]
+        L.mx_attn_decode_noalloc.restype = ctypes.c_int32
+        L.mx_attn_decode_noalloc.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.POINTER(ctypes.c_int32),
+                                             P, ctypes.POINTER(P), ctypes.POINTER(P), P, P, P]
         L.mx_attn_decode_f32.restype = ctypes.c_int32
         L.mx_attn_decode_f32.argtypes = L.mx_attn_decode.argtypes
         L.mx_attn_prefill_rope.restype = ctypes.c_int32
@@ -190,6 +193,18 @@ def decode_raw(desc: MxAttnDesc, kv_len, q: int, k_ptrs, v_ptrs, out: int, lse: 
     vp = (ctypes.c_void_p * n)(*v_ptrs)
     return lib().mx_attn_decode(ctypes.byref(desc), n, lens, q, kp, vp, out, lse or None, ws or None, ws_bytes,
                                 stream or None)
+
+
+def decode_noalloc_raw(desc: MxAttnDesc, kv_len, q: int, k_ptrs, v_ptrs, out: int, lse: int, stream: int) -> int:
+    """mx_attn_decode_noalloc on raw device addresses (no workspace: the library's scratch); returns the code."""
+    n = len(kv_len)
+    lens = (ctypes.c_int32 * n)(*kv_len)
+    kp = (ctypes.c_void_p * n)(*k_ptrs)
+    vp = (ctypes.c_void_p * n)(*v_ptrs)
+    return lib().mx_attn_decode_noalloc(ctypes.byref(desc), n, lens, q, kp, vp, out, lse or None, stream or None)
+
+
+SCRATCH_BYTES = 16 << 20  # MX_ATTN_SCRATCH_BYTES
 
 
 def decode_f32_raw(desc: MxAttnDesc, kv_len, q: int, k_ptrs, v_ptrs, out: int, lse: int, ws: int, ws_bytes: int,

@@ -9,10 +9,12 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "mx_kernels.hpp"
@@ -419,6 +421,41 @@ SelfAttnPlan self_attn_plan(const mx_self_attn_desc & d) {
     return s;
 }
 
+// ---- scratch of mx_attn_decode_noalloc: the decode workspace held by the library ----
+// One array per GPU (each device that runs the library holds its own copy until the process ends). In host code the
+// name `scratch` is a host-side stand-in, not a device address: the address of a device's copy comes from
+// hipGetSymbolAddress, called once per device with that device current, and only that address is handed to kernels.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;  // taken only by the first call on a device
+
+// The current device's scratch address; on the first call on a device, its split counters are zeroed with a kernel on
+// `stream` (ordered before the call's own launch; no memset, no allocation).
+int32_t device_scratch(hipStream_t stream, void ** out) {
+    int dev = 0;
+    if (int32_t rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return fail(MX_ATTN_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+    void * p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_acquire);
+        if (!p) {
+            void * addr = nullptr;
+            if (int32_t rc = hip_status(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+                return rc;
+            if (!addr) return fail(MX_ATTN_INTERNAL, "hipGetSymbolAddress(scratch) returned null");
+            if (int32_t rc = hip_status(mx::launch_fill_zero(addr, kScratchBytes, stream), "scratch init")) return rc;
+            g_scratch[dev].store(addr, std::memory_order_release);
+            p = addr;
+        }
+    }
+    *out = p;
+    return MX_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -629,6 +666,28 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
     if (desc->n_q == 0) return MX_ATTN_OK;
     return decode_impl(desc, batch, kv_len, q, reinterpret_cast<const void * const *>(k_caches),
                        reinterpret_cast<const void * const *>(v_caches), out, lse, workspace, ws_bytes, stream, nullptr, false);
+}
+
+MX_ATTN_API int32_t mx_attn_decode_noalloc(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len,
+                                           const uint16_t * q, const uint16_t * const * k_caches,
+                                           const uint16_t * const * v_caches, uint16_t * out, float * lse,
+                                           mx_attn_stream stream) {
+    if (int32_t rc = check_desc(desc)) return rc;
+    if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
+    if (desc->n_q == 0) return MX_ATTN_OK;
+    if (!kv_len) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len must not be null");
+    int32_t max_len = 0;
+    for (int32_t b = 0; b < batch; b++) max_len = std::max(max_len, kv_len[b]);
+    const size_t need = decode_ws_bytes(desc, batch, max_len);
+    if (need > kScratchBytes)
+        return fail(MX_ATTN_RESOURCE_EXHAUSTED,
+                    "this decode needs %zu bytes of scratch; the library holds %zu per GPU (mx_attn_decode takes a larger "
+                    "workspace)", need, kScratchBytes);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    void * ws = nullptr;
+    if (int32_t rc = device_scratch(st, &ws)) return rc;
+    return decode_impl(desc, batch, kv_len, q, reinterpret_cast<const void * const *>(k_caches),
+                       reinterpret_cast<const void * const *>(v_caches), out, lse, ws, kScratchBytes, stream, nullptr, false);
 }
 
 MX_ATTN_API int32_t mx_attn_decode_f32(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const float * q,

@@ -169,6 +169,24 @@ MX_ATTN_API int32_t mx_attn_decode(const mx_attn_desc * desc, int32_t batch, con
                                    float * lse, void * workspace, size_t ws_bytes, mx_attn_stream stream);
 
 /*
+ * mx_attn_decode without a workspace argument: the split partials and counters live in a device array the library
+ * holds, MX_ATTN_SCRATCH_BYTES on each GPU it runs on (until the process ends). No counterpart in the reference; it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): it calls no hipMalloc, hipFree or other allocating routine. Arguments and results as mx_attn_decode.
+ *
+ * Returns MX_ATTN_RESOURCE_EXHAUSTED when the shape needs more scratch than that (mx_attn_decode_workspace_bytes >
+ * MX_ATTN_SCRATCH_BYTES; e.g. 32 Llama-3-8B sequences at 8192 keys need 17 MB). All calls on one GPU share its array,
+ * which each call leaves ready for the next: calls that overlap on one GPU (concurrent streams) race, so order them
+ * on one stream. The first call on a GPU initialises the array with a kernel on its stream; a call on another stream
+ * must be ordered after that one.
+ */
+#define MX_ATTN_SCRATCH_BYTES ((size_t)16 << 20)
+MX_ATTN_API int32_t mx_attn_decode_noalloc(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len,
+                                           const uint16_t * q, const uint16_t * const * k_caches,
+                                           const uint16_t * const * v_caches, uint16_t * out, float * lse,
+                                           mx_attn_stream stream);
+
+/*
  * mx_attn_decode on the reference's f32 buffers: q rows and the output are f32 (q_stride / out_stride in floats), the
  * caches f16; the query is rounded to half in the kernel. Replaces attention_split + attention_combine on the Whisper
  * decoder's f32 q / attn buffers (metal_whisper_decoder.mm:205-225, llama_kernels.h:856-929) and the per-query
