@@ -182,9 +182,10 @@ class PrefillProblem:
 class LinearProblem:
     """mx_linear launches over `layers` distinct weight sets (so that weights stream from HBM), one input."""
 
-    def __init__(self, torch, gen, M, N, K, flags, layers, count=1):
+    def __init__(self, torch, gen, M, N, K, flags, layers, count=1, plan=False):
         from dooms_amd import _lib
         self.torch, self._lib = torch, _lib
+        self.plan = None
         self.M, self.N, self.K, self.flags, self.layers, self.count = M, N, K, flags, layers, count
         dev = "cuda"
         self.x = torch.randn(M, K, generator=gen, device=dev)
@@ -198,10 +199,23 @@ class LinearProblem:
         nb = _lib.linear_workspace_bytes(self.desc)
         self.ws = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
         self.nb = nb
+        if plan:  # mx_linear_plan (hipBLASLt), made here, outside the timed region
+            self.plan = _lib.linear_plan_create(self.desc)
+
+    def __del__(self):
+        if self.plan:
+            self._lib.linear_plan_destroy(self.plan)
 
     def step(self):
         _lib = self._lib
+        stream = self.torch.cuda.current_stream().cuda_stream
         for l in range(self.layers):
+            if self.plan:
+                _lib.check(_lib.linear_plan_run(self.plan, self.w[l][0].data_ptr(), self.x.data_ptr(),
+                                                self.y[0].data_ptr(), self.gamma.data_ptr(),
+                                                self.bias[0].data_ptr() if self.flags & _lib.LINEAR_BIAS else 0,
+                                                self.ws.data_ptr(), self.nb, stream))
+                continue
             _lib.check(_lib.linear_raw(self.desc, [w.data_ptr() for w in self.w[l]], self.x.data_ptr(),
                                        [y.data_ptr() for y in self.y], self.gamma.data_ptr(),
                                        [b.data_ptr() for b in self.bias] if self.flags & _lib.LINEAR_BIAS else None,
@@ -544,15 +558,21 @@ def main():
         # ---- the projections either side of the attention (mx_linear): Llama-3-8B shapes, Whisper cross cache ----
         from dooms_amd import _lib as L
         lin = {}
-        for name, M, N, Kd, flags, layers, count in [
-                ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1),
-                ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1),
-                ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1),
-                ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8)]:
-            lp = LinearProblem(torch, gen, M, N, Kd, flags, layers, count)
+        # kernel: which code produced the figure ("gemv_kernel" / "stage_kernel + gemm_kernel": this library's, the
+        # mx_linear path; "stage_kernel + hipBLASLt": an mx_linear_plan, the vendor GEMM chosen at plan creation)
+        for name, M, N, Kd, flags, layers, count, plan, kernel in [
+                ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1, False, "gemv_kernel"),
+                ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1, False, "gemv_kernel"),
+                ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, False,
+                 "stage_kernel + gemm_kernel"),
+                ("plan_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, True,
+                 "stage_kernel + hipBLASLt (mx_linear_plan)"),
+                ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8, False,
+                 "stage_kernel + gemm_kernel")]:
+            lp = LinearProblem(torch, gen, M, N, Kd, flags, layers, count, plan=plan)
             ms_l, _ = time_graph(torch, lp.step, max(5, K), max(1, W))
             us = ms_l * 1e3 / layers
-            e = {"M": M, "N": N, "K": Kd, "count": count, "us_per_launch": round(us, 2)}
+            e = {"M": M, "N": N, "K": Kd, "count": count, "kernel": kernel, "us_per_launch": round(us, 2)}
             if M <= 8:
                 e["GBps_weights"] = round(lp.weight_bytes() / (us * 1e-6) / 1e9, 1)
                 e["roofline"] = {"bound": "hbm", "frac": round(e["GBps_weights"] / HBM_PEAK_GBS, 4)}

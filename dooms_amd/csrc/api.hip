@@ -456,7 +456,65 @@ int32_t device_scratch(hipStream_t stream, void ** out) {
     return MX_ATTN_OK;
 }
 
+int32_t check_linear_desc(const mx_linear_desc * desc, int32_t count) {
+    if (!desc) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
+    const mx_linear_desc & d = *desc;
+    if (d.reserved != 0) return fail(MX_ATTN_INVALID_ARGUMENT, "desc->reserved must be 0");
+    if (d.M < 0 || d.N < 1 || d.K < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "need M >= 0, N >= 1, K >= 1 (M %d, N %d, K %d)", d.M, d.N, d.K);
+    if (d.K % 32) return fail(MX_ATTN_UNSUPPORTED, "K (%d) must be a multiple of 32", d.K);
+    if (d.flags & ~15u) return fail(MX_ATTN_INVALID_ARGUMENT, "unknown flags 0x%x", d.flags);
+    const bool out16 = d.flags & MX_LINEAR_OUT_F16;
+    if (d.x_stride < d.K || d.x_stride % 4) return fail(MX_ATTN_INVALID_ARGUMENT, "x_stride (%lld) must be >= K and a multiple of 4", (long long)d.x_stride);
+    if (d.y_stride < d.N || d.y_stride % (out16 ? 8 : 4))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "y_stride (%lld) must be >= N and a multiple of %d", (long long)d.y_stride, out16 ? 8 : 4);
+    if ((d.flags & MX_LINEAR_RMS_NORM) && !(std::isfinite(d.eps) && d.eps >= 0.f)) return fail(MX_ATTN_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    if (count < 1 || count > mx::kLinearMaxMats) return fail(MX_ATTN_INVALID_ARGUMENT, "count (%d) must be in [1, %d]", count, mx::kLinearMaxMats);
+    return MX_ATTN_OK;
+}
+
+// Checks of an mx_linear call and its kernel parameters (for M == 0 only the descriptor is checked).
+int32_t linear_params(const mx_linear_desc * desc, int32_t count, const uint16_t * const * W, const float * X,
+                      void * const * Y, const float * gamma, const float * const * bias, void * workspace,
+                      size_t ws_bytes, mx::LinearParams & p) {
+    if (int32_t rc = check_linear_desc(desc, count)) return rc;
+    const mx_linear_desc & d = *desc;
+    if (d.M == 0) return MX_ATTN_OK;
+    if (!W || !Y || !X) return fail(MX_ATTN_INVALID_ARGUMENT, "W, X and Y must not be null");
+    if (!aligned16(X)) return fail(MX_ATTN_INVALID_ARGUMENT, "X must be 16-byte aligned");
+    if ((d.flags & MX_LINEAR_RMS_NORM) && (!gamma || !aligned16(gamma))) return fail(MX_ATTN_INVALID_ARGUMENT, "gamma must be a 16-byte aligned pointer with MX_LINEAR_RMS_NORM");
+    if ((d.flags & MX_LINEAR_BIAS) && !bias) return fail(MX_ATTN_INVALID_ARGUMENT, "bias is null with MX_LINEAR_BIAS");
+    for (int32_t i = 0; i < count; i++) {
+        if (!W[i] || !Y[i]) return fail(MX_ATTN_INVALID_ARGUMENT, "W[%d] or Y[%d] is null", i, i);
+        if (!aligned16(W[i]) || !aligned16(Y[i])) return fail(MX_ATTN_INVALID_ARGUMENT, "W[%d] and Y[%d] must be 16-byte aligned", i, i);
+        p.w[i] = reinterpret_cast<const mx::half_t *>(W[i]);
+        p.y[i] = Y[i];
+        p.bias[i] = (d.flags & MX_LINEAR_BIAS) ? bias[i] : nullptr;
+    }
+    const size_t need = linear_ws_bytes(d);
+    if (need && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u)))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "a 256-byte aligned workspace of %zu bytes is needed", need);
+    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+    p.x = X;
+    p.gamma = gamma;
+    p.xh = static_cast<mx::half_t *>(workspace);
+    p.x_stride = d.x_stride;
+    p.y_stride = d.y_stride;
+    p.M = d.M;
+    p.N = d.N;
+    p.K = d.K;
+    p.count = count;
+    p.flags = d.flags;
+    p.eps = d.eps;
+    return MX_ATTN_OK;
+}
+
 }  // namespace
+
+// A library GEMM plan (include/mx_linear.h): the descriptor it was made for and its hipBLASLt objects.
+struct mx_linear_plan {
+    mx_linear_desc desc;
+    mx::BlasPlan * blas;
+};
 
 extern "C" {
 
@@ -728,47 +786,55 @@ MX_ATTN_API size_t mx_linear_workspace_bytes(const mx_linear_desc * desc) {
 MX_ATTN_API int32_t mx_linear(const mx_linear_desc * desc, int32_t count, const uint16_t * const * W, const float * X,
                               void * const * Y, const float * gamma, const float * const * bias, void * workspace,
                               size_t ws_bytes, mx_attn_stream stream) {
-    if (!desc) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
-    const mx_linear_desc & d = *desc;
-    if (d.reserved != 0) return fail(MX_ATTN_INVALID_ARGUMENT, "desc->reserved must be 0");
-    if (d.M < 0 || d.N < 1 || d.K < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "need M >= 0, N >= 1, K >= 1 (M %d, N %d, K %d)", d.M, d.N, d.K);
-    if (d.K % 32) return fail(MX_ATTN_UNSUPPORTED, "K (%d) must be a multiple of 32", d.K);
-    if (d.flags & ~15u) return fail(MX_ATTN_INVALID_ARGUMENT, "unknown flags 0x%x", d.flags);
-    const bool out16 = d.flags & MX_LINEAR_OUT_F16;
-    if (d.x_stride < d.K || d.x_stride % 4) return fail(MX_ATTN_INVALID_ARGUMENT, "x_stride (%lld) must be >= K and a multiple of 4", (long long)d.x_stride);
-    if (d.y_stride < d.N || d.y_stride % (out16 ? 8 : 4))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "y_stride (%lld) must be >= N and a multiple of %d", (long long)d.y_stride, out16 ? 8 : 4);
-    if ((d.flags & MX_LINEAR_RMS_NORM) && !(std::isfinite(d.eps) && d.eps >= 0.f)) return fail(MX_ATTN_INVALID_ARGUMENT, "eps must be finite and >= 0");
-    if (count < 1 || count > mx::kLinearMaxMats) return fail(MX_ATTN_INVALID_ARGUMENT, "count (%d) must be in [1, %d]", count, mx::kLinearMaxMats);
-    if (d.M == 0) return MX_ATTN_OK;
-    if (!W || !Y || !X) return fail(MX_ATTN_INVALID_ARGUMENT, "W, X and Y must not be null");
-    if (!aligned16(X)) return fail(MX_ATTN_INVALID_ARGUMENT, "X must be 16-byte aligned");
-    if ((d.flags & MX_LINEAR_RMS_NORM) && (!gamma || !aligned16(gamma))) return fail(MX_ATTN_INVALID_ARGUMENT, "gamma must be a 16-byte aligned pointer with MX_LINEAR_RMS_NORM");
-    if ((d.flags & MX_LINEAR_BIAS) && !bias) return fail(MX_ATTN_INVALID_ARGUMENT, "bias is null with MX_LINEAR_BIAS");
     mx::LinearParams p;
-    for (int32_t i = 0; i < count; i++) {
-        if (!W[i] || !Y[i]) return fail(MX_ATTN_INVALID_ARGUMENT, "W[%d] or Y[%d] is null", i, i);
-        if (!aligned16(W[i]) || !aligned16(Y[i])) return fail(MX_ATTN_INVALID_ARGUMENT, "W[%d] and Y[%d] must be 16-byte aligned", i, i);
-        p.w[i] = reinterpret_cast<const mx::half_t *>(W[i]);
-        p.y[i] = Y[i];
-        p.bias[i] = (d.flags & MX_LINEAR_BIAS) ? bias[i] : nullptr;
-    }
-    const size_t need = linear_ws_bytes(d);
-    if (need && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u)))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "a 256-byte aligned workspace of %zu bytes is needed", need);
-    if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
-    p.x = X;
-    p.gamma = gamma;
-    p.xh = static_cast<mx::half_t *>(workspace);
-    p.x_stride = d.x_stride;
-    p.y_stride = d.y_stride;
-    p.M = d.M;
-    p.N = d.N;
-    p.K = d.K;
-    p.count = count;
-    p.flags = d.flags;
-    p.eps = d.eps;
+    if (int32_t rc = linear_params(desc, count, W, X, Y, gamma, bias, workspace, ws_bytes, p)) return rc;
+    if (desc->M == 0) return MX_ATTN_OK;
     return hip_status(mx::launch_linear(p, static_cast<hipStream_t>(stream)), "linear launch");
+}
+
+MX_ATTN_API int32_t mx_linear_plan_create(const mx_linear_desc * desc, mx_linear_plan ** plan) {
+    if (!plan) return fail(MX_ATTN_INVALID_ARGUMENT, "plan is null");
+    *plan = nullptr;
+    if (int32_t rc = check_linear_desc(desc, 1)) return rc;
+    if (desc->M <= mx::kLinearGemvMaxRows)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "a plan is for prompt chunks (M > %d, got %d): mx_linear runs fewer rows",
+                    mx::kLinearGemvMaxRows, desc->M);
+    int dev = 0;
+    if (int32_t rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    mx::LinearParams shape{};
+    shape.M = desc->M;
+    shape.N = desc->N;
+    shape.K = desc->K;
+    shape.count = 1;
+    shape.flags = desc->flags;
+    shape.x_stride = desc->x_stride;
+    shape.y_stride = desc->y_stride;
+    std::string err;
+    mx::BlasPlan * b = mx::blas_plan_create(shape, dev, err);
+    if (!b) return fail(MX_ATTN_UNSUPPORTED, "linear plan: %s", err.c_str());
+    *plan = new mx_linear_plan{*desc, b};
+    return MX_ATTN_OK;
+}
+
+MX_ATTN_API void mx_linear_plan_destroy(mx_linear_plan * plan) {
+    if (!plan) return;
+    mx::blas_plan_destroy(plan->blas);
+    delete plan;
+}
+
+MX_ATTN_API int32_t mx_linear_plan_run(mx_linear_plan * plan, const uint16_t * W, const float * X, void * Y,
+                                       const float * gamma, const float * bias, void * workspace, size_t ws_bytes,
+                                       mx_attn_stream stream) {
+    if (!plan) return fail(MX_ATTN_INVALID_ARGUMENT, "plan is null");
+    int dev = 0;
+    if (int32_t rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != mx::blas_plan_device(plan->blas))
+        return fail(MX_ATTN_INVALID_ARGUMENT, "the plan belongs to device %d, the current device is %d",
+                    mx::blas_plan_device(plan->blas), dev);
+    mx::LinearParams p;
+    if (int32_t rc = linear_params(&plan->desc, 1, &W, X, &Y, gamma, bias ? &bias : nullptr, workspace, ws_bytes, p))
+        return rc;
+    return hip_status(mx::blas_plan_run(plan->blas, p, static_cast<hipStream_t>(stream)), "linear plan run");
 }
 
 }  // extern "C"

@@ -20,15 +20,12 @@
 //     consecutive rows hit 16 distinct 4-bank groups), the step after next loading while the current step multiplies.
 //     Each wave owns a 64 x 64 block (2 x 2 MFMA tiles); two workgroups per CU.
 //   * Several matrices with the same input and shape (the cross cache's K and V of every layer) run in one launch.
-//   * A single matrix's GEMM after the staging is a plain library GEMM and runs on hipBLASLt (blas_gemm below).
-#include <hipblaslt/hipblaslt.h>
+//   * mx_linear runs these kernels only. A caller may instead create a plan (linear_plan.hip) that runs a single matrix's
+//     GEMM after the staging on hipBLASLt, chosen and set up at create time.
 
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
-#include <map>
-#include <mutex>
-#include <tuple>
 #include <type_traits>
 
 #include "mx_common.hpp"
@@ -449,87 +446,11 @@ hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
 
 }  // namespace
 
-namespace {
-
-// ---- the plain half GEMM after the staging, on hipBLASLt ----
-// After stage_kernel the prompt-chunk projection is a plain f16 x f16 -> f32 (or f16) GEMM with a bias epilogue and
-// beta = 1 for the residual: a library GEMM. hipBLASLt is column-major; with row-major Y [M][y_stride] = X W^T this is
-// Y^T (N x M, ld y_stride) = op(W) (N x K) . X^T (K x M): A is W read transposed (col-major K x N, ld K), B the staged
-// rows (col-major K x M, ld kp). One handle per device and one algorithm per shape, found once (heuristic, no
-// workspace) and cached; when hipBLASLt offers none, gemm_kernel above runs instead. MX_LINEAR_GEMM=hip forces gemm_kernel
-// (read per call: the tests run both). Measured on the Llama-3-8B q|k|v chunk (M 2048, N 6144, K 4096), staging included:
-// 871 TFLOP/s against gemm_kernel's 620.
-struct BlasPlan {
-    hipblasLtMatmulDesc_t op = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-    bool ok = false;
-};
-std::mutex g_blas_mu;  // guards the maps below and the per-call attributes of a plan's descriptor
-std::map<int, hipblasLtHandle_t> g_blas_handles;
-std::map<std::tuple<int, int, int, int, int64_t, uint32_t>, BlasPlan> g_blas_plans;
-
-const BlasPlan * blas_plan(const LinearParams & p, int kp, hipblasLtHandle_t h, int dev) {
-    const uint32_t shape_flags = p.flags & (kLinearAccumulate | kLinearOutF16 | kLinearBias);
-    const auto key = std::make_tuple(dev, p.M, p.N, p.K, p.y_stride * 4096 + kp, shape_flags);
-    auto it = g_blas_plans.find(key);
-    if (it != g_blas_plans.end()) return it->second.ok ? &it->second : nullptr;
-    BlasPlan & pl = g_blas_plans[key];
-    const hipDataType yt = (p.flags & kLinearOutF16) ? HIP_R_16F : HIP_R_32F;
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    const hipblasLtEpilogue_t ep = (p.flags & kLinearBias) ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
-    const hipDataType bt = HIP_R_32F;
-    hipblasLtMatmulPreference_t pref = nullptr;
-    bool ok = hipblasLtMatmulDescCreate(&pl.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof ep) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof bt) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16F, p.K, p.N, p.K) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16F, p.K, p.M, kp) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&pl.c, yt, p.N, p.M, p.y_stride) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
-    if (ok) {
-        const uint64_t ws = 0;
-        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws);
-        hipblasLtMatmulHeuristicResult_t res{};
-        int n = 0;
-        ok = hipblasLtMatmulAlgoGetHeuristic(h, pl.op, pl.a, pl.b, pl.c, pl.c, pref, 1, &res, &n) == HIPBLAS_STATUS_SUCCESS &&
-             n > 0 && res.state == HIPBLAS_STATUS_SUCCESS;
-        if (ok) pl.algo = res.algo;
-    }
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-    pl.ok = ok;
-    return ok ? &pl : nullptr;
+hipError_t launch_stage(const LinearParams & p, hipStream_t stream) {
+    if (p.flags & kLinearNorm) hipLaunchKernelGGL(stage_kernel<true>, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(stage_kernel<false>, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
 }
-
-// Runs the product on hipBLASLt (count == 1); done = false (and hipSuccess) when it offers no algorithm for the shape or
-// refuses the call (an operand alignment its algorithm does not take, for one), so that gemm_kernel runs instead: a
-// refused hipblasLtMatmul enqueues nothing.
-hipError_t blas_gemm(const LinearParams & p, int kp, hipStream_t stream, bool & done) {
-    done = false;
-    int dev = 0;
-    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(g_blas_mu);
-    hipblasLtHandle_t & h = g_blas_handles[dev];
-    if (!h && hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) {
-        h = nullptr;
-        return hipSuccess;
-    }
-    const BlasPlan * pl = blas_plan(p, kp, h, dev);
-    if (!pl) return hipSuccess;
-    const float alpha = 1.f, beta = (p.flags & kLinearAccumulate) ? 1.f : 0.f;
-    const hipblasLtEpilogue_t ep =
-        ((p.flags & kLinearBias) && p.bias[0]) ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
-    const void * bias = p.bias[0];
-    done = hipblasLtMatmulDescSetAttribute(pl->op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof ep) == HIPBLAS_STATUS_SUCCESS &&
-           hipblasLtMatmulDescSetAttribute(pl->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof bias) == HIPBLAS_STATUS_SUCCESS &&
-           hipblasLtMatmul(h, pl->op, &alpha, p.w[0], pl->a, p.xh, pl->b, &beta, p.y[0], pl->c, p.y[0], pl->c, &pl->algo,
-                           nullptr, 0, stream) == HIPBLAS_STATUS_SUCCESS;
-    return hipSuccess;
-}
-
-}  // namespace
 
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
     if (p.M <= kLinearGemvMaxRows) {
@@ -538,18 +459,11 @@ hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
         if (p.M <= 4) return launch_gemv_t<4>(p, stream);
         return launch_gemv_t<8>(p, stream);
     }
-    const bool norm = p.flags & kLinearNorm;
-    if (norm) hipLaunchKernelGGL(stage_kernel<true>, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL(stage_kernel<false>, dim3((uint32_t)p.M), dim3(kThreads), 0, stream, p);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    // one matrix: hipBLASLt; several (the cross cache's K and V of every layer) stay one launch of gemm_kernel, faster
-    // than a library call per matrix (measured: 8 x 1500 x 1280 x 1280, 434 vs 364 TFLOP/s)
-    const char * force = std::getenv("MX_LINEAR_GEMM");
-    if (p.count == 1 && !(force && std::strcmp(force, "hip") == 0)) {
-        bool done = false;
-        if (hipError_t e = blas_gemm(p, (p.K + kTK - 1) / kTK * kTK, stream, done); e != hipSuccess) return e;
-        if (done) return hipSuccess;
-    }
+    if (hipError_t e = launch_stage(p, stream); e != hipSuccess) return e;
+    return launch_gemm(p, stream);
+}
+
+hipError_t launch_gemm(const LinearParams & p, hipStream_t stream) {
     const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);
     const dim3 grid((uint32_t)tiles);
     if (p.flags & kLinearOutF16) hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, p);

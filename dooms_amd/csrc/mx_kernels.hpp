@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace mx {
 
 typedef _Float16 half_t;
@@ -129,6 +131,14 @@ hipError_t launch_fill_zero(void * p, size_t bytes, hipStream_t stream);
 int prefill_rows_per_workgroup(int n_q, int n_head, int n_kv, int head_dim, int forced);
 hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t stream);
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
+hipError_t launch_stage(const LinearParams & p, hipStream_t stream);  // M > 8: the staged half input rows
+hipError_t launch_gemm(const LinearParams & p, hipStream_t stream);   // M > 8: gemm_kernel on the staged rows
+// hipBLASLt plans (linear_plan.hip): created for one shape (count 1, M > 8) on one device
+struct BlasPlan;
+BlasPlan * blas_plan_create(const LinearParams & shape, int device, std::string & err);
+void blas_plan_destroy(BlasPlan * plan);
+int blas_plan_device(const BlasPlan * plan);
+hipError_t blas_plan_run(BlasPlan * plan, const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
 // n_batch problems of the prefill kernel along blockIdx.y, offsets from p.*_batch
 hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, int sa, hipStream_t stream);
