@@ -7,7 +7,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libmx_attn.so")
-SOURCES = ["api.hip", "decode.hip", "prefill.hip", "rope.hip", "linear.hip", "linear_plan.hip"]
+SOURCES = ["api.hip", "decode.hip", "prefill.hip", "rope.hip", "small.hip", "linear.hip", "linear_plan.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops off: the compiler must not emit packed f32 arithmetic (its host pass warns that it does not know

@@ -57,8 +57,8 @@ int32_t check_desc(const mx_attn_desc * d) {
     if (d->n_head % d->n_head_kv != 0)
         return fail(MX_ATTN_INVALID_ARGUMENT, "n_head (%d) is not a multiple of n_head_kv (%d)", d->n_head, d->n_head_kv);
     if (d->head_dim < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "head_dim (%d) must be >= 1", d->head_dim);
-    if (d->head_dim != 64 && d->head_dim != 128)
-        return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is not supported (64 or 128)", d->head_dim);
+    if (d->head_dim < 4 || d->head_dim > 256 || (d->head_dim & (d->head_dim - 1)) != 0)
+        return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is not supported (a power of two in [4, 256])", d->head_dim);
     if (d->n_q < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_q (%d) must be >= 0", d->n_q);
     if (d->causal != 0 && d->causal != 1) return fail(MX_ATTN_INVALID_ARGUMENT, "causal must be 0 or 1");
     if (!std::isfinite(d->scale)) return fail(MX_ATTN_INVALID_ARGUMENT, "scale is not finite");
@@ -68,8 +68,9 @@ int32_t check_desc(const mx_attn_desc * d) {
         return fail(MX_ATTN_INVALID_ARGUMENT, "out_stride (%lld) < n_head * head_dim (%lld)", (long long)d->out_stride, (long long)qw);
     if (d->kv_stride < kvw)
         return fail(MX_ATTN_INVALID_ARGUMENT, "kv_stride (%lld) < n_head_kv * head_dim (%lld)", (long long)d->kv_stride, (long long)kvw);
-    if (d->q_stride % 8 || d->kv_stride % 8 || d->out_stride % 8)
-        return fail(MX_ATTN_INVALID_ARGUMENT, "strides must be multiples of 8 elements (16-byte rows)");
+    const int unit = std::min(8, d->head_dim);  // 16-byte rows (8-byte ones at head dim 4)
+    if (d->q_stride % unit || d->kv_stride % unit || d->out_stride % unit)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "strides must be multiples of %d elements", unit);
     return check_tuning(d->tuning);
 }
 
@@ -126,6 +127,9 @@ DecodeShape decode_shape(const mx_attn_desc * d) {
 constexpr int64_t kMaxTilesPerLaunch = 2048;
 constexpr size_t kCounterRegion = (size_t)kMaxTilesPerLaunch * mx::kCounterStride * 4;  // 512 KiB
 
+// Head dims below this run on the per-query kernel (small.hip), at and above it on the matrix-core kernels.
+constexpr int kMfmaMinHeadDim = 64;
+
 // Sequences one decode launch takes (0: a sequence alone has more tiles than a launch holds).
 int64_t decode_seqs_per_launch(const mx_attn_desc * d, int64_t n_rowtiles) {
     const int64_t tiles_per_seq = (int64_t)d->n_head_kv * n_rowtiles;
@@ -142,7 +146,7 @@ WsLayout decode_ws_layout(const mx_attn_desc * d, int32_t batch, int32_t max_kv_
     // the split plan never makes more than kMaxSplits splits of a sequence, nor more than one per quantum of keys
     const int64_t max_split = std::min<int64_t>(kMaxSplits, ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum);
     WsLayout w{0, 0};
-    if (max_split <= 1) return w;  // one split per sequence: no partials, no counters
+    if (max_split <= 1 || d->head_dim < kMfmaMinHeadDim) return w;  // one split per sequence (or the per-query kernel)
     w.counter_bytes = kCounterRegion;
     w.part_bytes = (size_t)(seqs * d->n_head_kv * s.n_rowtiles * max_split * s.rt * (d->head_dim + 4) * (int64_t)sizeof(float));
     return w;
@@ -170,6 +174,47 @@ void fill_freq(float (&freq)[mx::kMaxHeadDim / 2], const mx_attn_rope * rope, in
         freq[i] = (rope && rope->mode != 2 && i < head_dim / 2) ? std::pow(rope->base, -2.f * (float)i / (float)head_dim) : 0.f;
 }
 
+// rope_store of n_rows q|k|v rows (f32, q_stride floats apart) at positions p0 .. into the caches.
+int32_t rope_store_rows(const mx_attn_desc & d, const mx_attn_rope * rope, const float * qkv, int32_t n_rows,
+                        int32_t p0, void * k_cache, void * v_cache, float * q_out, hipStream_t st) {
+    mx::RopeStoreParams r;
+    r.qkv = qkv;
+    r.k = static_cast<mx::half_t *>(k_cache);
+    r.v = static_cast<mx::half_t *>(v_cache);
+    r.qkv_stride = d.q_stride;
+    r.kv_stride = d.kv_stride;
+    r.n_head = d.n_head;
+    r.n_head_kv = d.n_head_kv;
+    r.n_rows = n_rows;
+    r.p0 = p0;
+    r.rope_mode = rope->mode;
+    r.q_out = q_out;
+    fill_freq(r.rope_freq, rope, d.head_dim);
+    return hip_status(mx::launch_rope_store(r, d.head_dim, st), "rope_store launch");
+}
+
+// The per-query kernel's parameters (head dims below kMfmaMinHeadDim) without the sequences.
+mx::SmallAttnParams small_params(const mx_attn_desc & d, const void * q, void * out, float * lse, bool f32,
+                                 const mx_attn_rope * rope) {
+    mx::SmallAttnParams sp{};
+    sp.q = q;
+    sp.out = out;
+    sp.lse = lse;
+    sp.q_stride = d.q_stride;
+    sp.kv_stride = d.kv_stride;
+    sp.out_stride = d.out_stride;
+    sp.n_head = d.n_head;
+    sp.n_head_kv = d.n_head_kv;
+    sp.group = d.n_head / d.n_head_kv;
+    sp.n_q = d.n_q;
+    sp.causal = d.causal;
+    sp.q_f32 = sp.out_f32 = f32 ? 1 : 0;
+    sp.rope_mode = rope ? rope->mode : 2;
+    sp.scale_log2 = d.scale * 1.4426950408889634f;
+    fill_freq(sp.rope_freq, rope, d.head_dim);
+    return sp;
+}
+
 int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_cache, const void * v_cache, void * out,
                      float * lse, mx_attn_stream stream, const mx_attn_rope * rope) {
     const mx_attn_desc & d = *desc;
@@ -186,6 +231,16 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
         return fail(MX_ATTN_INVALID_ARGUMENT, "q, k_cache, v_cache and out must be 16-byte aligned");
     if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (d.head_dim < kMfmaMinHeadDim) {  // the per-query kernel: the chunk's keys and values first (stream order)
+        if (rope)
+            if (int32_t rc = rope_store_rows(d, rope, static_cast<const float *>(q), d.n_q, d.p0, const_cast<void *>(k_cache),
+                                             const_cast<void *>(v_cache), nullptr, st))
+                return rc;
+        mx::SmallAttnParams sp = small_params(d, q, out, lse, rope != nullptr, rope);
+        sp.seq[0] = mx::SmallSeq{static_cast<const mx::half_t *>(k_cache), static_cast<const mx::half_t *>(v_cache),
+                                 (int32_t)n_kv, d.p0, 0};
+        return hip_status(mx::launch_small_attn(sp, d.head_dim, 1, st), "attention launch");
+    }
 
     mx::PrefillParams p;
     p.q = static_cast<const mx::half_t *>(q);
@@ -214,22 +269,10 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.q_batch = p.kv_batch = p.out_batch = p.lse_batch = 0;
     p.hdv = p.head_stride = d.head_dim;
     fill_freq(p.rope_freq, rope, d.head_dim);
-    if (rope) {  // the chunk's keys and values go into the caches first (stream order)
-        mx::RopeStoreParams r;
-        r.qkv = static_cast<const float *>(q);
-        r.k = static_cast<mx::half_t *>(const_cast<void *>(k_cache));
-        r.v = static_cast<mx::half_t *>(const_cast<void *>(v_cache));
-        r.qkv_stride = d.q_stride;
-        r.kv_stride = d.kv_stride;
-        r.n_head = d.n_head;
-        r.n_head_kv = d.n_head_kv;
-        r.n_rows = d.n_q;
-        r.p0 = d.p0;
-        r.rope_mode = rope->mode;
-        r.q_out = nullptr;
-        fill_freq(r.rope_freq, rope, d.head_dim);
-        if (int32_t rc = hip_status(mx::launch_rope_store(r, d.head_dim, st), "rope_store launch")) return rc;
-    }
+    if (rope)  // the chunk's keys and values go into the caches first (stream order)
+        if (int32_t rc = rope_store_rows(d, rope, static_cast<const float *>(q), d.n_q, d.p0, const_cast<void *>(k_cache),
+                                         const_cast<void *>(v_cache), nullptr, st))
+            return rc;
     return hip_status(mx::launch_prefill(p, d.head_dim, st), "prefill launch");
 }
 
@@ -275,6 +318,25 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     const WsLayout wl = decode_ws_layout(desc, batch, max_len);
 
     const DecodeShape s = decode_shape(desc);
+    if (d.head_dim < kMfmaMinHeadDim) {  // the per-query kernel; the fused step's cache rows written first
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        for (int32_t b0 = 0; b0 < batch; b0 += mx::kMaxSeqPerLaunch) {
+            const int n_seq = std::min<int32_t>(mx::kMaxSeqPerLaunch, batch - b0);
+            mx::SmallAttnParams sp = small_params(d, q, out, lse, f32, rope);
+            for (int i = 0; i < n_seq; i++) {
+                const int32_t b = b0 + i, L = kv_len[b];
+                if (rope)
+                    if (int32_t rc = rope_store_rows(d, rope, static_cast<const float *>(q) + (int64_t)b * d.q_stride, 1,
+                                                     L - 1, const_cast<void *>(k_caches[b]),
+                                                     const_cast<void *>(v_caches[b]), nullptr, st))
+                        return rc;
+                sp.seq[i] = mx::SmallSeq{static_cast<const mx::half_t *>(k_caches[b]),
+                                         static_cast<const mx::half_t *>(v_caches[b]), L, L - d.n_q, (int64_t)b * d.n_q};
+            }
+            if (int32_t rc = hip_status(mx::launch_small_attn(sp, d.head_dim, n_seq, st), "attention launch")) return rc;
+        }
+        return MX_ATTN_OK;
+    }
     // one launch holds at most kMaxTilesPerLaunch (sequence, kv head, row tile) tiles (so its 1-D grid of up to 32
     // splits per tile stays far inside the grid's range)
     const int32_t seq_per_launch = (int32_t)decode_seqs_per_launch(desc, s.n_rowtiles);
@@ -361,7 +423,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
 constexpr int64_t kPrefillSplitRows = 512, kPrefillSplitRowsLong = 1024, kPrefillSplitKeysPerRow = 64;
 int64_t prefill_split_keys(const mx_attn_desc & d);
 bool prefill_split_route(const mx_attn_desc & d) {
-    if (d.n_q < 1) return false;
+    if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim) return false;
     const int64_t rows = (int64_t)d.n_q * (d.n_head / d.n_head_kv);
     if (decode_seqs_per_launch(&d, decode_shape(&d).n_rowtiles) < 1) return false;
     return rows <= kPrefillSplitRows ||
@@ -377,6 +439,8 @@ size_t prefill_split_q_offset(const mx_attn_desc & d, int32_t L) { return (decod
 
 // ---- IR SelfAttention (src/ir/op.h:31-32) ----
 
+constexpr int kSelfAttnMaxHeadDim = 128;  // the IR op's heads are padded to the prefill kernel's 64 or 128
+
 int32_t check_self_attn(const mx_self_attn_desc * d) {
     if (!d) return fail(MX_ATTN_INVALID_ARGUMENT, "desc is null");
     if (d->batch < 1 || d->batch > 65535 || d->n_tok < 0)
@@ -387,8 +451,8 @@ int32_t check_self_attn(const mx_self_attn_desc * d) {
     if (d->dtype < MX_ATTN_F32 || d->dtype > MX_ATTN_BF16) return fail(MX_ATTN_INVALID_ARGUMENT, "dtype %d is not f32, f16 or bf16", d->dtype);
     if (!std::isfinite(d->scale)) return fail(MX_ATTN_INVALID_ARGUMENT, "self_attention: scale must be finite");
     if (int32_t rc = check_tuning(d->tuning)) return rc;
-    if (d->embed / d->heads > mx::kMaxHeadDim)
-        return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is above %d", d->embed / d->heads, mx::kMaxHeadDim);
+    if (d->embed / d->heads > kSelfAttnMaxHeadDim)
+        return fail(MX_ATTN_UNSUPPORTED, "head_dim %d is above %d", d->embed / d->heads, kSelfAttnMaxHeadDim);
     if ((int64_t)d->batch * d->n_tok * 3 * d->embed > ((int64_t)1 << 40)) return fail(MX_ATTN_INVALID_ARGUMENT, "qkv is too large");
     return MX_ATTN_OK;
 }

@@ -459,6 +459,8 @@ __global__ void fill_zero_kernel(uint32_t * p, size_t n) {
 int decode_rows_per_tile(int rows) { return rows <= 4 ? 4 : rows <= 8 ? 8 : 16; }
 
 hipError_t launch_decode(const DecodeParams & p, int n_seq, int head_dim, int rt, int waves, hipStream_t stream) {
+    // head dim 256: 4 waves only (8 would spill: the double-buffered K/V block and O take every register of a wave)
+    if (head_dim == 256) return launch_decode_hd<256, 4>(p, n_seq, rt, stream);
     if (head_dim == 64)
         return waves == 8 ? launch_decode_hd<64, 8>(p, n_seq, rt, stream) : launch_decode_hd<64, 4>(p, n_seq, rt, stream);
     return waves == 8 ? launch_decode_hd<128, 8>(p, n_seq, rt, stream) : launch_decode_hd<128, 4>(p, n_seq, rt, stream);

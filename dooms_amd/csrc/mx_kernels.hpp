@@ -12,7 +12,7 @@ namespace mx {
 typedef _Float16 half_t;
 
 // Sequences per decode launch: their cache pointers, lengths and split counts ride in the kernel arguments.
-constexpr int kMaxHeadDim = 128;
+constexpr int kMaxHeadDim = 256;
 constexpr int kMaxSeqPerLaunch = 32;
 // Keys per split are a multiple of this (4 waves x 32-key blocks), and never fewer.
 constexpr int kDecodeChunkQuantum = 128;
@@ -49,6 +49,27 @@ struct DecodeParams {
     int32_t rope_mode;   // 0 adjacent pairs, 1 split halves (neox), 2 none
     float rope_freq[kMaxHeadDim / 2];  // base^(-2i / head_dim) in f32 for rotary pair i
     DecodeSeq seq[kMaxSeqPerLaunch];
+};
+
+// The per-query kernel for head dims below 64 (small.hip): query row t of sequence s sits at cache position
+// seq[s].p0 + t (its rotary angle; with causal it sees keys 0 .. p0 + t), its row index is seq[s].row0 + t.
+struct SmallSeq {
+    const half_t * k;
+    const half_t * v;
+    int32_t len;   // keys in the cache
+    int32_t p0;    // position of the first query row
+    int64_t row0;  // first query / output row
+};
+struct SmallAttnParams {
+    const void * q;  // half rows, or f32 rows (q_f32)
+    void * out;      // half rows, or f32 rows (out_f32)
+    float * lse;
+    int64_t q_stride, kv_stride, out_stride;
+    int32_t n_head, n_head_kv, group, n_q, causal, q_f32, out_f32;
+    int32_t rope_mode;  // 0 adjacent pairs, 1 split halves (neox), 2 none: the query rotated for its position
+    float scale_log2;
+    float rope_freq[kMaxHeadDim / 2];
+    SmallSeq seq[kMaxSeqPerLaunch];
 };
 
 struct PrefillParams {
@@ -140,6 +161,7 @@ void blas_plan_destroy(BlasPlan * plan);
 int blas_plan_device(const BlasPlan * plan);
 hipError_t blas_plan_run(BlasPlan * plan, const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
+hipError_t launch_small_attn(const SmallAttnParams & p, int head_dim, int n_seq, hipStream_t stream);
 // n_batch problems of the prefill kernel along blockIdx.y, offsets from p.*_batch
 hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_batch, int sa, hipStream_t stream);
 hipError_t launch_self_attn_pack(const SelfAttnPackParams & p, hipStream_t stream);

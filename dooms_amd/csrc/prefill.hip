@@ -90,7 +90,7 @@ __device__ __forceinline__ void prefill_work(uint32_t o, int nq, int G, int n_kv
 // elements apart. Q, K and V are rounded to half as they are loaded (K and V when the tile goes into LDS, so the
 // prefetch stays in flight), columns past p.hdv read as zeros, and the output is written in the rows' type.
 template <int HD, bool POS, int W, bool ROPE, int KSP, int SA>
-__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 ? 2 : 1, KSP == 1 ? 2 : 1)))
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 && HD <= 128 ? 2 : 1, KSP == 1 && HD <= 128 ? 2 : 1)))
 void prefill_kernel(PrefillParams p) {
     constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
     static_assert(W % KSP == 0, "whole row tiles");
@@ -503,6 +503,9 @@ void prefill_kernel(PrefillParams p) {
 // Plans: 8 = 8 waves x 32 rows, 4 = 4 waves x 32 rows, 2 = 4 waves over 2 row tiles x 2 key halves (64 rows).
 constexpr int kCUs = 256;
 int prefill_plan(int n_q, int n_head, int n_kv, int head_dim, int forced) {
+    // head dim 256: 4 waves of 32 rows, one workgroup per CU (the K/V double buffer takes 141 KB of LDS; 8 waves or
+    // the key-split plan would not fit the registers or the LDS)
+    if (head_dim == 256) return 4;
     if (forced == 2 || forced == 4 || forced == 8) return forced;
     const int64_t wg8 = (int64_t)((n_q + 255) / 256) * n_head, wg4 = (int64_t)((n_q + 127) / 128) * n_head;
     if (2 * wg4 <= kCUs && n_kv >= 8 * kBK) return 2;
@@ -627,7 +630,14 @@ hipError_t launch_prefill_batched(const PrefillParams & p, int head_dim, int n_b
     const bool pos = p.scale_log2 > 0.f;
     const int plan = prefill_plan(p.n_q, p.n_head * n_batch, p.n_kv, head_dim, p.plan);
     if (p.n_qtiles != (p.n_q + 32 * plan - 1) / (32 * plan)) return hipErrorInvalidValue;  // planned with other inputs
-    if (head_dim == 64) {
+    if (head_dim == 256) {  // plan 4 only (prefill_plan), f16 or rotated f32 query rows (no self-attention variants)
+        if (sa != 0 || plan != 4) return hipErrorInvalidValue;
+        const dim3 grid((uint32_t)p.n_qtiles * p.n_head, (uint32_t)n_batch), block(4 * kWave);
+        if (p.rope && pos) hipLaunchKernelGGL((prefill_kernel<256, true, 4, true, 1, 0>), grid, block, 0, stream, p);
+        else if (p.rope) hipLaunchKernelGGL((prefill_kernel<256, false, 4, true, 1, 0>), grid, block, 0, stream, p);
+        else if (pos) hipLaunchKernelGGL((prefill_kernel<256, true, 4, false, 1, 0>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((prefill_kernel<256, false, 4, false, 1, 0>), grid, block, 0, stream, p);
+    } else if (head_dim == 64) {
         if (pos) launch_prefill_t<64, true>(p, plan, n_batch, sa, stream);
         else launch_prefill_t<64, false>(p, plan, n_batch, sa, stream);
     } else {

@@ -68,8 +68,17 @@ hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_
     const int pairs = ((p.q_out ? p.n_head : 0) + p.n_head_kv) * head_dim / 2;
     // one pair per thread where the row has at most 1024 (each further pass of the loop is another dependent round trip)
     const int threads = std::min(1024, ((pairs + kWave - 1) / kWave) * kWave);
-    if (head_dim == 64) hipLaunchKernelGGL((rope_store_kernel<64>), dim3(p.n_rows), dim3(threads), 0, stream, p);
-    else hipLaunchKernelGGL((rope_store_kernel<128>), dim3(p.n_rows), dim3(threads), 0, stream, p);
+    const dim3 grid(p.n_rows), block(threads);
+    switch (head_dim) {
+        case 4: hipLaunchKernelGGL((rope_store_kernel<4>), grid, block, 0, stream, p); break;
+        case 8: hipLaunchKernelGGL((rope_store_kernel<8>), grid, block, 0, stream, p); break;
+        case 16: hipLaunchKernelGGL((rope_store_kernel<16>), grid, block, 0, stream, p); break;
+        case 32: hipLaunchKernelGGL((rope_store_kernel<32>), grid, block, 0, stream, p); break;
+        case 64: hipLaunchKernelGGL((rope_store_kernel<64>), grid, block, 0, stream, p); break;
+        case 128: hipLaunchKernelGGL((rope_store_kernel<128>), grid, block, 0, stream, p); break;
+        case 256: hipLaunchKernelGGL((rope_store_kernel<256>), grid, block, 0, stream, p); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

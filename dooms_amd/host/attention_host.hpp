@@ -91,7 +91,7 @@ struct LlamaAttentionConfig {  // the attention fields of LlamaDecoderConfig (me
     int32_t n_ctx = 0;       // positions per layer cache
     int32_t n_head = 0;
     int32_t n_head_kv = 0;
-    int32_t head_dim = 0;    // 64 or 128
+    int32_t head_dim = 0;    // a power of two in [4, 256]
     float rope_base = 10000.f;  // rotary frequency base (rope.freq_base)
     bool rope_neox = false;     // rotary pairs (i, i + head_dim / 2) (qwen2) instead of (2i, 2i + 1) (llama)
     // Launch plans fixed for measuring, as the reference's prefill_tile (metal_llama_decoder.h:35-37); all 0: the
@@ -101,15 +101,16 @@ struct LlamaAttentionConfig {  // the attention fields of LlamaDecoderConfig (me
 
 class LlamaAttention {
 public:
-    //   InvalidArgument  bad sizes or null caches     Unsupported  head_dim not 64/128     ResourceExhausted  workspace
+    //   InvalidArgument  bad sizes or null caches     Unsupported  head_dim not a power of two in [4, 256]
+    //   ResourceExhausted  workspace
     static Status create(const LlamaAttentionConfig & c, uint16_t * k_cache, uint16_t * v_cache, hipStream_t stream,
                          std::unique_ptr<LlamaAttention> & out) {
         if (c.n_layer < 1 || c.n_ctx < 1 || c.n_head < 1 || c.n_head_kv < 1 || c.head_dim < 1)
             return {Code::InvalidArgument, "n_layer, n_ctx, n_head, n_head_kv and head_dim must be >= 1"};
         if (!k_cache || !v_cache) return {Code::InvalidArgument, "caches must not be null"};
         if (c.n_head % c.n_head_kv) return {Code::InvalidArgument, "n_head must be a multiple of n_head_kv"};
-        if (c.head_dim != 64 && c.head_dim != 128)
-            return {Code::Unsupported, "head_dim " + std::to_string(c.head_dim) + " is not supported (64 or 128)"};
+        if (c.head_dim < 4 || c.head_dim > 256 || (c.head_dim & (c.head_dim - 1)) != 0)  // metal_llama_decoder.mm:432-435
+            return {Code::Unsupported, "head_dim must be a power of two in [4, 256], got " + std::to_string(c.head_dim)};
         std::unique_ptr<LlamaAttention> a(new LlamaAttention(c, k_cache, v_cache, stream));
         // one workspace for the decode rows and for the prompt chunks of few rows that mx_attn_prefill_ws runs on the
         // split-KV kernel (up to 512, or with a long enough cache 1024, rows per kv head), at the full context

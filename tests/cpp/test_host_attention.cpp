@@ -97,9 +97,18 @@ bool close(const std::vector<uint16_t> & got, const std::vector<double> & ref, c
 
 }  // namespace
 
+// The reference's tiny llama (4 q / 2 kv heads, test_metal_llama_decoder.cpp:56-57) at its default head_dim 16 (the
+// per-query kernel) and at 64 (the flash kernel, as the reference's test also runs it): a 45-token prompt in chunks of
+// 20, then decode steps, two layers.
+static void prompt_in_chunks_then_decode_steps(int hd);
 TEST(llama_prompt_in_chunks_then_decode_steps) {
+    prompt_in_chunks_then_decode_steps(16);
+    prompt_in_chunks_then_decode_steps(64);
+}
+
+static void prompt_in_chunks_then_decode_steps(int hd) {
     using namespace dooms_amd;
-    const int n_layer = 2, n_ctx = 96, nh = 4, nkv = 2, hd = 64, qw = nh * hd, kw = nkv * hd;
+    const int n_layer = 2, n_ctx = 96, nh = 4, nkv = 2, qw = nh * hd, kw = nkv * hd;
     Dev kc((size_t)n_layer * n_ctx * kw), vc((size_t)n_layer * n_ctx * kw);
     std::unique_ptr<LlamaAttention> attn;
     Status st = LlamaAttention::create({n_layer, n_ctx, nh, nkv, hd}, kc.p, vc.p, nullptr, attn);

@@ -85,6 +85,12 @@ def decode(d, lens=(100,), kp=None, vp=None, q=A, out=A, lse=0, ws=A, ws_bytes=1
     (dict(head_dim=0), _lib.INVALID_ARGUMENT, "head_dim"),
     (dict(head_dim=80, q_stride=2560, kv_stride=640, out_stride=2560), _lib.UNSUPPORTED, "not supported"),
     (dict(head_dim=96, q_stride=3072, kv_stride=768, out_stride=3072), _lib.UNSUPPORTED, "not supported"),
+    (dict(head_dim=2, q_stride=64, kv_stride=16, out_stride=64), _lib.UNSUPPORTED, "power of two"),
+    (dict(head_dim=512, q_stride=16384, kv_stride=4096, out_stride=16384), _lib.UNSUPPORTED, "power of two"),
+    (dict(head_dim=4, n_head_kv=1, n_head=4, q_stride=16, kv_stride=6, out_stride=16), _lib.INVALID_ARGUMENT,
+     "multiples of 4"),
+    (dict(head_dim=16, n_head=4, n_head_kv=2, q_stride=68, kv_stride=32, out_stride=64), _lib.INVALID_ARGUMENT,
+     "multiples of 8"),
     (dict(n_q=-1), _lib.INVALID_ARGUMENT, "n_q"),
     (dict(causal=2), _lib.INVALID_ARGUMENT, "causal"),
     (dict(scale=float("nan")), _lib.INVALID_ARGUMENT, "scale"),
