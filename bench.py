@@ -46,7 +46,50 @@ def parse():
     ap.add_argument("--only", choices=["decode", "prefill", "all", "decode-headline", "prefill-headline", "linear",
                                        "self-attention"], default="all",
                     help="*-headline: only the headline workload of that path (for profiling one kernel)")
+    ap.add_argument("--summarize", metavar="CSV",
+                    help="no GPU work: summarize a rocprofv3 kernel_trace.csv (durations) or counter_collection.csv "
+                         "(counters) over the last --last dispatches of the kernels whose names contain --kernel")
+    ap.add_argument("--kernel", default="decode_kernel")
+    ap.add_argument("--last", type=int, default=0, help="dispatches at the end of the trace to summarize (0: all)")
     return ap.parse_args()
+
+
+def summarize(path, kernel, last):
+    """The timed region of a profiled bench.py run is its last dispatches (graph replays after the warmup), so a
+    summary over the last `last` dispatches of `kernel` reconciles with the ms_per_step the same run printed.
+    Prints a text summary: durations (kernel trace) or per-dispatch counter averages (counter collection), and for
+    counters also what the same counters read for the run's 1 GiB copy kernel (the scale of FETCH_SIZE/WRITE_SIZE)."""
+    import csv
+    from collections import OrderedDict
+    with open(path, newline="") as f:
+        rows = list(csv.DictReader(f))
+    if "Counter_Name" in rows[0]:
+        disp = OrderedDict()
+        for r in rows:
+            disp.setdefault((r["Dispatch_Id"], r["Kernel_Name"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+        sel = [(k, v) for k, v in disp.items() if kernel in k[1]]
+        sel = sel[-last:] if last else sel
+        copies = [v for k, v in disp.items() if "copyBuffer" in k[1]]
+        print(f"kernel: {sel[0][0][1][:120]}")
+        print(f"dispatches summarized: {len(sel)} (the last {last or 'all'} of {sum(kernel in k[1] for k in disp)})")
+        for c in sel[0][1]:
+            vals = [v[c] for _, v in sel]
+            print(f"  {c}: avg {sum(vals) / len(vals):.2f}  min {min(vals):.2f}  max {max(vals):.2f}")
+        if copies:
+            for c in copies[-1]:
+                print(f"  copyBuffer (1 GiB copy of the same run) {c}: {copies[-1][c]:.2f}")
+        return 0
+    sel = [r for r in rows if kernel in r["Kernel_Name"]]
+    n_all = len(sel)
+    sel = sel[-last:] if last else sel
+    dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in sel]  # us
+    span = (int(sel[-1]["End_Timestamp"]) - int(sel[0]["Start_Timestamp"])) / 1e3
+    names = sorted({r["Kernel_Name"][:120] for r in sel})
+    print(f"kernel: {'; '.join(names)}")
+    print(f"dispatches summarized: {len(sel)} (the last {last or 'all'} of {n_all})")
+    print(f"duration us: avg {sum(dur) / len(dur):.3f}  min {min(dur):.3f}  max {max(dur):.3f}  sum {sum(dur):.1f}")
+    print(f"first start to last end: {span:.1f} us")
+    return 0
 
 
 def time_graph(torch, step, steps, warmup):
@@ -353,6 +396,8 @@ def cpu_prefill_baseline(torch, prob, budget_s, threads):
 
 def main():
     args = parse()
+    if args.summarize:
+        return summarize(args.summarize, args.kernel, args.last)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention hot path has no multi-GPU path here "
                                    "(run with --gpus 1)", "n_gpus": args.gpus}))
@@ -488,7 +533,7 @@ def main():
     if args.only in ("prefill", "all", "prefill-headline"):
         # ---- cfg5 Qwen2.5-7B 32k causal prefill in 2048-query chunks ----
         pp = PrefillProblem(torch, gen, 28, 4, 128, 32768, 2048, sigma=0.5)
-        ms_p, _ = time_graph(torch, pp.step, max(3, K // 4), max(1, W // 2))
+        ms_p, _ = time_graph(torch, pp.step, K, W)
         fl = pp.flops_per_layer()
         tflops = fl / (ms_p * 1e-3) / 1e12
         avg_us = ms_p * 1e3 / len(pp.chunks)

@@ -64,7 +64,7 @@ def test_small_lengths_gqa7(device, L):
 
 # cfg3: Llama-3-8B decode, batch 1 at 8192 (north-star shape), and batches 4/16 with lengths U[1024, 8192]
 def test_llama3_8b_decode_8192(device):
-    run_decode(device, 3, 32, 8, 128, [8192], check_heads=[0, 1, 2, 3, 13, 30, 31])
+    run_decode(device, 3, 32, 8, 128, [8192])  # every head
 
 
 def test_llama3_8b_decode_128k(device):
@@ -74,9 +74,10 @@ def test_llama3_8b_decode_128k(device):
 
 @pytest.mark.parametrize("batch", [4, 16])
 def test_llama3_8b_decode_batched(device, batch):
+    # every head of every sequence against the oracle (a per-split or per-XCD indexing slip cannot hide in an
+    # unchecked head)
     lens = list(np.random.default_rng(300 + batch).integers(1024, 8193, size=batch))
-    check = range(batch) if batch <= 4 else [0, 5, 15]
-    run_decode(device, 30 + batch, 32, 8, 128, lens, check_seqs=check, check_heads=[0, 3, 4, 17, 31])
+    run_decode(device, 30 + batch, 32, 8, 128, lens)
 
 
 def test_batch_over_launch_limit(device):

@@ -5,12 +5,15 @@ Reference: attention_prefill<64|128> (llama_kernels.h:632-769) as dispatched by 
 Reference tests mirrored: flash prefill on a 45-token prompt in chunks of 20 (test_metal_llama_decoder.cpp:497-532),
 chunk-size invariance, non-causal MHA (test_backend_ggml.cpp:677-745).
 """
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import pytest
 import torch
 
 from dooms_amd import attention as A
 from helpers import assert_close, normal_f16, ref_attention
+from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
@@ -114,12 +117,17 @@ def test_qwen7b_32k_chunked_equals_one_shot(device):
     torch.cuda.synchronize()
     assert torch.equal(one, out)
     assert torch.equal(lse1, lse)
-    rows = [0, 5, 2047, 16384, 30000, 32767]
-    heads = [0, 7, 27]
-    ro, rl = ref_attention(q, k, v, nh, nkv, hd, 1.0 / np.sqrt(hd), rows=rows, heads=heads)
+    # every head of rows in every chunk: the chunk's first and last rows, a 256-row workgroup tile's first and last,
+    # and one more, against the f64 oracle (all heads of a row in one oracle call)
+    rows = sorted({r for p0 in range(0, N, 2048) for r in (p0, p0 + 255, p0 + 256, p0 + 2047)})
     got = out.cpu().numpy().astype(np.float64)
-    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
-    assert_close(got[rows][:, cols], ro, hd, "32k", lse.cpu().numpy()[rows][:, heads], rl)
+    gl = lse.cpu().numpy()
+    oracle_row = lambda t: O.attention_f64(q[t:t + 1], k[:t + 1], v[:t + 1], nh, nkv, hd, 1.0 / np.sqrt(hd), p0=t,
+                                           causal=True)
+    with ThreadPoolExecutor(max_workers=8) as ex:  # the C oracle runs outside the GIL
+        refs = list(ex.map(oracle_row, rows))
+    for t, (ro, rl) in zip(rows, refs):
+        assert_close(got[t:t + 1], ro, hd, f"32k row {t}", gl[t:t + 1], rl)
 
 
 def test_one_row_per_key_closed_form(device):
