@@ -251,6 +251,7 @@ public:
         if (c.cross_splits < 0 || c.cross_splits > 32) return {Code::InvalidArgument, "cross_splits must be in [0, 32]"};
         if (c.n_state % c.n_head) return {Code::InvalidArgument, "n_state must be a multiple of n_head"};
         const int32_t hd = c.n_state / c.n_head;
+        // the reference's Whisper decoder takes 64 or 128 (metal_whisper_decoder.mm:342-343)
         if (hd != 64 && hd != 128) return {Code::Unsupported, "head_dim " + std::to_string(hd) + " is not supported (64 or 128)"};
         if (!self_k || !self_v || !cross_k || !cross_v) return {Code::InvalidArgument, "caches must not be null"};
         std::unique_ptr<WhisperAttention> a(new WhisperAttention(c, self_k, self_v, cross_k, cross_v, stream));

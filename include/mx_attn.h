@@ -54,7 +54,7 @@ extern "C" {
 /* Return codes: the numbering of dooms_code (include/dooms/dooms_c.h:24-33). */
 #define MX_ATTN_OK 0
 #define MX_ATTN_INVALID_ARGUMENT 1    /* null pointer, bad stride, n_head % n_head_kv != 0, kv_len < n_q, ... */
-#define MX_ATTN_UNSUPPORTED 4         /* head_dim not in {64, 128}, or a GQA group / batch this build does not run */
+#define MX_ATTN_UNSUPPORTED 4         /* head_dim not a power of two in [4, 256], or a shape one launch cannot hold */
 #define MX_ATTN_RESOURCE_EXHAUSTED 5  /* the workspace is smaller than mx_attn_decode_workspace_bytes asks for */
 #define MX_ATTN_INTERNAL 7            /* the HIP runtime reported an error (launch failure, ...) */
 
@@ -83,7 +83,7 @@ typedef struct mx_attn_tuning {
 typedef struct mx_attn_desc {
     int32_t n_head;      /* query heads */
     int32_t n_head_kv;   /* key/value heads; n_head % n_head_kv == 0 */
-    int32_t head_dim;    /* 64 or 128 */
+    int32_t head_dim;    /* a power of two in [4, 256] (metal_llama_decoder.mm:432-435) */
     int32_t n_q;         /* query rows (per sequence for mx_attn_decode) */
     int32_t p0;          /* mx_attn_prefill: cache position of query row 0 (the chunk offset); decode: ignored */
     int32_t n_kv;        /* mx_attn_prefill: keys in the cache (0 means p0 + n_q); decode: ignored (kv_len[]) */
