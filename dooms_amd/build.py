@@ -70,3 +70,31 @@ def build_host_test() -> str:
 
 if __name__ == "__main__":
     print(build(verbose=True))
+
+
+SAN_DIR = os.path.join(ROOT, "tests", "cpp", "_san")
+
+
+def build_sanitized_abi_check() -> str:
+    """The library's host code with AddressSanitizer and UndefinedBehaviorSanitizer (device code unchanged), linked
+    into tests/cpp/abi_checks_sanitized.cpp's driver of every entry point's argument checks; returns the binary."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(SAN_DIR, exist_ok=True)
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-Xarch_host",
+           "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=all"]
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    compile_flags = [f for f in FLAGS if f not in ("-shared", "-fvisibility=hidden")]
+    objs = [os.path.join(SAN_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    jobs = [[HIPCC, *compile_flags, *san, *inc, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    driver = os.path.join(ROOT, "tests", "cpp", "abi_checks_sanitized.cpp")
+    dobj = os.path.join(SAN_DIR, "driver.o")
+    jobs.append([HIPCC, "-std=c++17", "-O1", "-g", *san, *inc, "-c", driver, "-o", dobj])
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        results = list(ex.map(_run, jobs))
+    if any(rc != 0 for rc, _ in results):
+        raise RuntimeError("hipcc failed:\n" + "\n".join(m for _, m in results))
+    exe = os.path.join(SAN_DIR, "abi_checks_sanitized")
+    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-fsanitize=address,undefined", *objs, dobj, "-ldl", "-o", exe])
+    if rc != 0:
+        raise RuntimeError(f"link failed ({rc}):\n{msg}")
+    return exe

@@ -354,3 +354,19 @@ def test_linear_plan_checks():
     assert L.mx_linear_plan_create(ctypes.byref(ld(reserved=1)), ctypes.byref(h)) == _lib.INVALID_ARGUMENT
     assert L.mx_linear_plan_run(None, A, A, A, None, None, A, 1 << 20, None) == _lib.INVALID_ARGUMENT
     L.mx_linear_plan_destroy(None)  # allowed
+
+
+def test_host_code_under_address_and_undefined_behaviour_sanitizers():
+    """The library's host code (every .hip source's host side, device code unchanged) built with -fsanitize=address,
+    undefined and driven through every entry point's argument checks and the workspace-size arithmetic over many
+    shapes (tests/cpp/abi_checks_sanitized.cpp). No GPU needed: every call is refused before anything is enqueued."""
+    from dooms_amd import build as B
+    exe = os.path.join(B.SAN_DIR, "abi_checks_sanitized")
+    srcs = [os.path.join(B.CSRC, s) for s in os.listdir(B.CSRC)] + glob.glob(os.path.join(ROOT, "include", "*.h")) + \
+        [os.path.join(ROOT, "tests", "cpp", "abi_checks_sanitized.cpp")]
+    if not os.path.exists(exe) or os.path.getmtime(exe) < max(os.path.getmtime(s) for s in srcs):
+        exe = B.build_sanitized_abi_check()
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300,
+                       env={**os.environ, "ASAN_OPTIONS": "detect_leaks=0"})  # the HIP runtime's own allocations
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "abi_checks_sanitized: ok" in r.stdout

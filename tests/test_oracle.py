@@ -360,3 +360,13 @@ def test_self_attention_oracle_closed_forms():
     np.testing.assert_allclose(one[:, 0], qkv[:, 0, 2 * E:], atol=1e-14)
     np.testing.assert_allclose(O.self_attention_f64(qkv[::-1], H, 0.3), O.self_attention_f64(qkv, H, 0.3)[::-1],
                                atol=1e-14)
+
+
+def test_oracle_under_address_and_undefined_behaviour_sanitizers():
+    # every oracle function on small cases with exactly sized buffers, built with -fsanitize=address,undefined
+    # (oracle/sanitize_check.c); any out-of-bounds access, leak or undefined arithmetic fails the run
+    import subprocess
+    r = subprocess.run(["make", "-s", "-C", os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle"), "sanitize"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "sanitize_check: ok" in r.stdout
