@@ -396,7 +396,6 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         }
         p.chunk = (int32_t)std::min<int64_t>(chunk, INT32_MAX / 2);
         p.max_split = 1;
-        p.n_groups = n_seq * d.n_head_kv;
         for (int i = 0; i < n_seq; i++) {
             const int32_t n = kv_len[b0 + i];
             p.seq[i].k = static_cast<const mx::half_t *>(k_caches[b0 + i]);

@@ -91,29 +91,41 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     __shared__ int s_last;
     __shared__ float2 s_cs[F32 ? HD / 2 : 1];  // fused step: (cos, sin) of each rotary pair's angle
 
+    // Every argument the start of the kernel needs is fetched in one batch of scalar loads: pinned into registers here,
+    // before the first branch. Otherwise the compiler issues each load after the branch before its first use, and the
+    // kernel waits for up to four dependent round trips to the argument memory before its first K/V load. The sequence
+    // is blockIdx.y, so its descriptor's address is known at once.
+    const int bl = blockIdx.y;
+    const half_t * seq_k = p.seq[bl].k;
+    const half_t * seq_v = p.seq[bl].v;
+    int32_t L = p.seq[bl].len, n_split = p.seq[bl].n_split;
+    uint32_t T = p.n_rowtiles;
+    int32_t max_split = p.max_split, n_head_kv = p.n_head_kv, chunk = p.chunk, G = p.group, seq0 = p.seq0, n_q = p.n_q;
+    int32_t rows = p.rows, causal = p.causal;
+    int64_t q_stride = p.q_stride, kv_stride = p.kv_stride;
+    const half_t * qp = p.q;
+    asm volatile("" : "+s"(seq_k), "+s"(seq_v), "+s"(L), "+s"(n_split), "+s"(T), "+s"(max_split), "+s"(n_head_kv),
+                 "+s"(chunk), "+s"(G), "+s"(seq0), "+s"(n_q), "+s"(rows), "+s"(causal), "+s"(q_stride),
+                 "+s"(kv_stride), "+s"(qp));
+
     // Work item. The row tiles of one (sequence, kv head, split) read the same keys and values, so they run as
     // consecutive workgroups of one XCD (workgroups are dealt to the 8 XCDs round-robin: ids 8 apart share one), where
     // all but the first read hit that XCD's L2. With one row tile this is the identity.
-    const uint32_t T = p.n_rowtiles, id = blockIdx.x, k8 = id / 8;
-    const uint32_t grp = (k8 / T) * 8 + id % 8;  // (split, sequence, kv head) group
+    const uint32_t id = blockIdx.x, k8 = id / 8;
+    const uint32_t grp = (k8 / T) * 8 + id % 8;  // (split, kv head) group of the sequence
     const int rt = k8 % T;
-    const int s = grp % p.max_split;
-    const int y = grp / p.max_split;
-    if (y >= p.n_groups) return;  // padding of the grid to whole XCD rounds
-    const int g = y % p.n_head_kv;
-    const int bl = y / p.n_head_kv;
-    const DecodeSeq sq = p.seq[bl];
-    if (s >= sq.n_split) return;  // uniform over the workgroup, before any barrier
+    const int s = grp % max_split;
+    const int g = grp / max_split;
+    if (g >= n_head_kv) return;  // padding of the grid to whole XCD rounds
+    if (s >= n_split) return;    // uniform over the workgroup, before any barrier
 
-    const int L = sq.len;
-    const int j0 = s * p.chunk;
-    const int j1 = min(j0 + p.chunk, L);
+    const int j0 = s * chunk;
+    const int j1 = min(j0 + chunk, L);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int G = p.group;
-    const int64_t seq_row0 = (int64_t)(p.seq0 + bl) * p.n_q;  // first query row of the sequence
+    const int64_t seq_row0 = (int64_t)(seq0 + bl) * n_q;  // first query row of the sequence
 
-    const half_t * kbase = sq.k + (int64_t)g * HD;
-    const half_t * vbase = sq.v + (int64_t)g * HD;
+    const half_t * kbase = seq_k + (int64_t)g * HD;
+    const half_t * vbase = seq_v + (int64_t)g * HD;
     const int srow = lane % 16, sgrp = lane / 16;          // score lanes: row srow, keys 4 sgrp .. + 4 of a 16-key tile
     const int vslot = lane / LPR, vcol = 8 * (lane % LPR); // value lanes: key slot, first head dim
 
@@ -121,22 +133,22 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
             const int key = min(jb + 16 * mt + srow, L - 1);
-            const half_t * kp = kbase + (int64_t)key * p.kv_stride + 8 * sgrp;
+            const half_t * kp = kbase + (int64_t)key * kv_stride + 8 * sgrp;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) blk.k[mt][ks] = load16(kp + 32 * ks);
         }
 #pragma unroll
         for (int i = 0; i < NLV; i++) {
             const int key = min(jb + KPL * i + vslot, L - 1);
-            blk.v[i] = load16(vbase + (int64_t)key * p.kv_stride + vcol);
+            blk.v[i] = load16(vbase + (int64_t)key * kv_stride + vcol);
         }
     };
 
     // ---- this lane's score row and its query operand ----
     const int rr = rt * RT + srow;  // row index inside the (sequence, kv head) problem: rr = t * G + gi
-    const bool srow_ok = srow < RT && rr < p.rows;
+    const bool srow_ok = srow < RT && rr < rows;
     const int st = rr / G, sh = g * G + rr % G;
-    const int lim = p.causal ? L - p.n_q + st : L - 1;  // last visible key of the row
+    const int lim = causal ? L - n_q + st : L - 1;  // last visible key of the row
     half8_t qb[KS];
     float xq[F32 ? KS : 1][8] = {};  // the f32 query (fused step: rotated once the first block's loads are out)
     if constexpr (F32) {
@@ -150,7 +162,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     // only after the first block's loads are out; a conditional load here would make the compiler drain it first
     u32x4 qv[F32 ? 1 : KS];
     if constexpr (!F32) {
-        const half_t * qrow = p.q + (seq_row0 + (srow_ok ? st : 0)) * p.q_stride + (int64_t)(srow_ok ? sh : g * G) * HD;
+        const half_t * qrow = qp + (seq_row0 + (srow_ok ? st : 0)) * q_stride + (int64_t)(srow_ok ? sh : g * G) * HD;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qv[ks] = load16(qrow + 32 * ks + 8 * sgrp);
     }
@@ -336,7 +348,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
     // ---- merge the NW waves; write the output (one split) or publish this split's partial ----
     // Each thread owns head-dim pairs (r, 2 dp .. + 2) of the tile's RT x HD outputs.
-    const bool single = sq.n_split == 1;
+    const bool single = n_split == 1;
     const int64_t tile = ((int64_t)bl * p.n_head_kv + g) * p.n_rowtiles + rt;  // (sequence, kv head, row tile)
     float * part_tile = p.part + tile * p.max_split * RT * (HD + 4);
     constexpr int64_t SS = (int64_t)RT * (HD + 4);  // floats between the partials of consecutive splits
@@ -376,7 +388,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t done = __hip_atomic_fetch_add(p.counters + tile * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = done == (uint32_t)(sq.n_split - 1);
+        s_last = done == (uint32_t)(n_split - 1);
     }
     __syncthreads();
     if (!s_last) return;
@@ -386,7 +398,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     // own: per chunk of kMergeChunk splits it issues every load first ((m, l) of its row and its pair, for all the
     // chunk's splits; the row's (m, l) loads of a wave coalesce), then folds them with a running maximum. One memory
     // round trip per chunk, no LDS, no barrier. ----
-    const int ns = sq.n_split;
+    const int ns = n_split;
     constexpr int PPT = (NP + kThreads - 1) / kThreads;  // output pairs per thread
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
@@ -432,9 +444,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
 template <int HD, int RT, int NW>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
-    // 1-D grid: groups of (split, sequence, kv head), 8 per round of XCDs, each group's row tiles on one XCD
-    const int64_t groups = (int64_t)p.max_split * n_seq * p.n_head_kv;
-    const dim3 grid((uint32_t)(((groups + 7) / 8) * 8 * p.n_rowtiles));
+    // x: groups of (split, kv head), 8 per round of XCDs, each group's row tiles on one XCD; y: the sequence
+    const int64_t groups = (int64_t)p.max_split * p.n_head_kv;
+    const dim3 grid((uint32_t)(((groups + 7) / 8) * 8 * p.n_rowtiles), (uint32_t)n_seq);
     if (p.f32)
         hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW>), grid, dim3(NW * kWave), 0, stream, p);
     else

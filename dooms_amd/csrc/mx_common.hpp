@@ -48,7 +48,10 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
 __device__ __forceinline__ half8_t as_half8(u32x4 v) { return __builtin_bit_cast(half8_t, v); }
 
 // 16-byte global load through the vector memory path.
-__device__ __forceinline__ u32x4 load16(const void * p) { return *reinterpret_cast<const u32x4 *>(p); }
+// 16-byte load from global memory. The address space is explicit so that a pointer the compiler cannot trace back to a
+// kernel argument (one pinned into registers by an asm statement) still gives a global load, not a flat one, which
+// also counts against the LDS/scalar wait counter and so turns the waits for LDS into waits for memory.
+__device__ __forceinline__ u32x4 load16(const void * p) { return *(const __attribute__((address_space(1))) u32x4 *)(p); }
 
 // Maps a workgroup index to a work index so that each XCD (the chip has 8, and consecutive workgroups are dealt out to
 // them round-robin) runs a contiguous range of the work order: neighbours in that order share keys/values in one L2.

@@ -39,7 +39,6 @@ struct DecodeParams {
     int32_t n_rowtiles;  // ceil(rows / RT)
     int32_t chunk;       // keys per split
     int32_t max_split;   // max over the launch's sequences of n_split
-    int32_t n_groups;    // n_seq * n_head_kv: (sequence, key/value head) pairs of the launch
     int32_t seq0;        // index of the launch's first sequence in the caller's batch (query/output rows)
     float scale_log2;    // scale * log2(e): scores are kept in base-2 units
     int32_t f32;         // 1: f32 query rows in qkv (q_stride floats apart) and f32 output in out32
