@@ -191,7 +191,10 @@ class DecodeProblem:
 
 
 class PrefillProblem:
-    def __init__(self, torch, gen, n_head, n_kv, hd, N, chunk, layers=1, sigma=1.0):
+    """Causal prompt chunks of `chunk` rows against the growing cache. workspace=True runs mx_attn_prefill_ws, the entry
+    point the decoder's prompt path calls (the stream-K split over the CUs where planned); False mx_attn_prefill."""
+
+    def __init__(self, torch, gen, n_head, n_kv, hd, N, chunk, layers=1, sigma=1.0, workspace=True, tuning=None):
         from dooms_amd import _lib
         self.torch, self._lib = torch, _lib
         self.n_head, self.n_kv, self.hd, self.N, self.chunk, self.layers = n_head, n_kv, hd, N, chunk, layers
@@ -202,16 +205,26 @@ class PrefillProblem:
         self.out = torch.empty(N, n_head * hd, dtype=torch.float16, device=dev)
         self.chunks = [(p0, min(chunk, N - p0)) for p0 in range(0, N, chunk)]
         self.descs = [_lib.make_desc(n_head, n_kv, hd, M, n_head * hd, n_kv * hd, n_head * hd, 1.0 / math.sqrt(hd),
-                                     p0=p0, causal=1) for p0, M in self.chunks]
+                                     p0=p0, causal=1, tuning=tuning) for p0, M in self.chunks]
         rs = n_head * hd * 2
         self.qoff = [p0 * rs for p0, _ in self.chunks]
+        self.ws = None
+        if workspace:
+            nb = max(_lib.prefill_workspace_bytes(d) for d in self.descs)
+            self.ws = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
+            _lib.check(_lib.decode_workspace_init(self.ws.data_ptr(), self.ws.numel(),
+                                                  torch.cuda.current_stream().cuda_stream))
 
     def launch(self, layer, ci):
         _lib = self._lib
         p0, _ = self.chunks[ci]
-        _lib.check(_lib.prefill_raw(self.descs[ci], self.q[layer].data_ptr() + self.qoff[ci], self.k[layer].data_ptr(),
-                                    self.v[layer].data_ptr(), self.out.data_ptr() + self.qoff[ci], 0,
-                                    self.torch.cuda.current_stream().cuda_stream))
+        st = self.torch.cuda.current_stream().cuda_stream
+        q, o = self.q[layer].data_ptr() + self.qoff[ci], self.out.data_ptr() + self.qoff[ci]
+        if self.ws is None:
+            _lib.check(_lib.prefill_raw(self.descs[ci], q, self.k[layer].data_ptr(), self.v[layer].data_ptr(), o, 0, st))
+        else:
+            _lib.check(_lib.prefill_ws_raw(self.descs[ci], q, self.k[layer].data_ptr(), self.v[layer].data_ptr(), o, 0,
+                                           self.ws.data_ptr(), self.ws.numel(), st))
 
     def step(self):
         for l in range(self.layers):

@@ -35,7 +35,8 @@ ROPE_NONE = 2    # no rotation: Whisper
 class MxAttnTuning(ctypes.Structure):
     """mx_attn_tuning (include/mx_attn.h): 0 in a field keeps the library's plan."""
     _fields_ = [("decode_splits", ctypes.c_int32), ("decode_waves", ctypes.c_int32),
-                ("decode_max_workgroups", ctypes.c_int32), ("prefill_plan", ctypes.c_int32)]
+                ("decode_max_workgroups", ctypes.c_int32), ("prefill_plan", ctypes.c_int32),
+                ("prefill_stream", ctypes.c_int32)]
 
 
 class MxAttnDesc(ctypes.Structure):

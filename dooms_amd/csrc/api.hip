@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
+#include <queue>
 #include <string>
 
 #include "mx_kernels.hpp"
@@ -45,6 +46,8 @@ int32_t check_tuning(const mx_attn_tuning * t) {
         return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_max_workgroups (%d) must be >= 0", t->decode_max_workgroups);
     if (t->prefill_plan != 0 && t->prefill_plan != 2 && t->prefill_plan != 4 && t->prefill_plan != 8)
         return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->prefill_plan (%d) must be 0 (planned), 2, 4 or 8", t->prefill_plan);
+    if (t->prefill_stream < -1 || t->prefill_stream > 1)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->prefill_stream (%d) must be -1, 0 (planned) or 1", t->prefill_stream);
     return MX_ATTN_OK;
 }
 
@@ -215,8 +218,66 @@ mx::SmallAttnParams small_params(const mx_attn_desc & d, const void * q, void * 
     return sp;
 }
 
+// Stream-K plan of a flash prefill: ranges (0: the one-tile-per-workgroup grid) and the launch's (tile, key block) units.
+struct SkPlan {
+    int32_t ranges = 0;
+    int64_t total = 0;
+};
+constexpr int32_t kSkRanges = 256;  // one range per CU
+constexpr int64_t kSkMaxTiles = (int64_t)kCounterRegion / 4;
+// At least this many blocks per range (below, the merge and the lost prefetch at the segment edges cost more).
+constexpr int64_t kSkMinBlocksPerRange = 8;
+
+size_t prefill_sk_ws_bytes(int head_dim) {
+    const int64_t slot = head_dim == 64 ? mx::kPrefillSlotFloats<64> : mx::kPrefillSlotFloats<128>;
+    return kCounterRegion + (size_t)(2 * kSkRanges) * (size_t)slot * sizeof(float);
+}
+
+// When stream-K is planned (tuning->prefill_stream 0; 1 forces it wherever it applies, -1 never):
+//   * head dim 64 only. The head-dim-128 kernel runs the chip at its power limit, so CUs the grid leaves idle let the
+//     busy ones clock higher: a 2048-row chunk of 28 heads (224 tiles for 256 CUs) ran 920 TFLOP/s on the grid and 913
+//     split, 224 non-causal tiles 876 against 860. At head dim 64 a 4096-token Qwen2.5-0.5B prompt (224 tiles) went
+//     81.9 -> 71.0 us.
+//   * fewer than 4 tiles per CU, and the grid's time at least 8 % over the split's. The grid deals its tiles heaviest
+//     first and hands the next to the CU that frees first (its time is simulated so), which already balances a causal
+//     prompt of many tiles: a 4096-token Llama-3-8B prompt (512 tiles) ran 167 us on the grid, 217 split.
+SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
+    SkPlan k;
+    const int forced = d.tuning ? d.tuning->prefill_stream : 0;
+    if (forced < 0 || plan != 8 || (d.head_dim != 64 && d.head_dim != 128)) return k;
+    if (forced == 0 && d.head_dim != 64) return k;
+    const int32_t n_qtiles = (d.n_q + mx::kPrefillSkRows - 1) / mx::kPrefillSkRows;
+    const int64_t n_tiles = (int64_t)n_qtiles * d.n_head;
+    if (n_tiles > kSkMaxTiles || (forced == 0 && n_tiles >= 4 * kSkRanges)) return k;
+    int64_t total = 0;
+    for (int32_t qt = 0; qt < n_qtiles; qt++)
+        total += (int64_t)d.n_head * mx::prefill_tile_blocks(qt, d.n_q, d.p0, (int32_t)n_kv, d.causal);
+    if (total < kSkMinBlocksPerRange * kSkRanges) return k;
+    if (forced == 0) {
+        // the grid: tiles heaviest first (causal: by query tile descending), each to the CU that frees first
+        std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> cu;
+        for (int32_t i = 0; i < kSkRanges; i++) cu.push(0);
+        int64_t grid_time = 0;
+        for (int32_t i = 0; i < n_qtiles; i++) {
+            const int32_t qt = d.causal ? n_qtiles - 1 - i : i;
+            const int64_t nb = mx::prefill_tile_blocks(qt, d.n_q, d.p0, (int32_t)n_kv, d.causal);
+            for (int32_t h = 0; h < d.n_head; h++) {
+                const int64_t t = cu.top() + nb;
+                cu.pop();
+                cu.push(t);
+                grid_time = std::max(grid_time, t);
+            }
+        }
+        if ((double)total / kSkRanges > 0.92 * (double)grid_time) return k;
+    }
+    k.ranges = kSkRanges;
+    k.total = total;
+    return k;
+}
+
 int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_cache, const void * v_cache, void * out,
-                     float * lse, mx_attn_stream stream, const mx_attn_rope * rope) {
+                     float * lse, mx_attn_stream stream, const mx_attn_rope * rope, void * ws = nullptr,
+                     size_t ws_bytes = 0) {
     const mx_attn_desc & d = *desc;
     if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
     if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
@@ -269,6 +330,19 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.q_batch = p.kv_batch = p.out_batch = p.lse_batch = 0;
     p.hdv = p.head_stride = d.head_dim;
     fill_freq(p.rope_freq, rope, d.head_dim);
+    p.sk_ranges = 0;
+    p.sk_total = 0;
+    p.sk_part = nullptr;
+    p.sk_counters = nullptr;
+    if (ws && !(reinterpret_cast<uintptr_t>(ws) & 255u)) {  // stream-K when planned and the workspace holds its slots
+        const SkPlan k = prefill_sk_plan(d, n_kv, rows / 32);
+        if (k.ranges > 0 && ws_bytes >= prefill_sk_ws_bytes(d.head_dim)) {
+            p.sk_ranges = k.ranges;
+            p.sk_total = k.total;
+            p.sk_counters = static_cast<uint32_t *>(ws);
+            p.sk_part = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegion);
+        }
+    }
     if (rope)  // the chunk's keys and values go into the caches first (stream order)
         if (int32_t rc = rope_store_rows(d, rope, static_cast<const float *>(q), d.n_q, d.p0, const_cast<void *>(k_cache),
                                          const_cast<void *>(v_cache), nullptr, st))
@@ -685,7 +759,15 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
 
 MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc) {
     if (check_desc(desc)) return 0;
-    if (!prefill_split_route(*desc)) return 0;
+    if (!prefill_split_route(*desc)) {  // the flash kernel: the stream-K slots when that plan is taken
+        const mx_attn_desc & d = *desc;
+        if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim || d.p0 < 0 || d.n_kv < 0) return 0;
+        const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
+        if (n_kv > INT32_MAX) return 0;
+        const int plan =
+            mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim, d.tuning ? d.tuning->prefill_plan : 0) / 32;
+        return prefill_sk_plan(d, n_kv, plan).ranges > 0 ? prefill_sk_ws_bytes(d.head_dim) : 0;
+    }
     const int64_t L = prefill_split_keys(*desc);
     if (L < 1 || L > INT32_MAX) return 0;
     return prefill_split_q_offset(*desc, (int32_t)L) + (size_t)desc->n_q * desc->n_head * desc->head_dim * sizeof(float);
@@ -696,7 +778,8 @@ MX_ATTN_API int32_t mx_attn_prefill_ws(const mx_attn_desc * desc, const uint16_t
                                        size_t ws_bytes, mx_attn_stream stream) {
     if (int32_t rc = check_desc(desc)) return rc;
     const mx_attn_desc & d = *desc;
-    if (!workspace || !prefill_split_route(d)) return prefill_impl(desc, q, k_cache, v_cache, out, lse, stream, nullptr);
+    if (!workspace || !prefill_split_route(d))
+        return prefill_impl(desc, q, k_cache, v_cache, out, lse, stream, nullptr, workspace, ws_bytes);
     if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
     if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
     if (d.n_q == 0) return MX_ATTN_OK;
@@ -723,7 +806,8 @@ MX_ATTN_API int32_t mx_attn_prefill_rope_ws(const mx_attn_desc * desc, const mx_
     if (int32_t rc = check_desc(desc)) return rc;
     if (int32_t rc = check_rope(*desc, rope)) return rc;
     const mx_attn_desc & d = *desc;
-    if (!workspace || !prefill_split_route(d)) return prefill_impl(desc, qkv, k_cache, v_cache, out, lse, stream, rope);
+    if (!workspace || !prefill_split_route(d))
+        return prefill_impl(desc, qkv, k_cache, v_cache, out, lse, stream, rope, workspace, ws_bytes);
     if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
     if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
     if (d.n_q == 0) return MX_ATTN_OK;

@@ -92,8 +92,68 @@ struct PrefillParams {
     // (<= the kernel's, a multiple of 8; columns past it are zeros) and the elements between consecutive heads
     int32_t hdv, head_stride;
     int32_t plan;  // workgroup plan fixed by the caller (8, 4 or 2), or 0: prefill_plan's choice
+    // Stream-K launch (plan 8, one problem; sk_ranges 0 otherwise): sk_ranges workgroups each take an equal range of
+    // the launch's sk_total (query tile, 64-key block) units; a tile split between ranges is merged through sk_part
+    // (2 slots of kPrefillSlotFloats<HD> per range) and sk_counters (one uint32 per tile, zero between calls).
+    int32_t sk_ranges;
+    int64_t sk_total;
+    float * sk_part;
+    uint32_t * sk_counters;
     float rope_freq[kMaxHeadDim / 2];
 };
+
+// ---- Stream-K partition of an 8-wave prefill launch (host and device) ----
+// Tiles are the launch's (kv head, query tile of 256 rows, head of the group) triples in that order, each with
+// prefill_tile_blocks 64-key blocks; the blocks of all tiles in that order form the units 0 .. total - 1, and range r
+// is the units [lo(r), lo(r + 1)).
+constexpr int kPrefillSkRows = 256;  // query rows per tile (8 waves x 32)
+constexpr int kPrefillSkKeys = 64;   // keys per block
+// floats of one partial slot: per lane of the 8 waves its O values (head_dim / 2 of them), m and l
+template <int HD>
+constexpr int64_t kPrefillSlotFloats = 8 * (int64_t)(HD / 2 + 2) * 64;
+
+__host__ __device__ inline int32_t prefill_tile_blocks(int32_t qt, int32_t n_q, int32_t p0, int32_t n_kv, int32_t causal) {
+    const int32_t last_row = (qt + 1) * kPrefillSkRows < n_q ? (qt + 1) * kPrefillSkRows : n_q;  // one past the tile's last row
+    const int64_t kend = causal ? ((int64_t)p0 + last_row < n_kv ? (int64_t)p0 + last_row : n_kv) : n_kv;
+    return (int32_t)((kend + kPrefillSkKeys - 1) / kPrefillSkKeys);
+}
+__host__ __device__ inline int64_t sk_lo(int64_t total, int32_t ranges, int32_t r) { return (int64_t)r * total / ranges; }
+// the range that holds unit x (ranges are never empty: total >= ranges)
+__host__ __device__ inline int32_t sk_range_of(int64_t total, int32_t ranges, int64_t x) {
+    const int64_t r = ((x + 1) * ranges - 1) / total;
+    return (int32_t)(r < ranges - 1 ? r : ranges - 1);
+}
+struct SkTile {
+    int32_t kvh, qt, gi, nblk;  // kv head, query tile, head within the group, blocks of the tile
+    int64_t start;               // its first unit
+};
+// The tile that holds unit x; per_kv = group * sum over query tiles of their blocks (the units of one kv head).
+__host__ __device__ inline SkTile sk_locate(int64_t x, int64_t per_kv, int32_t group, int32_t n_qtiles, int32_t n_q,
+                                            int32_t p0, int32_t n_kv, int32_t causal) {
+    SkTile t;
+    t.kvh = (int32_t)(x / per_kv);
+    const int64_t rem = x - (int64_t)t.kvh * per_kv;
+    int64_t acc = 0;
+    t.qt = n_qtiles - 1;
+    t.nblk = prefill_tile_blocks(t.qt, n_q, p0, n_kv, causal);
+    for (int32_t q = 0; q < n_qtiles; q++) {
+        const int32_t nb = prefill_tile_blocks(q, n_q, p0, n_kv, causal);
+        if (rem < acc + (int64_t)group * nb) {
+            t.qt = q;
+            t.nblk = nb;
+            break;
+        }
+        acc += (int64_t)group * nb;
+    }
+    t.gi = (int32_t)((rem - acc) / t.nblk);
+    t.start = (int64_t)t.kvh * per_kv + acc + (int64_t)t.gi * t.nblk;
+    return t;
+}
+// Slot of the partial that range r holds for a tile starting at unit `start`: 2 r when it is the range's first
+// segment (the tile started in an earlier range, or exactly at lo(r)), else 2 r + 1 (the range's last segment).
+__host__ __device__ inline int64_t sk_slot(int64_t total, int32_t ranges, int32_t r, int64_t start) {
+    return 2 * (int64_t)r + (start > sk_lo(total, ranges, r) ? 1 : 0);
+}
 
 // Packing of the IR self-attention's [B][N][3E] q|k|v rows into the attention kernel's operands when the rows cannot be
 // read in place (head_dim not a multiple of 8): f32 query rows and f16 key|value rows with head_dim padded to hdp

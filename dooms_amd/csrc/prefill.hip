@@ -37,6 +37,15 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef half_t half2_t __attribute__((ext_vector_type(2)));
 constexpr half2_t kOnes2 = {(half_t)1.f, (half_t)1.f};
 
+// Relaxed device-scope accesses of the stream-K partials: coherent across the XCDs without cache maintenance.
+__device__ __forceinline__ void put_f32(float * a, float v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(a), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_f32(const float * a) {
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<float *>(a)), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+}
+
 // LDS tiles are row-major with padded rows: K rows HD + 8 halves apart (the 16-byte reads of 16 consecutive rows at one
 // column land on 16 distinct 4-bank groups), V rows HD + 32 halves apart (a row step of 16 banks mod 64: the 4 rows x
 // 32 bytes that each 16-lane group reads through the transposing read, for both groups of a 32-lane phase, land on 64
@@ -89,12 +98,23 @@ __device__ __forceinline__ void prefill_work(uint32_t o, int nq, int G, int n_kv
 // points): 1 f32, 2 bf16, 3 f16 rows with head_dim p.hdv (a multiple of 8, at most HD) and heads p.head_stride
 // elements apart. Q, K and V are rounded to half as they are loaded (K and V when the tile goes into LDS, so the
 // prefetch stays in flight), columns past p.hdv read as zeros, and the output is written in the rows' type.
-template <int HD, bool POS, int W, bool ROPE, int KSP, int SA>
-__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 && HD <= 128 ? 2 : 1, KSP == 1 && HD <= 128 ? 2 : 1)))
-void prefill_kernel(PrefillParams p) {
+// SK (stream-K, W = 8, KSP = 1, SA = 0 only): the tile's key blocks ib0 .. ib1 - 1 only. When that is not the whole
+// tile, the partial (m, l, O) goes to this range's slot (sk_slot) of p.sk_part and the tile's counter counts it in; the
+// range that completes the count merges every slot of the tile and writes the output.
+struct SkSegment {
+    int32_t ib0, ib1;   // key blocks of this segment
+    int32_t range;      // the workgroup's range
+    int64_t start;      // the tile's first unit
+    int64_t tile;       // the tile's index in the launch order (its counter)
+};
+
+template <int HD, bool POS, int W, bool ROPE, int KSP, int SA, bool SK>
+__device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSmem<HD, KSP> & sm, int kvh, int gi, int qt,
+                                             const SkSegment & seg) {
     constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
     static_assert(W % KSP == 0, "whole row tiles");
     static_assert(!(ROPE && SA), "the rotated prompt path reads f16 operands");
+    static_assert(!SK || (W == 8 && KSP == 1 && SA == 0), "stream-K: the 8-wave plan on the attention operands");
     constexpr int ES = SA == 1 ? 4 : 2;  // bytes per element of the q, k, v rows
     constexpr int NR = SA == 1 ? 2 : 1;  // 16-byte loads per 8 elements
     constexpr int KS = HD / 16;          // MFMA steps along head_dim for S^T
@@ -105,14 +125,8 @@ void prefill_kernel(PrefillParams p) {
     constexpr int NI = NB / kWaves;      // loads per thread per step, for each of K and V
     static_assert(NB % kWaves == 0, "whole loads per thread");
     constexpr int KP = PrefillSmem<HD, KSP>::KP, VP = PrefillSmem<HD, KSP>::VP;
-    __shared__ PrefillSmem<HD, KSP> sm;
 
-    // ---- work item: each XCD a contiguous range of a kv-head-major order, heavy query tiles first ----
-    const uint32_t n_work = (uint32_t)p.n_qtiles * p.n_head;
     const int G = p.group;
-    int kvh, gi, qt_order;
-    prefill_work(xcd_remap(blockIdx.x, n_work), p.n_qtiles, G, p.n_head_kv, kvh, gi, qt_order);
-    const int qt = p.causal ? p.n_qtiles - 1 - qt_order : qt_order;
     const int h = kvh * G + gi;
     const int q0 = qt * kPrefillRows;
     // problem blockIdx.y of a batch: its own query, cache, output and lse blocks
@@ -131,6 +145,8 @@ void prefill_kernel(PrefillParams p) {
     const int last_row = min(q0 + kPrefillRows, p.n_q) - 1;
     const int kend = p.causal ? min(p.n_kv, p.p0 + last_row + 1) : p.n_kv;
     const int nblk = (kend + KB - 1) / KB;  // steps of KB keys
+    const int ib0 = SK ? seg.ib0 : 0, ib1 = SK ? seg.ib1 : nblk;  // the steps of this call
+    const int nb = ib1 - ib0;
 
     const int64_t hstride = SA ? p.head_stride : HD;  // elements between consecutive heads of a row
     const char * kg = reinterpret_cast<const char *>(p.k) + (bkv + (int64_t)kvh * hstride) * ES;
@@ -233,14 +249,14 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) ld8(qp, 16 * ks + 8 * hgrp, qr[ks]);
     }
-    if (nblk > 0 && W == 4) {
+    if (nb > 0 && W == 4) {
         // the short-prompt plans: steps 0 and 1 go out together (step 1 into registers of its own, unconditionally:
         // past the cache its rows are clamped to the last one and never used), so the prologue waits for one round
         // trip instead of two (the 8-wave plan's long chunks keep the plain order)
         u32x4 k1[NI][NR], v1[NI][NR];
-        load_tile(0);
+        load_tile(ib0 * KB);
         __builtin_amdgcn_sched_barrier(0);
-        load_tile_into(KB, k1, v1);
+        load_tile_into((ib0 + 1) * KB, k1, v1);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (!ROPE) {  // the query is used from here on (the compiler would otherwise hoist its use above)
 #pragma unroll
@@ -257,8 +273,8 @@ void prefill_kernel(PrefillParams p) {
                 kreg[i][j] = k1[i][j];
                 vreg[i][j] = v1[i][j];
             }
-    } else if (nblk > 0) {
-        load_tile(0);
+    } else if (nb > 0) {
+        load_tile(ib0 * KB);
         if constexpr (!ROPE) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++)
@@ -267,7 +283,7 @@ void prefill_kernel(PrefillParams p) {
         }
         q_operand();
         store_tile(0);
-        if (nblk > 1) load_tile(KB);
+        if (nb > 1) load_tile((ib0 + 1) * KB);
     } else {
         q_operand();
     }
@@ -289,13 +305,14 @@ void prefill_kernel(PrefillParams p) {
     // + 32 dt columns) and receives V[rows + 0..3][32 dt + lane % 32]
     const int v_base = (4 * hgrp + (lane % 16) / 4) * VP + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
 
-    for (int ib = 0; ib < nblk; ib++) {
+    for (int jb = 0; jb < nb; jb++) {
+        const int ib = ib0 + jb;
         const int kb = ib * KB + kh * kBK;  // this wave's block of the step
-        const int buf = ib & 1;
+        const int buf = jb & 1;
         __syncthreads();  // step ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
-        if (ib + 1 < nblk) {
+        if (jb + 1 < nb) {
             store_tile(buf ^ 1);
-            if (ib + 2 < nblk) load_tile((ib + 2) * KB);
+            if (jb + 2 < nb) load_tile((ib + 2) * KB);
         }
         if (kb >= kend || (p.causal && kb > wave_last)) continue;  // every key of the block is past this wave's rows
         const half_t * ks_ = sm.k[buf] + kh * kBK * KP;
@@ -443,6 +460,68 @@ void prefill_kernel(PrefillParams p) {
         }
     }
 
+    if constexpr (SK) {
+        if (ib0 != 0 || ib1 != nblk) {
+            // ---- part of a tile: its (m, l, O) into this range's slot with device-scope stores, which are complete
+            // before the tile's counter counts it in; the range that brings the count to the tile's number of ranges
+            // folds every slot of the tile, in range order (its own read back too, so that the result does not depend
+            // on which range finished last), and writes the output ----
+            constexpr int J = HD / 2 + 2;  // floats per lane: O, m, l
+            __shared__ int s_sk_last;
+            const int64_t total = p.sk_total;
+            const int32_t R = p.sk_ranges;
+            auto lane_slot = [&](int64_t slot) {
+                return p.sk_part + slot * kPrefillSlotFloats<HD> + (int64_t)wave * J * kWave + lane;
+            };
+            const int64_t own = sk_slot(total, R, seg.range, seg.start);
+            {
+                float * d = lane_slot(own);
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) put_f32(d + (16 * dt + v) * kWave, o[dt][v]);
+                put_f32(d + (J - 2) * kWave, m_run);
+                put_f32(d + (J - 1) * kWave, l_run);
+            }
+            const int32_t r_first = sk_range_of(total, R, seg.start), r_last = sk_range_of(total, R, seg.start + nblk - 1);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                const uint32_t done =
+                    __hip_atomic_fetch_add(p.sk_counters + seg.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_sk_last = done == (uint32_t)(r_last - r_first);
+            }
+            __syncthreads();
+            if (!s_sk_last) return;
+            __builtin_amdgcn_s_waitcnt(0);
+            m_run = kNegInf;
+            l_run = 0.f;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) o[dt][v] = 0.f;
+            for (int32_t r = r_first; r <= r_last; r++) {
+                const float * d = lane_slot(sk_slot(total, R, r, seg.start));
+                float x[DT][16];
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) x[dt][v] = get_f32(d + (16 * dt + v) * kWave);
+                const float m1 = get_f32(d + (J - 2) * kWave), l1 = get_f32(d + (J - 1) * kWave);
+                const float mn = fmaxf(m_run, m1);
+                const float w0 = m_run == kNegInf ? 0.f : exp2_fast(m_run - mn);
+                const float w1 = m1 == kNegInf ? 0.f : exp2_fast(m1 - mn);
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) o[dt][v] = o[dt][v] * w0 + x[dt][v] * w1;
+                l_run = l_run * w0 + l1 * w1;
+                m_run = mn;
+            }
+            if (threadIdx.x == 0) __hip_atomic_store(p.sk_counters + seg.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
     // ---- normalize and store: lane holds O[qrow][32 dt + 8 (v / 4) + 4 hgrp + v % 4] ----
     if (qrow < p.n_q) {
         const float inv = 1.f / l_run;
@@ -483,6 +562,46 @@ void prefill_kernel(PrefillParams p) {
     }
 }
 
+template <int HD, bool POS, int W, bool ROPE, int KSP, int SA>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 && HD <= 128 ? 2 : 1, KSP == 1 && HD <= 128 ? 2 : 1)))
+void prefill_kernel(PrefillParams p) {
+    __shared__ PrefillSmem<HD, KSP> sm;
+    // ---- work item: each XCD a contiguous range of a kv-head-major order, heavy query tiles first ----
+    const uint32_t n_work = (uint32_t)p.n_qtiles * p.n_head;
+    int kvh, gi, qt_order;
+    prefill_work(xcd_remap(blockIdx.x, n_work), p.n_qtiles, p.group, p.n_head_kv, kvh, gi, qt_order);
+    const int qt = p.causal ? p.n_qtiles - 1 - qt_order : qt_order;
+    prefill_tile<HD, POS, W, ROPE, KSP, SA, false>(p, sm, kvh, gi, qt, SkSegment{});
+}
+
+// Stream-K: p.sk_ranges workgroups (one per CU), each over an equal range of the (tile, key block) units, so that no CU
+// idles while another finishes a tile (a 2048-row chunk of 28 heads is 224 equal tiles for 256 CUs; a causal prompt's
+// tiles differ in length). Workgroup b runs on XCD b % 8 (workgroups are dealt to the XCDs round-robin) and takes range
+// (b % 8) R / 8 + b / 8: each XCD walks one contiguous eighth of the kv-head-major order, so its L2 streams the K/V of
+// few kv heads.
+template <int HD, bool POS, bool ROPE>
+__global__ __launch_bounds__(8 * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_sk_kernel(PrefillParams p) {
+    __shared__ PrefillSmem<HD, 1> sm;
+    const int32_t R = p.sk_ranges;
+    const int32_t r = (int32_t)(blockIdx.x % 8) * (R / 8) + (int32_t)(blockIdx.x / 8);
+    const int64_t total = p.sk_total, lo = sk_lo(total, R, r), hi = sk_lo(total, R, r + 1);
+    int64_t per_kv = 0;
+    for (int q = 0; q < p.n_qtiles; q++) per_kv += prefill_tile_blocks(q, p.n_q, p.p0, p.n_kv, p.causal);
+    per_kv *= p.group;
+    for (int64_t x = lo; x < hi;) {
+        const SkTile t = sk_locate(x, per_kv, p.group, p.n_qtiles, p.n_q, p.p0, p.n_kv, p.causal);
+        SkSegment seg;
+        seg.ib0 = (int32_t)(x - t.start);
+        seg.ib1 = (int32_t)(hi - t.start < t.nblk ? hi - t.start : t.nblk);
+        seg.range = r;
+        seg.start = t.start;
+        seg.tile = ((int64_t)t.kvh * p.n_qtiles + t.qt) * p.group + t.gi;
+        __syncthreads();  // the previous segment's waves are done with the LDS tiles
+        prefill_tile<HD, POS, 8, ROPE, 1, 0, true>(p, sm, t.kvh, t.gi, t.qt, seg);
+        x = t.start + seg.ib1;
+    }
+}
 
 }  // namespace
 
@@ -611,6 +730,12 @@ hipError_t launch_self_attn_unpack(const SelfAttnUnpackParams & p, hipStream_t s
 
 template <int HD, bool POS, bool ROPE, int SA>
 void launch_prefill_r(const PrefillParams & p, int plan, int n_batch, hipStream_t stream) {
+    if constexpr (SA == 0) {
+        if (p.sk_ranges > 0) {  // planned by the caller for plan 8 and one problem only
+            hipLaunchKernelGGL((prefill_sk_kernel<HD, POS, ROPE>), dim3((uint32_t)p.sk_ranges), dim3(8 * kWave), 0, stream, p);
+            return;
+        }
+    }
     const dim3 grid((uint32_t)p.n_qtiles * p.n_head, (uint32_t)n_batch);
     if (plan == 8) hipLaunchKernelGGL((prefill_kernel<HD, POS, 8, ROPE, 1, SA>), grid, dim3(8 * kWave), 0, stream, p);
     else if (plan == 4) hipLaunchKernelGGL((prefill_kernel<HD, POS, 4, ROPE, 1, SA>), grid, dim3(4 * kWave), 0, stream, p);

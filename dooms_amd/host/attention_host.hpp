@@ -94,6 +94,7 @@ struct LlamaAttentionConfig {  // the attention fields of LlamaDecoderConfig (me
     int32_t head_dim = 0;    // a power of two in [4, 256]
     float rope_base = 10000.f;  // rotary frequency base (rope.freq_base)
     bool rope_neox = false;     // rotary pairs (i, i + head_dim / 2) (qwen2) instead of (2i, 2i + 1) (llama)
+    int32_t n_batch = 0;        // the largest prompt chunk prompt() is given (n_batch, metal_llama_decoder.h:33); 0: 2048
     // Launch plans fixed for measuring, as the reference's prefill_tile (metal_llama_decoder.h:35-37); all 0: the
     // library's plans. Not model metadata.
     mx_attn_tuning tuning{};
@@ -123,6 +124,13 @@ public:
             dp.causal = 1;
             bytes = std::max(bytes, mx_attn_prefill_workspace_bytes(&dp));
         }
+        // and the flash kernel's stream-K slots, when its plan splits the largest chunk over the CUs (at the end of the
+        // context, where its tiles are longest; a chunk that finds the workspace short of them runs unsplit)
+        const int32_t n_batch = std::min<int32_t>(c.n_ctx, c.n_batch > 0 ? c.n_batch : 2048);
+        mx_attn_desc db = a->desc(n_batch, 0, 0);
+        db.p0 = c.n_ctx - n_batch;
+        db.causal = 1;
+        bytes = std::max(bytes, mx_attn_prefill_workspace_bytes(&db));
         if (Status st = a->ws_.reserve(bytes, stream); !st.is_ok()) return st;
         out = std::move(a);
         return {};

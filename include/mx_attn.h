@@ -49,7 +49,7 @@ extern "C" {
 #endif
 
 #define MX_ATTN_API __attribute__((visibility("default")))
-#define MX_ATTN_ABI_VERSION 2
+#define MX_ATTN_ABI_VERSION 3
 
 /* Return codes: the numbering of dooms_code (include/dooms/dooms_c.h:24-33). */
 #define MX_ATTN_OK 0
@@ -74,6 +74,8 @@ typedef struct mx_attn_tuning {
     int32_t decode_max_workgroups; /* decode: workgroup cap of one launch for the split plan, >= 1; 0: 1536 */
     int32_t prefill_plan;          /* flash prefill workgroups (prefill_tile): 8 = 8 waves x 32 query rows, 4 = 4 waves x
                                       32 rows, 2 = 4 waves over 2 row tiles splitting each tile's key blocks; 0: planned */
+    int32_t prefill_stream;        /* the 8-wave plan's stream-K split over the CUs (mx_attn_prefill_ws and
+                                      mx_attn_prefill_rope_ws only): 1 whenever it applies, -1 never, 0: planned */
 } mx_attn_tuning;
 
 /*

@@ -32,7 +32,7 @@ def exported():
 
 
 def test_library_loads():
-    assert _lib.lib().mx_attn_abi_version() == 2
+    assert _lib.lib().mx_attn_abi_version() == 3
 
 
 def test_exports_exactly_the_header():
@@ -45,8 +45,9 @@ def test_desc_layout_matches_c(tmp_path):
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mx_attn.h"\n'
                    'int main(void){printf("%zu %zu %zu %zu %zu\\n", sizeof(mx_attn_desc), offsetof(mx_attn_desc, reserved),'
                    ' offsetof(mx_attn_desc, q_stride), offsetof(mx_attn_desc, out_stride), offsetof(mx_attn_desc, scale));'
-                   'printf("%zu %zu %zu %zu\\n", offsetof(mx_attn_desc, tuning), sizeof(mx_attn_tuning),'
-                   ' offsetof(mx_attn_tuning, prefill_plan), offsetof(mx_self_attn_desc, tuning));'
+                   'printf("%zu %zu %zu %zu %zu\\n", offsetof(mx_attn_desc, tuning), sizeof(mx_attn_tuning),'
+                   ' offsetof(mx_attn_tuning, prefill_plan), offsetof(mx_attn_tuning, prefill_stream),'
+                   ' offsetof(mx_self_attn_desc, tuning));'
                    'return 0;}\n')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
@@ -55,7 +56,7 @@ def test_desc_layout_matches_c(tmp_path):
     D = _lib.MxAttnDesc
     T, S = _lib.MxAttnTuning, _lib.MxSelfAttnDesc
     assert got == [ctypes.sizeof(D), D.reserved.offset, D.q_stride.offset, D.out_stride.offset, D.scale.offset,
-                   D.tuning.offset, ctypes.sizeof(T), T.prefill_plan.offset, S.tuning.offset]
+                   D.tuning.offset, ctypes.sizeof(T), T.prefill_plan.offset, T.prefill_stream.offset, S.tuning.offset]
 
 
 def desc(**kw):
@@ -104,6 +105,8 @@ def decode(d, lens=(100,), kp=None, vp=None, q=A, out=A, lse=0, ws=A, ws_bytes=1
     (dict(tuning=dict(decode_waves=6)), _lib.INVALID_ARGUMENT, "decode_waves"),
     (dict(tuning=dict(decode_max_workgroups=-2)), _lib.INVALID_ARGUMENT, "decode_max_workgroups"),
     (dict(tuning=dict(prefill_plan=3)), _lib.INVALID_ARGUMENT, "prefill_plan"),
+    (dict(tuning=dict(prefill_stream=2)), _lib.INVALID_ARGUMENT, "prefill_stream"),
+    (dict(tuning=dict(prefill_stream=-2)), _lib.INVALID_ARGUMENT, "prefill_stream"),
 ])
 def test_descriptor_checks(kw, code, msg):
     for call in (lambda d: prefill(d), lambda d: decode(d)):
@@ -210,8 +213,32 @@ def test_prefill_ws_checks():
     # the decode workspace (the counter region, 32 splits of partials), then room for the rotated f32 query rows of the
     # rope call
     assert n == 2048 * 256 + 32 * 4 * 7 * 16 * 132 * 4 + 16 * 28 * 128 * 4
+    # a 2048-row chunk of 28 heads: 224 tiles of the 8-wave grid for 256 CUs. At head dim 64 the stream-K split is
+    # planned; its workspace is the counter region, then 2 partial slots per range (256 ranges) of 8 waves x 64 lanes
+    # x (32 + 2) floats. At head dim 128 the grid runs (no workspace) unless the tuning forces the split.
+    big64 = desc(n_head=28, n_head_kv=4, head_dim=64, n_q=2048, p0=0, q_stride=1792, kv_stride=256, out_stride=1792)
+    assert _lib.prefill_workspace_bytes(big64) == 2048 * 256 + 512 * 8 * 64 * 34 * 4
     big = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584)
-    assert _lib.prefill_workspace_bytes(big) == 0  # the flash kernel, no workspace
+    assert _lib.prefill_workspace_bytes(big) == 0
+    forced = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584,
+                  tuning=dict(prefill_stream=1))
+    assert _lib.prefill_workspace_bytes(forced) == 2048 * 256 + 512 * 8 * 64 * 66 * 4
+    off = desc(n_head=28, n_head_kv=4, head_dim=64, n_q=2048, p0=0, q_stride=1792, kv_stride=256, out_stride=1792,
+               tuning=dict(prefill_stream=-1))
+    assert _lib.prefill_workspace_bytes(off) == 0  # the flash kernel's own grid, no workspace
+    # a causal 4096-token prompt of 14 heads at head dim 64 (224 tiles): planned; of 32 heads (512 tiles, which the
+    # grid's heaviest-first dealing balances): not
+    assert _lib.prefill_workspace_bytes(desc(n_head=14, n_head_kv=2, head_dim=64, n_q=4096, q_stride=896,
+                                             kv_stride=128, out_stride=896)) == 2048 * 256 + 512 * 8 * 64 * 34 * 4
+    assert _lib.prefill_workspace_bytes(desc(n_head=32, n_head_kv=8, head_dim=64, n_q=4096, q_stride=2048,
+                                             kv_stride=512, out_stride=2048)) == 0
+    # 256 equal tiles (non-causal, 2048 rows of 32 heads): one full round of the grid, nothing to balance
+    even = desc(n_head=32, n_head_kv=8, n_q=2048, p0=0, n_kv=4096, causal=0, q_stride=4096, kv_stride=1024,
+                out_stride=4096)
+    assert _lib.prefill_workspace_bytes(even) == 0
+    assert _lib.prefill_workspace_bytes(desc(n_head=32, n_head_kv=8, n_q=2048, p0=0, n_kv=4096, causal=0,
+                                             q_stride=4096, kv_stride=1024, out_stride=4096,
+                                             tuning=dict(prefill_stream=1))) == 2048 * 256 + 512 * 8 * 64 * 66 * 4
     assert _lib.prefill_workspace_bytes(desc(n_head=3, n_head_kv=2)) == 0 and "multiple" in _lib.last_error()
     call = lambda d, ws=A, nb=1 << 40: _lib.prefill_ws_raw(d, A, A, A, A, 0, ws, nb, 0)
     n_dec = n - 16 * 28 * 128 * 4  # mx_attn_prefill_ws itself needs only the decode part
@@ -370,3 +397,16 @@ def test_host_code_under_address_and_undefined_behaviour_sanitizers():
                        env={**os.environ, "ASAN_OPTIONS": "detect_leaks=0"})  # the HIP runtime's own allocations
     assert r.returncode == 0, r.stdout + r.stderr
     assert "abi_checks_sanitized: ok" in r.stdout
+
+
+def test_stream_k_partition(tmp_path):
+    # the stream-K prefill's partition arithmetic (mx_kernels.hpp), checked on the CPU over many launch shapes by
+    # tests/cpp/sk_partition_check.cpp: every unit in exactly one segment, each split tile's slots where its merge reads
+    exe = tmp_path / "sk_partition_check"
+    src = os.path.join(ROOT, "tests", "cpp", "sk_partition_check.cpp")
+    subprocess.run(["/opt/rocm/bin/hipcc", "-O2", "-std=c++17", "--offload-arch=gfx950",
+                    "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "dooms_amd", "csrc"), src,
+                    "-o", str(exe)], check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+    assert "0 failures" in r.stdout
