@@ -51,6 +51,9 @@ def parse():
                          "(counters) over the last --last dispatches of the kernels whose names contain --kernel")
     ap.add_argument("--kernel", default="decode_kernel")
     ap.add_argument("--last", type=int, default=0, help="dispatches at the end of the trace to summarize (0: all)")
+    ap.add_argument("--trace-decode", action="store_true",
+                    help="phase timestamps of the decode kernel (dooms_amd/libmx_attn_trace.so) on the headline and "
+                         "short-shape workloads: one JSON line per workload, microseconds from the launch's first start")
     return ap.parse_args()
 
 
@@ -407,10 +410,56 @@ def cpu_prefill_baseline(torch, prob, budget_s, threads):
     return flops / t_total / 1e12, rows, t_total
 
 
+def trace_decode(args):
+    """Per-workgroup phase stamps of the decode kernel (the MX_ATTN_TRACE build), read after the graph-timed replays:
+    the stamps are those of the last launch (the last layer of the last replay)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+    from dooms_amd import _lib
+    _lib.LIB_PATH = os.path.join(ROOT, "dooms_amd", "libmx_attn_trace.so")
+    L = _lib.lib()
+    L.mx_attn_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    L.mx_attn_trace_read.restype = ctypes.c_int
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    workloads = [("cfg3 Llama-3-8B batch 1, 8192 keys", 32, 8, 128, [8192], 1, 32),
+                 ("cfg1 Qwen2.5-0.5B, 513 keys", 14, 2, 64, [513], 1, 32),
+                 ("cfg4 Whisper cross-attention, 1500 frames, greedy", 20, 20, 64, [1500], 1, 32),
+                 ("cfg4 Whisper self-attention, 449 keys", 20, 20, 64, [449], 1, 32)]
+    names = ["wave walk done", "waves merged", "partial published", "split counted", "splits merged"]
+    for name, nh, nkv, hd, lens, nq, layers in workloads:
+        prob = DecodeProblem(torch, gen, nh, nkv, hd, lens, layers, n_q=nq)
+        ms, _ = time_graph(torch, prob.step, args.steps, args.warmup)
+        buf = np.zeros(8192 * 16, dtype=np.uint64)
+        assert L.mx_attn_trace_read(buf.ctypes.data, buf.nbytes) == 0
+        t = buf.reshape(8192, 16).astype(np.int64)
+        last = t[:, 0].max()
+        t = t[t[:, 0] >= last - 5000]  # the last launch's workgroups (older stamps are > 50 us earlier)
+        t0 = t[:, 0].min()
+        rel = lambda col, sel: (col[sel] - t0) / 100.0  # the real-time clock ticks at 100 MHz
+        waves = t[:, 1:9]
+        walk = np.where(waves > 0, waves, 0).max(axis=1)
+        cols = [walk, t[:, 9], t[:, 10], t[:, 11], t[:, 12]]
+        phases = {}
+        for nm, col in zip(names, cols):
+            sel = col > 0
+            if sel.any():
+                x = rel(col, sel)
+                phases[nm] = {"p50": round(float(np.median(x)), 2), "max": round(float(x.max()), 2), "n": int(sel.sum())}
+        print(json.dumps({"workload": name, "us_per_launch_graph": round(ms * 1000 / layers, 3),
+                          "workgroups": int(len(t)), "start_spread_us": round(float((t[:, 0].max() - t0) / 100), 2),
+                          "phases_us_from_first_start": phases}), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.summarize:
         return summarize(args.summarize, args.kernel, args.last)
+    if args.trace_decode:
+        return trace_decode(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention hot path has no multi-GPU path here "
                                    "(run with --gpus 1)", "n_gpus": args.gpus}))

@@ -30,7 +30,7 @@ def build(verbose: bool = False, out: str = LIB, defines=()) -> str:
     """Compiles every HIP source (one hipcc per source, in parallel) and links dooms_amd/libmx_attn.so; returns its
     path. Raises on a compile error. `out` and `defines` (extra -D macros) serve experiments that build variants."""
     from concurrent.futures import ThreadPoolExecutor
-    objdir = os.path.join(os.path.dirname(out), "_build")
+    objdir = os.path.join(os.path.dirname(out), "_build", os.path.splitext(os.path.basename(out))[0])
     os.makedirs(objdir, exist_ok=True)
     inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC, *[f"-D{d}" for d in defines]]
     compile_flags = [f for f in FLAGS if f != "-shared"]
@@ -48,6 +48,15 @@ def build(verbose: bool = False, out: str = LIB, defines=()) -> str:
         print(msgs + msg, file=sys.stderr)
     os.replace(out + ".tmp", out)
     return out
+
+
+LIB_TRACE = os.path.join(os.path.dirname(LIB), "libmx_attn_trace.so")
+
+
+def build_trace(verbose: bool = False) -> str:
+    """The phase-trace variant of the library (MX_ATTN_TRACE: the decode kernel stamps its phases per workgroup and
+    exports mx_attn_trace_read), used by `bench.py --trace-decode`; the product library compiles the stamps away."""
+    return build(verbose=verbose, out=LIB_TRACE, defines=("MX_ATTN_TRACE=1",))
 
 
 TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host_attention.cpp")

@@ -443,6 +443,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         p.rows = s.rows;
         p.n_rowtiles = s.n_rowtiles;
         p.seq0 = b0;
+        p.xcd_heads = n_seq == 1 && d.n_head_kv % 8 == 0;
         p.scale_log2 = d.scale * 1.4426950408889634f;
         // split plan (see workgroup_cap)
         const int64_t quantum = mx::kDecodeChunkQuantum;
