@@ -317,8 +317,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int v = 0; v < 4; v++) bmax = fmaxf(bmax, sc[mt][v]);
-        bmax = fmaxf(bmax, shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, shfl_xor(bmax, 32));
+        bmax = xor32_max(xor16_max(bmax));
         const float m_new = fmaxf(m_run, bmax);
         const bool none = m_new == kNegInf;      // no visible key yet for this row
         const float m_use = none ? 0.f : m_new;  // then every exponent below is 2^-inf = 0
@@ -361,8 +360,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
     if (lane == 0) MX_TRACE(1 + wave);
     // ---- wave totals: l over the 4 score-lane groups; O is complete per lane (the products summed every key) ----
-    l_run += shfl_xor(l_run, 16);
-    l_run += shfl_xor(l_run, 32);
+    l_run = xor32_add(xor16_add(l_run));
     if (lane < RT) {
         s_m[wave][lane] = m_run;
         s_l[wave][lane] = l_run;

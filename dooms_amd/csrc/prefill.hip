@@ -322,21 +322,22 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
         // product waits only for reads issued one product earlier.
         float16_t sc[2];
         {
-            constexpr int NS = 2 * KS;  // products: (mt, kk) in order
-            u32x4 ka[2];
+            constexpr int NS = 2 * KS;  // products
+            // (kk, mt) order: the two key tiles' products alternate, so consecutive products are independent (cfg5 +0.8 %)
+            constexpr int RA = 1;  // reads in flight ahead of the product (2 or 3 measured no faster)
+            u32x4 ka[RA + 1];
             auto kread = [&](int i) {
-                return *reinterpret_cast<const u32x4 *>(ks_ + k_base + 32 * (i / KS) * KP + 16 * (i % KS));
+                return *reinterpret_cast<const u32x4 *>(ks_ + k_base + 32 * (i % 2) * KP + 16 * (i / 2));
             };
-            ka[0] = kread(0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) sc[0][v] = sc[1][v] = 0.f;
+#pragma unroll
+            for (int i = 0; i < RA; i++) ka[i] = kread(i);
 #pragma unroll
             for (int i = 0; i < NS; i++) {
-                if (i + 1 < NS) ka[(i + 1) & 1] = kread(i + 1);
-                const int mt = i / KS, kk = i % KS;
-                if (kk == 0) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) sc[mt][v] = 0.f;
-                }
-                sc[mt] = mfma32x32x16(as_half8(ka[i & 1]), qb[kk], sc[mt]);
+                if (i + RA < NS) ka[(i + RA) % (RA + 1)] = kread(i + RA);
+                const int mt = i % 2, kk = i / 2;
+                sc[mt] = mfma32x32x16(as_half8(ka[i % (RA + 1)]), qb[kk], sc[mt]);
             }
         }
         // block max (raw scores when the scale is positive); the mask only where a block crosses the diagonal or the
@@ -365,7 +366,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                     bmax = fmaxf(bmax, x);
                 }
         }
-        bmax = fmaxf(bmax, shfl_xor(bmax, 32));
+        bmax = xor32_max(bmax);
         // lazy rescale: the reference maximum moves only when the block's maximum exceeds it by more than 8 (base 2);
         // the probabilities then stay below 2^8, well inside f16, and the O rescale below is rare
         const float m_cand = fmaxf(m_run, POS ? bmax * c : bmax);
@@ -425,7 +426,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
         }
     }
 
-    l_run += shfl_xor(l_run, 32);
+    l_run = xor32_add(l_run);
     if constexpr (KSP > 1) {
         // ---- the KSP waves of a row tile merge their (m, l, O): waves kh > 0 leave theirs in LDS (the tiles are no
         // longer read), the wave kh = 0 folds them in ----
