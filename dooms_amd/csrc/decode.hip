@@ -51,6 +51,7 @@ constexpr int kBlockKeys = 32;  // keys per wave iteration
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMergeChunk = 16;  // splits whose partials one thread has in flight at once during the merge
+constexpr int kMaxSplitsPerTile = 32;  // the host's split plan never makes more
 
 // Relaxed device-scope atomic accesses of float pairs: coherent across the XCDs without cache maintenance.
 __device__ __forceinline__ void publish2(float * p, float a, float b) {
@@ -62,6 +63,17 @@ __device__ __forceinline__ void collect2(const float * p, float & a, float & b) 
                                          __HIP_MEMORY_SCOPE_AGENT);
     a = __uint_as_float((uint32_t)v);
     b = __uint_as_float((uint32_t)(v >> 32));
+}
+
+// 16-byte device-scope (sc1) buffer loads: coherent across the XCDs, a quarter of the instructions of 4-byte atomic
+// loads. The resource is built from a wave-uniform base (a per-lane base would make the compiler loop over the distinct
+// descriptors of the wave); lanes differ in their byte offsets.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void * base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+}
+constexpr int kCpolSc1 = 16;  // the cache-policy bit that makes a buffer access device-scope on gfx950
+__device__ __forceinline__ u32x4 load16_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
 }
 
 template <int HD>
@@ -82,6 +94,126 @@ __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, 
     } else {
         p.out[off] = (half_t)a;
         p.out[off + 1] = (half_t)b;
+    }
+}
+
+// The cross-split merge of a tile with more splits than one load round of the per-pair merge holds (> kMergeChunk):
+// every (m, l) pair of the tile is loaded once (one thread each) and turned into per-split weights 2^(m - M) in LDS,
+// while the accumulator columns come in 16-byte device-scope loads, each column's splits striped over SF threads and
+// the stripes summed through LDS. Half the bytes of the per-pair merge through the merging CU, whose threads would
+// each load their row's (m, l) for every split: Llama-3-8B at 8192 keys (32 splits) 13.85 -> 13.44 us per launch.
+// With few splits the two extra barriers cost more than the bytes saved, so the per-pair merge stays there; it also
+// stays in the 4-wave and head-dim-64 kernels (batch 4 +0.1 us; at head dim 64 the path's registers cost a wave of
+// occupancy: 112 -> 136 VGPRs).
+template <int HD, int RT, bool F32, int NW, size_t LDS_BYTES>
+__device__ __forceinline__ void merge_wide(const DecodeParams & p, const float * part_tile, int ns, int rt, int g, int G,
+                                           int64_t seq_row0, char * lds) {
+    constexpr int kThreads = NW * kWave;
+    constexpr int SS = RT * (HD + 4);                       // floats between the partials of consecutive splits
+    constexpr int NC = RT * HD / 4;                         // float4 columns of the tile
+    constexpr int SF = kThreads >= NC ? kThreads / NC : 1;  // threads per column (stripes of the splits)
+    constexpr int CPT = NC > kThreads ? NC / kThreads : 1;  // columns per thread
+    constexpr int MC = 16 / CPT > 0 ? 16 / CPT : 1;         // splits of each column loaded per round
+    constexpr int NPAIR = kMaxSplitsPerTile * RT;           // (m, l) slots: [split][row]
+    constexpr int MLT = (NPAIR + kThreads - 1) / kThreads;  // (m, l) pairs per thread
+    constexpr int kStatBytes = (NPAIR * 12 + RT * 8 + 15) / 16 * 16;
+    float2 * s_ml = reinterpret_cast<float2 *>(lds);        // [split][row] (m, l); an empty split as (-inf, 0)
+    float * s_w = reinterpret_cast<float *>(s_ml + NPAIR);  // [split][row] 2^(m - M)
+    float2 * s_row = reinterpret_cast<float2 *>(s_w + NPAIR);  // [row] (M, total)
+    float4_t * s_acc = reinterpret_cast<float4_t *>(lds + kStatBytes);  // [stripe - 1][column]
+    static_assert(kStatBytes + (SF - 1) * NC * 16 <= (int64_t)LDS_BYTES, "merge scratch fits the V staging areas");
+    const __amdgpu_buffer_rsrc_t rsrc = dev_rsrc(part_tile);
+    const int stripe = SF > 1 ? (int)threadIdx.x / NC : 0;  // wave-uniform
+    auto column = [&](int j) { return SF > 1 ? (int)threadIdx.x % NC : (int)threadIdx.x + j * kThreads; };
+    float2 ml[MLT];
+#pragma unroll
+    for (int i = 0; i < MLT; i++) {
+        const int e = min((int)threadIdx.x + i * kThreads, ns * RT - 1);  // past the end: a valid pair, not used
+        collect2(part_tile + (e / RT) * SS + (e % RT) * (HD + 4) + HD, ml[i].x, ml[i].y);
+    }
+    u32x4 px[CPT][MC];
+    auto load_round = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int col = column(j), pc = (col / (HD / 4)) * (HD + 4) + 4 * (col % (HD / 4));
+#pragma unroll
+            for (int e = 0; e < MC; e++) px[j][e] = load16_dev(rsrc, 4 * (pc + min(s0 + SF * e, ns - 1) * SS));
+        }
+    };
+    load_round(stripe);
+    // (the (m, l) loads went out first: the waits below leave the accumulator loads in flight)
+#pragma unroll
+    for (int i = 0; i < MLT; i++) {
+        const int e = (int)threadIdx.x + i * kThreads;
+        if (e < NPAIR) s_ml[e] = e < ns * RT && ml[i].y > 0.f ? ml[i] : make_float2(kNegInf, 0.f);
+    }
+    __syncthreads();
+    // each (split, row): the row's maximum over the splits (independent LDS reads, no branch) and the split's weight;
+    // split 0 also the row's total
+#pragma unroll
+    for (int i = 0; i < MLT; i++) {
+        const int e = (int)threadIdx.x + i * kThreads;
+        if (e >= NPAIR) break;  // wave-uniform
+        const int r = e % RT;
+        float mk[kMaxSplitsPerTile];
+#pragma unroll
+        for (int k = 0; k < kMaxSplitsPerTile; k++) mk[k] = s_ml[k * RT + r].x;
+        float M = kNegInf;
+#pragma unroll
+        for (int k = 0; k < kMaxSplitsPerTile; k++) M = fmaxf(M, mk[k]);
+        const float Mu = M == kNegInf ? 0.f : M;
+        s_w[e] = exp2_fast(s_ml[e].x - Mu);
+        if (e < RT) {
+            float tot = 0.f;
+#pragma unroll
+            for (int k = 0; k < kMaxSplitsPerTile; k++) tot = __builtin_fmaf(s_ml[k * RT + r].y, exp2_fast(mk[k] - Mu), tot);
+            s_row[r] = make_float2(M, tot);
+        }
+    }
+    __syncthreads();
+    float4_t acc[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; j++) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = stripe;;) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int r = column(j) / (HD / 4);
+#pragma unroll
+            for (int e = 0; e < MC; e++) {
+                const int k = s0 + SF * e;  // past the last split the slots' weights are 0 up to kMaxSplitsPerTile
+                const float w = k < kMaxSplitsPerTile ? s_w[min(k, kMaxSplitsPerTile - 1) * RT + r] : 0.f;
+                acc[j] += __builtin_bit_cast(float4_t, px[j][e]) * w;
+            }
+        }
+        s0 += SF * MC;
+        if (s0 >= ns) break;  // wave-uniform
+        load_round(s0);
+    }
+    if constexpr (SF > 1) {
+        if (stripe > 0) s_acc[(stripe - 1) * NC + threadIdx.x % NC] = acc[0];
+        __syncthreads();
+        if (stripe > 0) return;
+#pragma unroll
+        for (int k = 1; k < SF; k++) acc[0] += s_acc[(k - 1) * NC + threadIdx.x];
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int col = column(j), r = col / (HD / 4), c = 4 * (col % (HD / 4));
+        const int row = rt * RT + r;
+        if (row >= p.rows) continue;
+        const int t = row / G, h = g * G + row % G;
+        const float2 mt = s_row[r];
+        const float inv = 1.f / mt.y;
+        const int64_t off = (seq_row0 + t) * p.out_stride + (int64_t)h * HD + c;
+        if constexpr (F32) {
+            *reinterpret_cast<float4_t *>(p.out32 + off) = acc[j] * inv;
+        } else {
+            typedef half_t half4_t __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<half4_t *>(p.out + off) =
+                half4_t{(half_t)(acc[j][0] * inv), (half_t)(acc[j][1] * inv), (half_t)(acc[j][2] * inv),
+                        (half_t)(acc[j][3] * inv)};
+        }
+        if (c == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (mt.x + log2_fast(mt.y)) * kLn2;
     }
 }
 
@@ -428,6 +560,18 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     // chunk's splits; the row's (m, l) loads of a wave coalesce), then folds them with a running maximum. One memory
     // round trip per chunk, no LDS, no barrier. ----
     const int ns = n_split;
+    if constexpr (HD >= 128 && NW == 8) {
+        if (ns > kMergeChunk) {
+            merge_wide<HD, RT, F32, NW, sizeof s_v>(p, part_tile, ns, rt, g, G, seq_row0, reinterpret_cast<char *>(s_v));
+            if (threadIdx.x == 0)
+                __hip_atomic_store(p.counters + tile * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef MX_ATTN_TRACE
+            __syncthreads();
+            if (threadIdx.x == 0) MX_TRACE(12);
+#endif
+            return;
+        }
+    }
     constexpr int PPT = (NP + kThreads - 1) / kThreads;  // output pairs per thread
 #pragma unroll
     for (int j = 0; j < PPT; j++) {

@@ -116,10 +116,13 @@ def test_causal_prompt_rows(device, n_q, L):
     run_decode(device, 50 + n_q + L, 20, 20, 64, [L], n_q=n_q, causal=True)
 
 
+@pytest.mark.parametrize("lens", [[700, 5], [8192, 5]])
 @pytest.mark.parametrize("n_head,n_head_kv,hd", [(4, 1, 64), (7, 1, 128), (16, 1, 128), (32, 1, 64), (8, 8, 128)])
-def test_group_sizes(device, n_head, n_head_kv, hd):
-    # 1..32 query heads per kv head: row tiles of 4, 8 and 16 rows, and several tiles
-    run_decode(device, 60 + n_head, n_head, n_head_kv, hd, [700, 5])
+def test_group_sizes(device, n_head, n_head_kv, hd, lens):
+    # 1..32 query heads per kv head: row tiles of 4, 8 and 16 rows, and several tiles; 8192 keys make 32 splits of 256
+    # keys on 8-wave workgroups (at head dim 128 the merge that stripes the splits over the threads), 700 keys 6 (the
+    # per-pair merge)
+    run_decode(device, 60 + n_head + lens[0], n_head, n_head_kv, hd, lens)
 
 
 def test_causal_gqa_multi_rowtile(device):
@@ -228,6 +231,12 @@ def test_f32_whisper_prompt_rows(device):
 
 def test_f32_llama3_8b_batch3(device):
     run_decode_f32(device, 43, 32, 8, 128, [1, 700, 5000], check_heads=[0, 13, 31])
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd,n_q", [(14, 2, 64, 1), (20, 20, 64, 5), (32, 8, 128, 4)])
+def test_f32_many_splits(device, n_head, n_head_kv, hd, n_q):
+    # 32 splits per tile on the f32 entry point (row tiles of 4, 8 and 16 rows; at head dim 128 the striped merge)
+    run_decode_f32(device, 44 + n_q, n_head, n_head_kv, hd, [8192], n_q=n_q)
 
 
 @pytest.mark.parametrize("waves", [4, 8])
