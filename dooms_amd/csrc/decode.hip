@@ -317,14 +317,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
             for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, xq[ks]);
         }
     }
-    // f16 query rows: loaded by every lane (rows past the tile read the problem's first row, a valid address) and zeroed
-    // only after the first block's loads are out; a conditional load here would make the compiler drain it first
+    // f16 query rows: loaded unconditionally behind the first block of keys and values (below); a conditional load
+    // would make the compiler drain it before the block's loads
     u32x4 qv[F32 ? 1 : KS];
-    if constexpr (!F32) {
-        const half_t * qrow = qp + (seq_row0 + (srow_ok ? st : 0)) * q_stride + (int64_t)(srow_ok ? sh : g * G) * HD;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) qv[ks] = load16(qrow + 32 * ks + 8 * sgrp);
-    }
+    const half_t * qrow = qp + (seq_row0 + (srow_ok ? st : 0)) * q_stride + (int64_t)(srow_ok ? sh : g * G) * HD;
 
     // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
     const int jb_new = (L - 1) & ~(kBlockKeys - 1);
@@ -354,12 +350,15 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     int jb = j0 + kBlockKeys * wave;
     B cur, nxt;
     load_block(jb, cur);
+    // f16 query rows: loaded by every lane (rows past the tile read the problem's first row, a valid address) behind the
+    // first block and zeroed where they are first used, in the walk behind the next block's prefetch. All the waves of
+    // a kv head's splits read the same query bytes; behind the keys and values that read no longer holds back their
+    // stream (loads return in order): batch 16 56.8 -> 55.7 us, the short shapes within +-0.1 us.
     if constexpr (!F32) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            asm volatile("" : "+v"(qv[ks])::"memory");  // used from here on, behind the block's loads
-            qb[ks] = as_half8(srow_ok ? qv[ks] : u32x4{0u, 0u, 0u, 0u});
-        }
+        for (int ks = 0; ks < KS; ks++) qv[ks] = load16(qrow + 32 * ks + 8 * sgrp);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (F32) {
         // the new key and value are used only from here on, so any wait for them leaves the block's loads in flight
@@ -410,9 +409,20 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     half_t * vw = s_v[wave];
     const int v_rd = (4 * sgrp + (lane % 16) / 4) * VP + 4 * (lane % 4);
 
+    bool q_pending = !F32;
     for (; jb < j1; jb += kBlockKeys * NW) {
         const int jn = jb + kBlockKeys * NW;
         if (jn < j1) load_block(jn, nxt);
+        if constexpr (!F32) {
+            if (q_pending) {  // the first block: the query operand, its wait leaving the next block in flight
+                q_pending = false;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    asm volatile("" : "+v"(qv[ks])::"memory");
+                    qb[ks] = as_half8(srow_ok ? qv[ks] : u32x4{0u, 0u, 0u, 0u});
+                }
+            }
+        }
         if constexpr (F32) {
             if (wave_new && jb == jb_new) {  // the new key and value replace what the cache held at L - 1
                 const int mt_new = ((L - 1) % kBlockKeys) / 16, i_new = ((L - 1) % kBlockKeys) / KPL;
