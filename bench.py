@@ -425,12 +425,14 @@ def trace_decode(args):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
     workloads = [("cfg3 Llama-3-8B batch 1, 8192 keys", 32, 8, 128, [8192], 1, 32),
+                 ("cfg3 fused step (mx_attn_decode_rope), batch 1, 8192 keys", 32, 8, 128, [8192], 0, 32),
                  ("cfg1 Qwen2.5-0.5B, 513 keys", 14, 2, 64, [513], 1, 32),
                  ("cfg4 Whisper cross-attention, 1500 frames, greedy", 20, 20, 64, [1500], 1, 32),
                  ("cfg4 Whisper self-attention, 449 keys", 20, 20, 64, [449], 1, 32)]
     names = ["wave walk done", "waves merged", "partial published", "split counted", "splits merged"]
     for name, nh, nkv, hd, lens, nq, layers in workloads:
-        prob = DecodeProblem(torch, gen, nh, nkv, hd, lens, layers, n_q=nq)
+        # n_q 0 marks the fused step on the reference's f32 q|k|v rows (adjacent-pair rotary, base 500000)
+        prob = DecodeProblem(torch, gen, nh, nkv, hd, lens, layers, n_q=max(nq, 1), rope=(0, 500000.0) if nq == 0 else None)
         ms, _ = time_graph(torch, prob.step, args.steps, args.warmup)
         buf = np.zeros(8192 * 16, dtype=np.uint64)
         assert L.mx_attn_trace_read(buf.ctypes.data, buf.nbytes) == 0
