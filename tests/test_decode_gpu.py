@@ -67,6 +67,13 @@ def test_llama3_8b_decode_8192(device):
     run_decode(device, 3, 32, 8, 128, [8192])  # every head
 
 
+@pytest.mark.parametrize("n_head,n_head_kv,n_q,causal", [(32, 8, 16, True), (16, 16, 1, False)])
+def test_one_sequence_heads_per_xcd(device, n_head, n_head_kv, n_q, causal):
+    # one sequence with a multiple of 8 kv heads: kv head g's splits run on XCD g % 8; 16 causal rows make 4 row tiles
+    # per kv head, 16 kv heads two heads per XCD (8192 keys: 32 splits of 256 keys)
+    run_decode(device, 77 + n_q, n_head, n_head_kv, 128, [8192], n_q=n_q, causal=causal)
+
+
 def test_llama3_8b_decode_128k(device):
     # a 131072-token context: 32 splits of 4096 keys per kv head, each wave walking 16 blocks before the merge
     run_decode(device, 76, 32, 8, 128, [131072], check_heads=[0, 9, 31])
