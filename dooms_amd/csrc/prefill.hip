@@ -9,10 +9,12 @@
 //   * One workgroup = 8 waves = 256 query rows of one query head (4 waves = 128 rows for short prompts); each wave owns
 //     32 rows. When even those would leave most CUs idle, two waves share a 32-row tile and split its key blocks. The register budget is held to 256 per lane, so each SIMD interleaves two waves: one wave's softmax runs
 //     on the vector ALU while the other's products run on the matrix core; all waves of a CU share each K/V tile.
-//   * Key/value blocks of 64 rows pass through LDS, double-buffered: block i + 1 goes from registers into the free LDS
-//     buffer and block i + 2 is loaded from HBM/L2 into registers while block i is multiplied; one barrier per block.
-//     Both tiles are stored row-major with padded rows, so the K reads below and the transposing V reads are free of
-//     bank conflicts and address with compile-time offsets.
+//   * Key/value blocks of 64 rows pass through LDS. The 8-wave head-dim-128 plan on f16 operands loads them straight
+//     into LDS (global_load_lds_dwordx4) into three buffers, two steps ahead, as 1 KB blocks of 16 rows x 64 bytes with
+//     a bank swizzle chosen by which bytes each lane fetches; the other plans double-buffer: block i + 1 goes from
+//     registers into the free LDS buffer and block i + 2 is loaded into registers while block i is multiplied, in
+//     row-major tiles with padded rows. Either way the K reads and the transposing V reads are free of bank conflicts
+//     and address with per-lane bases plus compile-time offsets; one barrier per block.
 //   * Transposed scores: S^T (keys x queries) = K Q^T on v_mfma_f32_32x32x16_f16. In the result each lane holds 16 keys
 //     of ONE query (the lane 32 away the other 16), so the row max and sum need one cross-lane step, and the
 //     probabilities already sit in the B-operand layout of O^T += V^T P^T: P never touches LDS. Q^T is loaded once into
@@ -26,12 +28,23 @@
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
+#include <type_traits>
+
 
 namespace mx {
 
 namespace {
 
 constexpr int kBK = 64;  // keys per block
+
+// f(std::integral_constant<int, i>) for i = B .. E - 1, each i a compile-time constant (immediate operands of inline asm)
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F && f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef half_t half2_t __attribute__((ext_vector_type(2)));
@@ -51,12 +64,31 @@ __device__ __forceinline__ float get_f32(const float * a) {
 // 32 bytes that each 16-lane group reads through the transposing read, for both groups of a 32-lane phase, land on 64
 // distinct banks; the tile store writes 4 rows x 4 chunks per 16 lanes, also 16 distinct 4-bank groups). Every read
 // address is a per-lane base plus a compile-time offset, so the loop spends no ALU on addressing.
-template <int HD, int KSP>
+template <int HD, int KSP, bool DL = false>
 struct PrefillSmem {
     static constexpr int KP = HD + 8;
     static constexpr int VP = HD + 32;
     half_t k[2][KSP * kBK * KP];
     half_t v[2][KSP * kBK * VP];
+};
+
+// Direct-to-LDS tiles (DL: the 8-wave, head-dim-128 plan on f16 operands). global_load_lds_dwordx4 writes the 16 bytes
+// of lane l to LDS byte 16 l of the instruction's 1 KB destination, so a tile is a grid of 1 KB blocks, each one
+// instruction: block (cb, rb) = 4 cb + rb holds rows 16 rb .. + 16 x 16-byte chunks 4 cb .. + 4 (64 contiguous bytes of
+// each row in memory), row r % 16 at block byte 64 (r % 16). Which chunk a lane fetches sets the bank spread:
+//   K: chunk c of row r sits at 16 ((c % 4) ^ ((r % 16) / 4)) in its row's 64 bytes: the 16-byte reads of 16
+//      consecutive rows at one chunk land on 16 distinct 4-bank groups, and the swizzle leaves the compile-time part of
+//      a read's chunk index (its 32-byte half) additive: two per-lane bases, the rest instruction offsets;
+//   V: no swizzle: each 32-lane phase of the transposing read takes 4 consecutive rows x 64 bytes, 256 contiguous bytes.
+// Three buffers: the loads of step i + 2 go out while step i is multiplied, with no registers in between.
+constexpr int kDLBuf = 3;  // a fourth buffer (three steps ahead) measured the same
+template <int HD, int W, int KSP, int SA>
+constexpr bool prefill_dl() { return HD == 128 && W == 8 && KSP == 1 && SA == 0; }
+
+template <int HD, int KSP>
+struct PrefillSmem<HD, KSP, true> {
+    half_t k[kDLBuf][KSP * kBK * HD];
+    half_t v[kDLBuf][KSP * kBK * HD];
 };
 
 // Work order of the prefill grid (o = 0 .. n_qtiles * n_head - 1), cut by xcd_remap into one contiguous range per XCD:
@@ -109,8 +141,9 @@ struct SkSegment {
 };
 
 template <int HD, bool POS, int W, bool ROPE, int KSP, int SA, bool SK>
-__device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSmem<HD, KSP> & sm, int kvh, int gi, int qt,
-                                             const SkSegment & seg) {
+__device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>()> & sm,
+                                             int kvh, int gi, int qt, const SkSegment & seg) {
+    constexpr bool DL = prefill_dl<HD, W, KSP, SA>();
     constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
     static_assert(W % KSP == 0, "whole row tiles");
     static_assert(!(ROPE && SA), "the rotated prompt path reads f16 operands");
@@ -124,7 +157,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     constexpr int NB = (KB / 16) * (C8 / 4);  // (16 keys x 4 chunks) load blocks per step
     constexpr int NI = NB / kWaves;      // loads per thread per step, for each of K and V
     static_assert(NB % kWaves == 0, "whole loads per thread");
-    constexpr int KP = PrefillSmem<HD, KSP>::KP, VP = PrefillSmem<HD, KSP>::VP;
+    constexpr int KP = PrefillSmem<HD, KSP>::KP, VP = PrefillSmem<HD, KSP>::VP;  // padded row pitches (not DL)
 
     const int G = p.group;
     const int h = kvh * G + gi;
@@ -186,6 +219,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     auto vrow = [&](int b) { return 16 * (b % (KB / 16)) + 4 * (lane / 16) + (lane % 16) / 4; };
     auto vchunk = [&](int b) { return 4 * (b / (KB / 16)) + lane % 4; };
     auto load_tile_into = [&](int kb, u32x4 (&kr)[NI][NR], u32x4 (&vr)[NI][NR]) __attribute__((always_inline)) {
+        if constexpr (DL) return;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
@@ -196,11 +230,30 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     };
     auto load_tile = [&](int kb) __attribute__((always_inline)) { load_tile_into(kb, kreg, vreg); };
     auto store_tile = [&](int buf) {
+        if constexpr (DL) return;  // the DL plan has no register staging
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int b = i * kWaves + wave;
             *reinterpret_cast<u32x4 *>(&sm.k[buf][krow(b) * KP + 8 * kchunk(b)]) = half8(kreg[i], 8 * kchunk(b));
             *reinterpret_cast<u32x4 *>(&sm.v[buf][vrow(b) * VP + 8 * vchunk(b)]) = half8(vreg[i], 8 * vchunk(b));
+        }
+    };
+
+    // DL: step kb's K and V tiles straight into LDS buffer buf, instruction j = i W + wave filling block j
+    auto issue_tile = [&](int kb, int buf) __attribute__((always_inline)) {
+        if constexpr (DL) {
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int j = i * kWaves + wave, rb = j % 4, cb = j / 4;  // this instruction's block
+                const int row = 16 * rb + lane / 4;                         // the row this lane fills
+                const int key = min(kb + row, p.n_kv - 1);
+                const int ck = 4 * cb + ((lane % 4) ^ (lane / 16)), cv = 4 * cb + lane % 4;
+                const char * kr = kg + (int64_t)key * p.kv_stride * 2, * vr = vg + (int64_t)key * p.kv_stride * 2;
+                __builtin_amdgcn_global_load_lds(kr + 16 * ck, (__attribute__((address_space(3))) void *)&sm.k[buf][512 * j],
+                                                 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vr + 16 * cv, (__attribute__((address_space(3))) void *)&sm.v[buf][512 * j],
+                                                 16, 0, 0);
+            }
         }
     };
 
@@ -249,7 +302,20 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) ld8(qp, 16 * ks + 8 * hgrp, qr[ks]);
     }
-    if (nb > 0 && W == 4) {
+    if constexpr (DL) {
+        // the query went out first; steps 0 and 1 follow straight into LDS (the wait for the query leaves them in flight)
+        if (nb > 0) issue_tile(ib0 * KB, 0);
+#pragma unroll
+        for (int a = 1; a < kDLBuf - 1; a++)
+            if (nb > a) issue_tile((ib0 + a) * KB, a);
+        if constexpr (!ROPE) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int j = 0; j < NR; j++) asm volatile("" : "+v"(qr[ks][j])::"memory");
+        }
+        q_operand();
+    } else if (nb > 0 && W == 4) {
         // the short-prompt plans: steps 0 and 1 go out together (step 1 into registers of its own, unconditionally:
         // past the cache its rows are clamped to the last one and never used), so the prologue waits for one round
         // trip instead of two (the 8-wave plan's long chunks keep the plain order)
@@ -290,7 +356,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     // Wait here for the query operand (and the prologue's loads): inside the loop the only loads in flight are then the
     // prefetch of a later block, whose registers the block's math does not read, so no wait inside the loop has to
     // drain them (a wait the compiler would otherwise place before the first product, serializing loads and math).
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if (!DL) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
     float16_t o[DT];
 #pragma unroll
@@ -304,19 +370,39 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     // transposing read: lane a of 16-lane group c supplies V[4 hgrp + a / 4][16 (c % 2) + 4 (a % 4)] (+ 16 u + 8 s8 rows,
     // + 32 dt columns) and receives V[rows + 0..3][32 dt + lane % 32]
     const int v_base = (4 * hgrp + (lane % 16) / 4) * VP + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
+    // DL read bases (halves): K chunk 2 kk + hgrp of row l32 in block (kk / 2, l32 / 16), one base per kk % 2; V as the
+    // padded read with 64-byte rows
+    int dl_k[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++) dl_k[b] = 512 * (l32 / 16) + 32 * (l32 % 16) + 8 * ((2 * b + hgrp) ^ ((l32 % 16) / 4));
+    const int dl_v = (4 * hgrp + (lane % 16) / 4) * 32 + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
 
     for (int jb = 0; jb < nb; jb++) {
         const int ib = ib0 + jb;
         const int kb = ib * KB + kh * kBK;  // this wave's block of the step
-        const int buf = jb & 1;
-        __syncthreads();  // step ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
-        if (jb + 1 < nb) {
-            store_tile(buf ^ 1);
-            if (jb + 2 < nb) load_tile((ib + 2) * KB);
+        int buf;
+        if constexpr (DL) {
+            buf = jb % kDLBuf;
+            // this wave's loads of step ib are complete (those of step ib + 1 may still be in flight), then every
+            // wave's are: step ib is in buffer `buf`, and buffer (jb + 2) % 3 was last read in the previous step
+            static_assert(kDLBuf == 3, "the waits below keep one later step in flight");
+            if (jb + 1 < nb) __builtin_amdgcn_s_waitcnt(0x0F70 | NI * 2);          // vmcnt(2 NI)
+            else __builtin_amdgcn_s_waitcnt(0x0F70);                                     // vmcnt(0)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (jb + kDLBuf - 1 < nb) issue_tile((ib + kDLBuf - 1) * KB, (jb + kDLBuf - 1) % kDLBuf);
+        } else {
+            buf = jb & 1;
+            __syncthreads();  // step ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
+            if (jb + 1 < nb) {
+                store_tile(buf ^ 1);
+                if (jb + 2 < nb) load_tile((ib + 2) * KB);
+            }
         }
         if (kb >= kend || (p.causal && kb > wave_last)) continue;  // every key of the block is past this wave's rows
-        const half_t * ks_ = sm.k[buf] + kh * kBK * KP;
-        const half_t * vs_ = sm.v[buf] + kh * kBK * VP;
+        const half_t * ks_ = DL ? sm.k[buf] : sm.k[buf] + kh * kBK * KP;
+        const half_t * vs_ = DL ? sm.v[buf] : sm.v[buf] + kh * kBK * VP;
 
         // S^T = K Q^T: 2 tiles of 32 keys. The K operand of step i + 1 is read before the product of step i, so each
         // product waits only for reads issued one product earlier.
@@ -327,6 +413,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
             constexpr int RA = 1;  // reads in flight ahead of the product (2 or 3 measured no faster)
             u32x4 ka[RA + 1];
             auto kread = [&](int i) {
+                if constexpr (DL)  // K[32 mt + l32][16 kk + 8 hgrp]: block (kk / 2, 2 mt + l32 / 16)
+                    return *reinterpret_cast<const u32x4 *>(ks_ + dl_k[(i / 2) % 2] + 2048 * (i / 4) + 1024 * (i % 2));
                 return *reinterpret_cast<const u32x4 *>(ks_ + k_base + 32 * (i % 2) * KP + 16 * (i / 2));
             };
 #pragma unroll
@@ -397,9 +485,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
             auto vread = [&](int i, short4_t (&t)[2]) {
                 const int u = i / DT, dt = i % DT;
 #pragma unroll
-                for (int s8 = 0; s8 < 2; s8++)
-                    t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)(
-                        vs_ + v_base + (16 * u + 8 * s8) * VP + 32 * dt));
+                for (int s8 = 0; s8 < 2; s8++) {
+                    const half_t * a = vs_ + v_base + (16 * u + 8 * s8) * VP + 32 * dt;
+                    t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)a);
+                }
             };
             half8_t pb[4];
 #pragma unroll
@@ -414,14 +503,40 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                 for (int e = 0; e < 8; e += 2)
                     bsum = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, bsum, false);
             l_run = l_run * corr + bsum;
-            vread(0, vt[0]);
-#pragma unroll
-            for (int i = 0; i < NP; i++) {
-                if (i + 1 < NP) vread(i + 1, vt[(i + 1) & 1]);
-                const short4_t lo = vt[i & 1][0], hi = vt[i & 1][1];
+            auto pv = [&](int i, const short4_t (&t)[2]) __attribute__((always_inline)) {
+                const short4_t lo = t[0], hi = t[1];
                 const half8_t a = __builtin_bit_cast(half8_t, (short __attribute__((ext_vector_type(8)))){
                     lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
                 o[i % DT] = mfma32x32x16(a, pb[i / DT], o[i % DT]);
+            };
+            if constexpr (DL) {
+                // The transposing reads as inline asm with their own waits: the compiler cannot tell the intrinsic's
+                // LDS read from the direct loads still writing another buffer, and would drain them (vmcnt(0)) before
+                // the first read of every block. Rows 16 u + 8 s8 + 4 hgrp + (lane % 16) / 4 of block (dt, u).
+                const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)vs_ + 2 * dl_v;
+                static_for<0, NP + 1>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value;
+                    if constexpr (i < NP) {
+                        constexpr int off = 2 * (512 * (4 * (i % DT) + i / DT));
+                        asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                                     : "=&v"(vt[i & 1][0]), "=&v"(vt[i & 1][1])
+                                     : "v"(va), "i"(off), "i"(off + 512));
+                    }
+                    if constexpr (i > 0) {  // product i - 1: its two reads done, product i's may be in flight
+                        if constexpr (i < NP)
+                            asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(vt[(i - 1) & 1][0]), "+v"(vt[(i - 1) & 1][1]));
+                        else
+                            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[(i - 1) & 1][0]), "+v"(vt[(i - 1) & 1][1]));
+                        pv(i - 1, vt[(i - 1) & 1]);
+                    }
+                });
+            } else {
+                vread(0, vt[0]);
+#pragma unroll
+                for (int i = 0; i < NP; i++) {
+                    if (i + 1 < NP) vread(i + 1, vt[(i + 1) & 1]);
+                    pv(i, vt[i & 1]);
+                }
             }
         }
     }
@@ -566,7 +681,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
 template <int HD, bool POS, int W, bool ROPE, int KSP, int SA>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 && HD <= 128 ? 2 : 1, KSP == 1 && HD <= 128 ? 2 : 1)))
 void prefill_kernel(PrefillParams p) {
-    __shared__ PrefillSmem<HD, KSP> sm;
+    __shared__ PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>()> sm;
     // ---- work item: each XCD a contiguous range of a kv-head-major order, heavy query tiles first ----
     const uint32_t n_work = (uint32_t)p.n_qtiles * p.n_head;
     int kvh, gi, qt_order;
@@ -583,7 +698,7 @@ void prefill_kernel(PrefillParams p) {
 template <int HD, bool POS, bool ROPE>
 __global__ __launch_bounds__(8 * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_sk_kernel(PrefillParams p) {
-    __shared__ PrefillSmem<HD, 1> sm;
+    __shared__ PrefillSmem<HD, 1, prefill_dl<HD, 8, 1, 0>()> sm;
     const int32_t R = p.sk_ranges;
     const int32_t r = (int32_t)(blockIdx.x % 8) * (R / 8) + (int32_t)(blockIdx.x / 8);
     const int64_t total = p.sk_total, lo = sk_lo(total, R, r), hi = sk_lo(total, R, r + 1);
