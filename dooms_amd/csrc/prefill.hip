@@ -166,7 +166,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     const int64_t bq = blockIdx.y * p.q_batch, bkv = blockIdx.y * p.kv_batch, bo = blockIdx.y * p.out_batch;
     float * const lse_g = p.lse ? p.lse + blockIdx.y * p.lse_batch : nullptr;
 
-    const int wave = threadIdx.x / kWave;  // wave-uniform, in a scalar register
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform, in a scalar register
     const int rt = wave % RPW, kh = wave / RPW;  // the wave's row tile and its block of each step
     const int lane = threadIdx.x % kWave;
     const int l32 = lane % 32, hgrp = lane / 32;
@@ -240,18 +240,37 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     };
 
     // DL: step kb's K and V tiles straight into LDS buffer buf, instruction j = i W + wave filling block j
+    // Each lane's source bytes relative to the step's first key row are fixed for the kernel: 32-bit offsets from a
+    // uniform step base (the loads' scalar-base form, no per-load address arithmetic); only a step that runs past the
+    // cache clamps its rows to the last one.
+    uint32_t dl_ko[DL ? NI : 1], dl_vo[DL ? NI : 1];
+    int dl_row[DL ? NI : 1];
+    const uint32_t row_bytes = (uint32_t)p.kv_stride * 2;
+    if constexpr (DL) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int j = i * kWaves + wave, rb = j % 4, cb = j / 4;  // this instruction's block
+            dl_row[i] = 16 * rb + lane / 4;                             // the row this lane fills
+            dl_ko[i] = dl_row[i] * row_bytes + 16 * (4 * cb + ((lane % 4) ^ (lane / 16)));
+            dl_vo[i] = dl_row[i] * row_bytes + 16 * (4 * cb + lane % 4);
+        }
+    }
     auto issue_tile = [&](int kb, int buf) __attribute__((always_inline)) {
         if constexpr (DL) {
+            const char * kst = kg + (int64_t)kb * row_bytes, * vst = vg + (int64_t)kb * row_bytes;
+            const bool partial = kb + KB > p.n_kv;
 #pragma unroll
             for (int i = 0; i < NI; i++) {
-                const int j = i * kWaves + wave, rb = j % 4, cb = j / 4;  // this instruction's block
-                const int row = 16 * rb + lane / 4;                         // the row this lane fills
-                const int key = min(kb + row, p.n_kv - 1);
-                const int ck = 4 * cb + ((lane % 4) ^ (lane / 16)), cv = 4 * cb + lane % 4;
-                const char * kr = kg + (int64_t)key * p.kv_stride * 2, * vr = vg + (int64_t)key * p.kv_stride * 2;
-                __builtin_amdgcn_global_load_lds(kr + 16 * ck, (__attribute__((address_space(3))) void *)&sm.k[buf][512 * j],
+                const int j = i * kWaves + wave;
+                uint32_t ko = dl_ko[i], vo = dl_vo[i];
+                if (__builtin_expect(partial, 0)) {
+                    const uint32_t back = (uint32_t)max(kb + dl_row[i] - (p.n_kv - 1), 0) * row_bytes;
+                    ko -= back;
+                    vo -= back;
+                }
+                __builtin_amdgcn_global_load_lds(kst + ko, (__attribute__((address_space(3))) void *)&sm.k[buf][512 * j],
                                                  16, 0, 0);
-                __builtin_amdgcn_global_load_lds(vr + 16 * cv, (__attribute__((address_space(3))) void *)&sm.v[buf][512 * j],
+                __builtin_amdgcn_global_load_lds(vst + vo, (__attribute__((address_space(3))) void *)&sm.v[buf][512 * j],
                                                  16, 0, 0);
             }
         }
