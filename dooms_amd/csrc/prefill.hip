@@ -383,6 +383,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
 #pragma unroll
         for (int v = 0; v < 16; v++) o[dt][v] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
+    float m_thr = kNegInf, nm_use = 0.f;  // m_run + 8 (the lazy rescale's threshold) and -m_run (0 while m_run = -inf)
 
     // per-lane LDS read bases (halves); everything else is a compile-time offset
     const int k_base = l32 * KP + 8 * hgrp;  // K[32 mt + l32][16 kk + 8 hgrp]
@@ -476,24 +477,26 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
         bmax = xor32_max(bmax);
         // lazy rescale: the reference maximum moves only when the block's maximum exceeds it by more than 8 (base 2);
         // the probabilities then stay below 2^8, well inside f16, and the O rescale below is rare
-        const float m_cand = fmaxf(m_run, POS ? bmax * c : bmax);
-        const float m_new = m_cand > m_run + 8.f ? m_cand : m_run;
-        const bool none = m_new == kNegInf;       // no visible key yet in this row
-        const float m_use = none ? 0.f : m_new;   // then every exponent below is 2^-inf = 0
-        const float corr = none ? 1.f : exp2_fast(m_run - m_new);
-        m_run = m_new;
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                sc[mt][v] = exp2_fast(POS ? __builtin_fmaf(sc[mt][v], c, -m_use) : sc[mt][v] - m_use);
-            }
-        if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {  // the running max moved in some row of the wave
+        // (one compare and a ballot per block; the new maximum, the factor and the rescale of O and l only when it moves)
+        const float bm = POS ? bmax * c : bmax;
+        if (__builtin_amdgcn_ballot_w64(bm > m_thr)) {  // the running max moves in some row of the wave
+            const float m_new = bm > m_thr ? bm : m_run;
+            const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
+            m_run = m_new;
+            m_thr = m_new + 8.f;
+            nm_use = m_new == kNegInf ? 0.f : -m_new;  // no visible key yet: every exponent below is 2^-inf = 0
+            l_run *= corr;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int v = 0; v < 16; v++) o[dt][v] *= corr;
         }
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                sc[mt][v] = exp2_fast(POS ? __builtin_fmaf(sc[mt][v], c, nm_use) : sc[mt][v] + nm_use);
+            }
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
         // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V. The reads of
@@ -515,13 +518,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
 #pragma unroll
                 for (int e = 0; e < 8; e++) pb[u][e] = (half_t)sc[u / 2][8 * (u % 2) + e];
             // the row sum of the half probabilities that multiply V, on v_dot2_f32_f16 (two per instruction, f32 sum)
-            float bsum = 0.f;
 #pragma unroll
             for (int u = 0; u < 4; u++)
 #pragma unroll
                 for (int e = 0; e < 8; e += 2)
-                    bsum = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, bsum, false);
-            l_run = l_run * corr + bsum;
+                    l_run = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, l_run, false);
             auto pv = [&](int i, const short4_t (&t)[2]) __attribute__((always_inline)) {
                 const short4_t lo = t[0], hi = t[1];
                 const half8_t a = __builtin_bit_cast(half8_t, (short __attribute__((ext_vector_type(8)))){
