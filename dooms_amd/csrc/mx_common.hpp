@@ -49,9 +49,16 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
 // (v_permlane16_swap) hands lane l the value of lane l ^ 32 (l ^ 16) in one of its two results and keeps its own in the
 // other, so the max or sum of the two is the pair's in every lane (the same sum in both lanes of a pair: a + b = b + a).
 // Every lane of the wave must be active.
+// The max is one v_max_f32 in asm: fmaxf on the swap's results costs a canonicalizing v_max of each first (the
+// compiler cannot tell that they are not signaling NaNs); scores are never NaN here.
+__device__ __forceinline__ float vmax_raw(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float xor32_max(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return vmax_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_add(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -59,7 +66,7 @@ __device__ __forceinline__ float xor32_add(float v) {
 }
 __device__ __forceinline__ float xor16_max(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return vmax_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor16_add(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -432,20 +432,42 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
             // (kk, mt) order: the two key tiles' products alternate, so consecutive products are independent (cfg5 +0.8 %)
             constexpr int RA = 1;  // reads in flight ahead of the product (2 or 3 measured no faster)
             u32x4 ka[RA + 1];
+            // DL: K[32 mt + l32][16 kk + 8 hgrp] in block (kk / 2, 2 mt + l32 / 16), at dl_k[kk % 2] + the block's offset
             auto kread = [&](int i) {
-                if constexpr (DL)  // K[32 mt + l32][16 kk + 8 hgrp]: block (kk / 2, 2 mt + l32 / 16)
-                    return *reinterpret_cast<const u32x4 *>(ks_ + dl_k[(i / 2) % 2] + 2048 * (i / 4) + 1024 * (i % 2));
                 return *reinterpret_cast<const u32x4 *>(ks_ + k_base + 32 * (i % 2) * KP + 16 * (i / 2));
             };
 #pragma unroll
             for (int v = 0; v < 16; v++) sc[0][v] = sc[1][v] = 0.f;
+            u32x4 kf[DL ? NS : 1];
+            const uint32_t kb0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ks_;
+            const uint32_t ka0 = kb0 + 2 * dl_k[0], ka1 = kb0 + 2 * dl_k[1];
+            if constexpr (DL) {
+                // every K fragment of the block in flight at once (inline asm, as the V reads below), each product
+                // waiting for its own: LDS reads complete in order, so product i needs lgkmcnt(NS - 1 - i)
+                static_assert(NS <= 16, "lgkmcnt counts at most 15 later reads");
+                static_for<0, NS>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value;
+                    constexpr int off = 2 * (2048 * (i / 4) + 1024 * (i % 2));
+                    const uint32_t a = (i / 2) % 2 ? ka1 : ka0;
+                    u32x4 t;
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(t) : "v"(a), "i"(off));
+                    kf[i] = t;
+                });
+                static_for<0, NS>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value;
+                    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(kf[i]) : "i"(NS - 1 - i));
+                    sc[i % 2] = mfma32x32x16(as_half8(kf[i]), qb[i / 2], sc[i % 2]);
+                    __builtin_amdgcn_sched_barrier(0);  // each product right behind its wait
+                });
+            } else {
 #pragma unroll
-            for (int i = 0; i < RA; i++) ka[i] = kread(i);
+                for (int i = 0; i < RA; i++) ka[i] = kread(i);
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                if (i + RA < NS) ka[(i + RA) % (RA + 1)] = kread(i + RA);
-                const int mt = i % 2, kk = i / 2;
-                sc[mt] = mfma32x32x16(as_half8(ka[i % (RA + 1)]), qb[kk], sc[mt]);
+                for (int i = 0; i < NS; i++) {
+                    if (i + RA < NS) ka[(i + RA) % (RA + 1)] = kread(i + RA);
+                    const int mt = i % 2, kk = i / 2;
+                    sc[mt] = mfma32x32x16(as_half8(ka[i % (RA + 1)]), qb[kk], sc[mt]);
+                }
             }
         }
         // block max (raw scores when the scale is positive); the mask only where a block crosses the diagonal or the
