@@ -420,6 +420,142 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
         }
 }
 
+// ---- M > 8, large products: 256 x 256 tiles of 8 waves (each 128 x 64, 4 x 2 MFMA tiles), K in steps of 32 ----
+// A 128 x 128 tile streams 64 bytes per clock and CU from L2 at the MFMA rate, the whole of an XCD's L2 bandwidth;
+// 256 x 256 halves the bytes per product (and 128 x 64 per wave cuts the LDS reads per product by a quarter). The
+// tiles go from HBM/L2 straight into LDS (global_load_lds_dwordx4: lane l's 16 bytes land at byte 16 l of the
+// instruction's 1 KB destination), three buffers deep (the loads of step s + 2 in flight while step s multiplies), no
+// registers in between. An operand tile (256 rows x 32 columns, 64 bytes per row) is 16 blocks of 16 rows, one load
+// instruction each; 16-byte chunk c of row r sits at 16 (c ^ ((r % 16) / 4)) within its row's 64 bytes, so the 16-byte
+// operand reads of 16 consecutive rows at one chunk land on 16 distinct 4-bank groups. 96 KB of LDS: one workgroup per
+// CU, two waves per SIMD.
+constexpr int kBM = 256, kBN = 256, kBK = 32;
+constexpr int kGemmCUs = 256;
+constexpr int kBigWaves = 8, kBigThreads = kBigWaves * kWave;
+constexpr int kBigBufs = 3;
+constexpr int kBigTile = kBM * kBK;                            // halves of one operand tile of one step
+constexpr int kBigLoads = kBM * kBK * 2 / 1024 / kBigWaves;    // 1 KB direct loads per wave, operand and step (2)
+constexpr int kBigMI = 4, kBigNJ = 2;                          // 32 x 32 MFMA tiles per wave: 128 rows x 64 columns
+
+template <bool OUT16>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p) {
+    __shared__ __attribute__((aligned(1024))) half_t xs[kBigBufs][kBigTile];
+    __shared__ __attribute__((aligned(1024))) half_t ws[kBigBufs][kBigTile];
+    const int n_tiles = (p.N + kBN - 1) / kBN, m_tiles = (p.M + kBM - 1) / kBM;
+    // consecutive work items share a weight tile (different token tiles); contiguous ranges per XCD
+    const uint32_t t = xcd_remap(blockIdx.x, (uint32_t)(p.count * n_tiles * m_tiles));
+    const int mt = t % m_tiles, nt = (t / m_tiles) % n_tiles, mi = t / (m_tiles * n_tiles);
+    const int m0 = mt * kBM, n0 = nt * kBN;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+    const int l32 = lane % 32, hi = lane / 32;
+
+    // Each lane's source bytes relative to the step's first column are fixed: rows past M (N) repeat the last row.
+    // The staged rows are kp halves apart (K rounded up to 64, zero-padded); the weight rows K halves apart.
+    const int kp = (p.K + 63) / 64 * 64;
+    const char * a_base = reinterpret_cast<const char *>(p.xh + (int64_t)m0 * kp);
+    const char * b_base = reinterpret_cast<const char *>(p.w[mi] + (int64_t)n0 * p.K);
+    uint32_t a_off[kBigLoads], b_off[kBigLoads];
+#pragma unroll
+    for (int i = 0; i < kBigLoads; i++) {
+        const int j = i * kBigWaves + wave;      // the block this instruction fills
+        const int row = 16 * j + lane / 4;       // the row this lane fills
+        const int c = (lane % 4) ^ (lane / 16);  // the chunk it fetches for position lane % 4
+        a_off[i] = (uint32_t)(min(m0 + row, p.M - 1) - m0) * kp * 2 + 16 * c;
+        b_off[i] = (uint32_t)(min(n0 + row, p.N - 1) - n0) * p.K * 2 + 16 * c;
+    }
+    auto issue = [&](int step, int buf) __attribute__((always_inline)) {
+        const int64_t k0 = (int64_t)step * kBK * 2;  // bytes
+#pragma unroll
+        for (int i = 0; i < kBigLoads; i++) {
+            const int j = i * kBigWaves + wave;
+            __builtin_amdgcn_global_load_lds(a_base + k0 + a_off[i],
+                                             (__attribute__((address_space(3))) void *)&xs[buf][512 * j], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(b_base + k0 + b_off[i],
+                                             (__attribute__((address_space(3))) void *)&ws[buf][512 * j], 16, 0, 0);
+        }
+    };
+
+    float16_t acc[kBigMI][kBigNJ];
+#pragma unroll
+    for (int i = 0; i < kBigMI; i++)
+#pragma unroll
+        for (int j = 0; j < kBigNJ; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+    // this wave's block: rows 128 wm + 32 i + l32 of A (blocks 8 wm + 2 i + l32 / 16), columns 64 wn + 32 j + l32 (rows
+    // of B, blocks 4 wn + 2 j + l32 / 16); fragment (row, chunk 2 ks + hi) at halves
+    // 512 (row / 16) + 32 (row % 16) + 8 ((2 ks + hi) ^ ((row % 16) / 4))
+    const int wm = wave / 4, wn = wave % 4;
+    int rd[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) rd[ks] = 512 * (l32 / 16) + 32 * (l32 % 16) + 8 * ((2 * ks + hi) ^ ((l32 % 16) / 4));
+    const int nk = p.K / kBK;
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    for (int s = 0; s < nk; s++) {
+        const int buf = s % kBigBufs;
+        // this wave's loads of step s are complete (step s + 1's may be in flight), then every wave's are; buffer
+        // (s + 2) % 3 was last read in step s - 1
+        if (s + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | 2 * kBigLoads);  // vmcnt(the next step's loads)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                              // vmcnt(0)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 2 < nk) issue(s + 2, (s + 2) % kBigBufs);
+        // the operand reads as inline asm (the compiler cannot tell them from the direct loads in flight, and would
+        // wait for those), all 12 of the step in flight, the products of each 16-column slice behind their reads
+        const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)xs[buf] + 2 * 4096 * wm;
+        const uint32_t wa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ws[buf] + 2 * 2048 * wn;
+        u32x4 fa[2][kBigMI], fb[2][kBigNJ];
+        static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
+            constexpr int ks = decltype(KS)::value;
+            const uint32_t ra_ = xa + 2 * rd[ks], rb_ = wa + 2 * rd[ks];
+            static_for<0, kBigMI>([&](auto I) __attribute__((always_inline)) {
+                constexpr int i = decltype(I)::value;
+                u32x4 r;
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(ra_), "i"(2 * 1024 * i));
+                fa[ks][i] = r;
+            });
+            static_for<0, kBigNJ>([&](auto J) __attribute__((always_inline)) {
+                constexpr int j = decltype(J)::value;
+                u32x4 r;
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(rb_), "i"(2 * 1024 * j));
+                fb[ks][j] = r;
+            });
+        });
+        static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
+            constexpr int ks = decltype(KS)::value;
+            if constexpr (ks == 0)
+                asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fa[0][2]), "+v"(fa[0][3]),
+                             "+v"(fb[0][0]), "+v"(fb[0][1]));
+            else
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fa[1][2]), "+v"(fa[1][3]),
+                             "+v"(fb[1][0]), "+v"(fb[1][1]));
+#pragma unroll
+            for (int i = 0; i < kBigMI; i++)
+#pragma unroll
+                for (int j = 0; j < kBigNJ; j++)
+                    acc[i][j] = mfma32x32x16(as_half8(fa[ks][i]), as_half8(fb[ks][j]), acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+
+    // lane holds Y[m0 + 128 wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + 64 wn + 32 j + l32]
+#pragma unroll
+    for (int i = 0; i < kBigMI; i++)
+#pragma unroll
+        for (int j = 0; j < kBigNJ; j++) {
+            const int n = n0 + 64 * wn + 32 * j + l32;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + 128 * wm + 32 * i + 8 * (v / 4) + 4 * hi + v % 4;
+                if (m < p.M) store_y<OUT16>(p, mi, m, n, acc[i][j][v]);
+            }
+        }
+}
+
 // Waves per workgroup: the (matrix, 4-row group) items spread evenly over the CUs, one workgroup per CU (the weight
 // stream of each CU then ends at the same time), up to 8 waves; beyond 2048 items, several workgroups of 8 per CU.
 template <int MT>
@@ -464,6 +600,13 @@ hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
 }
 
 hipError_t launch_gemm(const LinearParams & p, hipStream_t stream) {
+    // 256 x 256 tiles when they give at least 3/4 of the CUs a tile (one workgroup per CU); else 128 x 128 tiles
+    const int big = p.count * ((p.N + kBN - 1) / kBN) * ((p.M + kBM - 1) / kBM);
+    if (4 * big >= 3 * kGemmCUs) {
+        if (p.flags & kLinearOutF16) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
+        else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
+        return hipGetLastError();
+    }
     const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);
     const dim3 grid((uint32_t)tiles);
     if (p.flags & kLinearOutF16) hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, p);

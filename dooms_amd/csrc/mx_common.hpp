@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mx {
 
 typedef _Float16 half_t;
@@ -71,6 +73,15 @@ __device__ __forceinline__ float xor16_max(float v) {
 __device__ __forceinline__ float xor16_add(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// f(std::integral_constant<int, i>) for i = B .. E - 1, each i a compile-time constant (immediate operands of inline asm)
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F && f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
 }
 
 __device__ __forceinline__ half8_t as_half8(u32x4 v) { return __builtin_bit_cast(half8_t, v); }

@@ -37,15 +37,6 @@ namespace {
 
 constexpr int kBK = 64;  // keys per block
 
-// f(std::integral_constant<int, i>) for i = B .. E - 1, each i a compile-time constant (immediate operands of inline asm)
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F && f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef half_t half2_t __attribute__((ext_vector_type(2)));
 constexpr half2_t kOnes2 = {(half_t)1.f, (half_t)1.f};

@@ -137,6 +137,14 @@ def test_gemm_step_counts(device, M, N, K):
     run(device, 20 + K, M, N, K, norm=True, bias=True)
 
 
+def test_gemm_big_tiles_ragged(device):
+    """A product with enough 256 x 256 tiles for the large-tile GEMM: M and N not multiples of 256 (rows and
+    columns past them repeat the last one and are never stored), 5 steps of 32 columns, with the RMS normalization,
+    bias and accumulation; rows sampled across the tiles and at both edges."""
+    run(device, 10, 1300, 8300, 160, norm=True, bias=True, accumulate=True,
+        rows=[0, 1, 255, 256, 511, 700, 1023, 1024, 1279, 1280, 1299])
+
+
 def test_gemm_llama3_attn_output_chunk(device):
     run(device, 7, 300, 4096, 4096, accumulate=True, rows=[0, 1, 127, 128, 255, 299])
 
