@@ -667,17 +667,17 @@ def main():
         # ---- the projections either side of the attention (mx_linear): Llama-3-8B shapes, Whisper cross cache ----
         from dooms_amd import _lib as L
         lin = {}
-        # kernel: which code produced the figure ("gemv_kernel" / "stage_kernel + gemm_kernel": this library's, the
+        # kernel: which code produced the figure ("gemv_kernel" / "stage_kernel + gemm_*kernel": this library's, the
         # mx_linear path; "stage_kernel + hipBLASLt": an mx_linear_plan, the vendor GEMM chosen at plan creation)
         for name, M, N, Kd, flags, layers, count, plan, kernel in [
                 ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1, False, "gemv_kernel"),
                 ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1, False, "gemv_kernel"),
                 ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, False,
-                 "stage_kernel + gemm_kernel"),
+                 "stage_kernel + gemm_big_kernel"),
                 ("plan_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, True,
                  "stage_kernel + hipBLASLt (mx_linear_plan)"),
                 ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8, False,
-                 "stage_kernel + gemm_kernel")]:
+                 "stage_kernel + gemm_big_kernel")]:
             lp = LinearProblem(torch, gen, M, N, Kd, flags, layers, count, plan=plan)
             ms_l, _ = time_graph(torch, lp.step, max(5, K), max(1, W))
             us = ms_l * 1e3 / layers

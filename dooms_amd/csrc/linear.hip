@@ -429,18 +429,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
 // instruction each; 16-byte chunk c of row r sits at 16 (c ^ ((r % 16) / 4)) within its row's 64 bytes, so the 16-byte
 // operand reads of 16 consecutive rows at one chunk land on 16 distinct 4-bank groups. 96 KB of LDS: one workgroup per
 // CU, two waves per SIMD.
-constexpr int kBM = 256, kBN = 256, kBK = 32;
+// BN = 128 (256 x 128 tiles, 8 waves of 64 x 64) serves products whose 256 x 256 tiles would leave CUs idle.
+constexpr int kBM = 256, kBK = 32;
 constexpr int kGemmCUs = 256;
 constexpr int kBigWaves = 8, kBigThreads = kBigWaves * kWave;
 constexpr int kBigBufs = 3;
-constexpr int kBigTile = kBM * kBK;                            // halves of one operand tile of one step
-constexpr int kBigLoads = kBM * kBK * 2 / 1024 / kBigWaves;    // 1 KB direct loads per wave, operand and step (2)
-constexpr int kBigMI = 4, kBigNJ = 2;                          // 32 x 32 MFMA tiles per wave: 128 rows x 64 columns
+constexpr int kBigLoads = kBM * kBK * 2 / 1024 / kBigWaves;    // 1 KB direct loads of A per wave and step (2)
 
-template <bool OUT16>
-__global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p) {
-    __shared__ __attribute__((aligned(1024))) half_t xs[kBigBufs][kBigTile];
-    __shared__ __attribute__((aligned(1024))) half_t ws[kBigBufs][kBigTile];
+template <bool OUT16, int BN>
+__device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
+    constexpr int kBN = BN;
+    constexpr int WN = BN / 64, WM = kBigWaves / WN;   // waves along N (64 columns each) and along M
+    constexpr int kBigMI = kBM / WM / 32, kBigNJ = 2;  // 32 x 32 MFMA tiles per wave
+    constexpr int BLoads = BN * kBK * 2 / 1024 / kBigWaves;  // 1 KB direct loads of B per wave and step
+    static_assert(BLoads >= 1 && kBigMI >= 1, "whole loads and tiles per wave");
+    __shared__ __attribute__((aligned(1024))) half_t xs[kBigBufs][kBM * kBK];
+    __shared__ __attribute__((aligned(1024))) half_t ws[kBigBufs][BN * kBK];
     const int n_tiles = (p.N + kBN - 1) / kBN, m_tiles = (p.M + kBM - 1) / kBM;
     // consecutive work items share a weight tile (different token tiles); contiguous ranges per XCD
     const uint32_t t = xcd_remap(blockIdx.x, (uint32_t)(p.count * n_tiles * m_tiles));
@@ -454,24 +458,30 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p
     const int kp = (p.K + 63) / 64 * 64;
     const char * a_base = reinterpret_cast<const char *>(p.xh + (int64_t)m0 * kp);
     const char * b_base = reinterpret_cast<const char *>(p.w[mi] + (int64_t)n0 * p.K);
-    uint32_t a_off[kBigLoads], b_off[kBigLoads];
+    uint32_t a_off[kBigLoads], b_off[BLoads];
+    const int c = (lane % 4) ^ (lane / 16);  // the chunk a lane fetches for position lane % 4 of its row
 #pragma unroll
     for (int i = 0; i < kBigLoads; i++) {
-        const int j = i * kBigWaves + wave;      // the block this instruction fills
-        const int row = 16 * j + lane / 4;       // the row this lane fills
-        const int c = (lane % 4) ^ (lane / 16);  // the chunk it fetches for position lane % 4
+        const int row = 16 * (i * kBigWaves + wave) + lane / 4;  // the row this lane fills in block i W + wave
         a_off[i] = (uint32_t)(min(m0 + row, p.M - 1) - m0) * kp * 2 + 16 * c;
+    }
+#pragma unroll
+    for (int i = 0; i < BLoads; i++) {
+        const int row = 16 * (i * kBigWaves + wave) + lane / 4;
         b_off[i] = (uint32_t)(min(n0 + row, p.N - 1) - n0) * p.K * 2 + 16 * c;
     }
     auto issue = [&](int step, int buf) __attribute__((always_inline)) {
         const int64_t k0 = (int64_t)step * kBK * 2;  // bytes
+        // A and B loads interleaved
 #pragma unroll
         for (int i = 0; i < kBigLoads; i++) {
-            const int j = i * kBigWaves + wave;
             __builtin_amdgcn_global_load_lds(a_base + k0 + a_off[i],
-                                             (__attribute__((address_space(3))) void *)&xs[buf][512 * j], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(b_base + k0 + b_off[i],
-                                             (__attribute__((address_space(3))) void *)&ws[buf][512 * j], 16, 0, 0);
+                                             (__attribute__((address_space(3))) void *)&xs[buf][512 * (i * kBigWaves + wave)],
+                                             16, 0, 0);
+            if (i < BLoads)
+                __builtin_amdgcn_global_load_lds(b_base + k0 + b_off[i],
+                                                 (__attribute__((address_space(3))) void *)&ws[buf][512 * (i * kBigWaves + wave)],
+                                                 16, 0, 0);
         }
     };
 
@@ -483,10 +493,9 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
 
-    // this wave's block: rows 128 wm + 32 i + l32 of A (blocks 8 wm + 2 i + l32 / 16), columns 64 wn + 32 j + l32 (rows
-    // of B, blocks 4 wn + 2 j + l32 / 16); fragment (row, chunk 2 ks + hi) at halves
-    // 512 (row / 16) + 32 (row % 16) + 8 ((2 ks + hi) ^ ((row % 16) / 4))
-    const int wm = wave / 4, wn = wave % 4;
+    // this wave's block: rows (256 / WM) wm + 32 i + l32 of A, columns 64 wn + 32 j + l32 (rows of B); fragment
+    // (row, chunk 2 ks + hi) at halves 512 (row / 16) + 32 (row % 16) + 8 ((2 ks + hi) ^ ((row % 16) / 4))
+    const int wm = wave / WN, wn = wave % WN;
     int rd[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) rd[ks] = 512 * (l32 / 16) + 32 * (l32 % 16) + 8 * ((2 * ks + hi) ^ ((l32 % 16) / 4));
@@ -497,15 +506,15 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p
         const int buf = s % kBigBufs;
         // this wave's loads of step s are complete (step s + 1's may be in flight), then every wave's are; buffer
         // (s + 2) % 3 was last read in step s - 1
-        if (s + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | 2 * kBigLoads);  // vmcnt(the next step's loads)
+        if (s + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | (kBigLoads + BLoads));  // vmcnt(the next step's loads)
         else __builtin_amdgcn_s_waitcnt(0x0F70);                              // vmcnt(0)
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (s + 2 < nk) issue(s + 2, (s + 2) % kBigBufs);
         // the operand reads as inline asm (the compiler cannot tell them from the direct loads in flight, and would
-        // wait for those), all 12 of the step in flight, the products of each 16-column slice behind their reads
-        const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)xs[buf] + 2 * 4096 * wm;
+        // wait for those), all of the step's in flight, the products of each 16-column slice behind their reads
+        const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)xs[buf] + 2 * 32 * (kBM / WM) * wm;
         const uint32_t wa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ws[buf] + 2 * 2048 * wn;
         u32x4 fa[2][kBigMI], fb[2][kBigNJ];
         static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
@@ -526,12 +535,22 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p
         });
         static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
             constexpr int ks = decltype(KS)::value;
-            if constexpr (ks == 0)
-                asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fa[0][2]), "+v"(fa[0][3]),
-                             "+v"(fb[0][0]), "+v"(fb[0][1]));
-            else
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fa[1][2]), "+v"(fa[1][3]),
-                             "+v"(fb[1][0]), "+v"(fb[1][1]));
+            // slice 0 waits for its reads (slice 1's in flight), slice 1 for all: one wait per slice, tied to the
+            // slice's fragments
+            static_assert(kBigNJ == 2 && (kBigMI == 4 || kBigMI == 2), "the waits below name every fragment");
+            if constexpr (kBigMI == 4) {
+                if constexpr (ks == 0)
+                    asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fa[0][2]), "+v"(fa[0][3]),
+                                 "+v"(fb[0][0]), "+v"(fb[0][1]));
+                else
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fa[1][2]), "+v"(fa[1][3]),
+                                 "+v"(fb[1][0]), "+v"(fb[1][1]));
+            } else {
+                if constexpr (ks == 0)
+                    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fb[0][0]), "+v"(fb[0][1]));
+                else
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fb[1][0]), "+v"(fb[1][1]));
+            }
 #pragma unroll
             for (int i = 0; i < kBigMI; i++)
 #pragma unroll
@@ -541,7 +560,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p
         });
     }
 
-    // lane holds Y[m0 + 128 wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + 64 wn + 32 j + l32]
+    // lane holds Y[m0 + (256 / WM) wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + 64 wn + 32 j + l32]
 #pragma unroll
     for (int i = 0; i < kBigMI; i++)
 #pragma unroll
@@ -550,11 +569,16 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p
             if (n >= p.N) continue;
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int m = m0 + 128 * wm + 32 * i + 8 * (v / 4) + 4 * hi + v % 4;
+                const int m = m0 + (kBM / WM) * wm + 32 * i + 8 * (v / 4) + 4 * hi + v % 4;
                 if (m < p.M) store_y<OUT16>(p, mi, m, n, acc[i][j][v]);
             }
         }
 }
+
+template <bool OUT16>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p) { gemm_big_tile<OUT16, 256>(p); }
+template <bool OUT16>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_mid_kernel(LinearParams p) { gemm_big_tile<OUT16, 128>(p); }
 
 // Waves per workgroup: the (matrix, 4-row group) items spread evenly over the CUs, one workgroup per CU (the weight
 // stream of each CU then ends at the same time), up to 8 waves; beyond 2048 items, several workgroups of 8 per CU.
@@ -600,11 +624,19 @@ hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
 }
 
 hipError_t launch_gemm(const LinearParams & p, hipStream_t stream) {
-    // 256 x 256 tiles when they give at least 3/4 of the CUs a tile (one workgroup per CU); else 128 x 128 tiles
-    const int big = p.count * ((p.N + kBN - 1) / kBN) * ((p.M + kBM - 1) / kBM);
+    // 256 x 256 tiles when they give at least 3/4 of the CUs a tile (one workgroup per CU), else 256 x 128 tiles on the
+    // same terms, else 128 x 128 tiles (three workgroups per CU)
+    const int mtl = (p.M + kBM - 1) / kBM;
+    const int big = p.count * ((p.N + 255) / 256) * mtl, mid = p.count * ((p.N + 127) / 128) * mtl;
+    const bool f16 = p.flags & kLinearOutF16;
     if (4 * big >= 3 * kGemmCUs) {
-        if (p.flags & kLinearOutF16) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
+        if (f16) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
         else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
+        return hipGetLastError();
+    }
+    if (4 * mid >= 3 * kGemmCUs) {
+        if (f16) hipLaunchKernelGGL(gemm_mid_kernel<true>, dim3((uint32_t)mid), dim3(kBigThreads), 0, stream, p);
+        else hipLaunchKernelGGL(gemm_mid_kernel<false>, dim3((uint32_t)mid), dim3(kBigThreads), 0, stream, p);
         return hipGetLastError();
     }
     const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);

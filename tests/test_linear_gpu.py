@@ -145,6 +145,12 @@ def test_gemm_big_tiles_ragged(device):
         rows=[0, 1, 255, 256, 511, 700, 1023, 1024, 1279, 1280, 1299])
 
 
+def test_gemm_mid_tiles_ragged(device):
+    """Enough 256 x 128 tiles (but too few 256 x 256 ones) for the 256 x 128 GEMM: ragged M and N, 3 steps of 32
+    columns, f16 output with bias."""
+    run(device, 11, 1900, 3896, 96, bias=True, out_f16=True, rows=[0, 1, 255, 256, 1023, 1536, 1791, 1792, 1899])
+
+
 def test_gemm_llama3_attn_output_chunk(device):
     run(device, 7, 300, 4096, 4096, accumulate=True, rows=[0, 1, 127, 128, 255, 299])
 
