@@ -504,7 +504,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     // ---- wave totals: l over the 4 score-lane groups; O is complete per lane (the products summed every key) ----
     l_run = xor32_add(xor16_add(l_run));
     if (lane < RT) {
-        s_m[wave][lane] = m_run;
+        s_m[wave][lane] = l_run > 0.f ? m_run : kNegInf;  // a wave with no visible key counts as -inf
         s_l[wave][lane] = l_run;
     }
     if (srow < RT) {
@@ -526,15 +526,19 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
         const int row = rt * RT + r;
         if (row >= p.rows) continue;
+        // branch-free: a wave without keys has m = -inf, weight 2^-inf = 0 and O = 0, so every read is independent
+        // (a test of l > 0 per wave compiled to a chain of dependent LDS reads and branches in the launch's tail)
+        float mw[NW];
+#pragma unroll
+        for (int w = 0; w < NW; w++) mw[w] = s_m[w][r];
         float M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < NW; w++)
-            if (s_l[w][r] > 0.f) M = fmaxf(M, s_m[w][r]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w]);
+        const float Mu = M == kNegInf ? 0.f : M;
         float tot = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            if (!(s_l[w][r] > 0.f)) continue;
-            const float wt = exp2_fast(s_m[w][r] - M);
+            const float wt = exp2_fast(mw[w] - Mu);
             tot += s_l[w][r] * wt;
             a0 += s_o(w)[r * HD + d] * wt;
             a1 += s_o(w)[r * HD + d + 1] * wt;
