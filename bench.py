@@ -429,7 +429,8 @@ def trace_decode(args):
                  ("cfg1 Qwen2.5-0.5B, 513 keys", 14, 2, 64, [513], 1, 32),
                  ("cfg4 Whisper cross-attention, 1500 frames, greedy", 20, 20, 64, [1500], 1, 32),
                  ("cfg4 Whisper self-attention, 449 keys", 20, 20, 64, [449], 1, 32)]
-    names = ["wave walk done", "waves merged", "partial published", "split counted", "splits merged"]
+    names = ["wave walk done", "waves merged", "partial published", "split counted", "splits merged",
+             "merge: weights", "merge: accumulated"]
     for name, nh, nkv, hd, lens, nq, layers in workloads:
         # n_q 0 marks the fused step on the reference's f32 q|k|v rows (adjacent-pair rotary, base 500000)
         prob = DecodeProblem(torch, gen, nh, nkv, hd, lens, layers, n_q=max(nq, 1), rope=(0, 500000.0) if nq == 0 else None)
@@ -443,7 +444,7 @@ def trace_decode(args):
         rel = lambda col, sel: (col[sel] - t0) / 100.0  # the real-time clock ticks at 100 MHz
         waves = t[:, 1:9]
         walk = np.where(waves > 0, waves, 0).max(axis=1)
-        cols = [walk, t[:, 9], t[:, 10], t[:, 11], t[:, 12]]
+        cols = [walk, t[:, 9], t[:, 10], t[:, 11], t[:, 12], t[:, 13], t[:, 15]]
         phases = {}
         for nm, col in zip(names, cols):
             sel = col > 0

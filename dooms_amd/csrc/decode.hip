@@ -98,7 +98,8 @@ __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, 
 }
 
 // The cross-split merge of a tile with more splits than one load round of the per-pair merge holds (> kMergeChunk):
-// every (m, l) pair of the tile is loaded once (one thread each) and turned into per-split weights 2^(m - M) in LDS,
+// every (m, l) pair of the tile is loaded once (split = lane, one wave per row) and turned into per-split weights
+// 2^(m - M) and the row's total by reductions inside the wave (a thread per row looping over the splits took ~0.6 us),
 // while the accumulator columns come in 16-byte device-scope loads, each column's splits striped over SF threads and
 // the stripes summed through LDS. Half the bytes of the per-pair merge through the merging CU, whose threads would
 // each load their row's (m, l) for every split: Llama-3-8B at 8192 keys (32 splits) 13.85 -> 13.44 us per launch.
@@ -114,22 +115,24 @@ __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float *
     constexpr int SF = kThreads >= NC ? kThreads / NC : 1;  // threads per column (stripes of the splits)
     constexpr int CPT = NC > kThreads ? NC / kThreads : 1;  // columns per thread
     constexpr int MC = 16 / CPT > 0 ? 16 / CPT : 1;         // splits of each column loaded per round
-    constexpr int NPAIR = kMaxSplitsPerTile * RT;           // (m, l) slots: [split][row]
-    constexpr int MLT = (NPAIR + kThreads - 1) / kThreads;  // (m, l) pairs per thread
-    constexpr int kStatBytes = (NPAIR * 12 + RT * 8 + 15) / 16 * 16;
-    float2 * s_ml = reinterpret_cast<float2 *>(lds);        // [split][row] (m, l); an empty split as (-inf, 0)
-    float * s_w = reinterpret_cast<float *>(s_ml + NPAIR);  // [split][row] 2^(m - M)
+    constexpr int NPAIR = kMaxSplitsPerTile * RT;           // weight slots: [split][row]
+    constexpr int RPW = (RT + NW - 1) / NW;                 // rows per wave for the (m, l) reductions
+    static_assert(kMaxSplitsPerTile <= kWave, "one lane per split");
+    constexpr int kStatBytes = (NPAIR * 4 + RT * 8 + 15) / 16 * 16;
+    float * s_w = reinterpret_cast<float *>(lds);               // [split][row] 2^(m - M)
     float2 * s_row = reinterpret_cast<float2 *>(s_w + NPAIR);  // [row] (M, total)
     float4_t * s_acc = reinterpret_cast<float4_t *>(lds + kStatBytes);  // [stripe - 1][column]
     static_assert(kStatBytes + (SF - 1) * NC * 16 <= (int64_t)LDS_BYTES, "merge scratch fits the V staging areas");
     const __amdgpu_buffer_rsrc_t rsrc = dev_rsrc(part_tile);
     const int stripe = SF > 1 ? (int)threadIdx.x / NC : 0;  // wave-uniform
     auto column = [&](int j) { return SF > 1 ? (int)threadIdx.x % NC : (int)threadIdx.x + j * kThreads; };
-    float2 ml[MLT];
+    // (m, l) of split `lane` and row `wave + NW i`, so that each row's maximum and total are reductions inside one wave
+    const int wave = (int)threadIdx.x / kWave, lane = (int)threadIdx.x % kWave;
+    float2 ml[RPW];
 #pragma unroll
-    for (int i = 0; i < MLT; i++) {
-        const int e = min((int)threadIdx.x + i * kThreads, ns * RT - 1);  // past the end: a valid pair, not used
-        collect2(part_tile + (e / RT) * SS + (e % RT) * (HD + 4) + HD, ml[i].x, ml[i].y);
+    for (int i = 0; i < RPW; i++) {
+        const int r = min(wave + NW * i, RT - 1), k = min(lane, ns - 1);  // past the end: a valid pair, not used
+        collect2(part_tile + k * SS + r * (HD + 4) + HD, ml[i].x, ml[i].y);
     }
     u32x4 px[CPT][MC];
     auto load_round = [&](int s0) __attribute__((always_inline)) {
@@ -142,35 +145,27 @@ __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float *
     };
     load_round(stripe);
     // (the (m, l) loads went out first: the waits below leave the accumulator loads in flight)
+    // each row: M = max over its splits, the splits' weights 2^(m - M) and the total, in the row's wave; an empty or
+    // missing split has m = -inf (weight 0) and l = 0
 #pragma unroll
-    for (int i = 0; i < MLT; i++) {
-        const int e = (int)threadIdx.x + i * kThreads;
-        if (e < NPAIR) s_ml[e] = e < ns * RT && ml[i].y > 0.f ? ml[i] : make_float2(kNegInf, 0.f);
-    }
-    __syncthreads();
-    // each (split, row): the row's maximum over the splits (independent LDS reads, no branch) and the split's weight;
-    // split 0 also the row's total
+    for (int i = 0; i < RPW; i++) {
+        const int r = wave + NW * i;  // wave-uniform
+        if (r >= RT) break;
+        const bool ok = lane < ns && ml[i].y > 0.f;
+        const float m = ok ? ml[i].x : kNegInf, l = ok ? ml[i].y : 0.f;
+        float M = xor16_max(xor32_max(m));
 #pragma unroll
-    for (int i = 0; i < MLT; i++) {
-        const int e = (int)threadIdx.x + i * kThreads;
-        if (e >= NPAIR) break;  // wave-uniform
-        const int r = e % RT;
-        float mk[kMaxSplitsPerTile];
-#pragma unroll
-        for (int k = 0; k < kMaxSplitsPerTile; k++) mk[k] = s_ml[k * RT + r].x;
-        float M = kNegInf;
-#pragma unroll
-        for (int k = 0; k < kMaxSplitsPerTile; k++) M = fmaxf(M, mk[k]);
+        for (int o = 8; o >= 1; o /= 2) M = vmax_raw(M, shfl_xor(M, o));
         const float Mu = M == kNegInf ? 0.f : M;
-        s_w[e] = exp2_fast(s_ml[e].x - Mu);
-        if (e < RT) {
-            float tot = 0.f;
+        const float w = exp2_fast(m - Mu);
+        float tot = xor16_add(xor32_add(l * w));
 #pragma unroll
-            for (int k = 0; k < kMaxSplitsPerTile; k++) tot = __builtin_fmaf(s_ml[k * RT + r].y, exp2_fast(mk[k] - Mu), tot);
-            s_row[r] = make_float2(M, tot);
-        }
+        for (int o = 8; o >= 1; o /= 2) tot += shfl_xor(tot, o);
+        if (lane < kMaxSplitsPerTile) s_w[lane * RT + r] = w;
+        if (lane == 0) s_row[r] = make_float2(M, tot);
     }
     __syncthreads();
+    if (threadIdx.x == 0) MX_TRACE(13);
     float4_t acc[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; j++) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -189,6 +184,7 @@ __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float *
         if (s0 >= ns) break;  // wave-uniform
         load_round(s0);
     }
+    if (threadIdx.x == 0) MX_TRACE(15);
     if constexpr (SF > 1) {
         if (stripe > 0) s_acc[(stripe - 1) * NC + threadIdx.x % NC] = acc[0];
         __syncthreads();
@@ -263,6 +259,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     if (threadIdx.x == 0) {
         MX_TRACE(0);
         MX_TRACE_CLEAR(12);
+        MX_TRACE_CLEAR(13);
+        MX_TRACE_CLEAR(15);
     }
     const uint32_t id = blockIdx.x, k8 = id / 8, u = k8 / T;
     const int rt = k8 % T;
