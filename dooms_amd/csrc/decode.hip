@@ -97,15 +97,15 @@ __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, 
     }
 }
 
-// The cross-split merge of a tile with more splits than one load round of the per-pair merge holds (> kMergeChunk):
-// every (m, l) pair of the tile is loaded once (split = lane, one wave per row) and turned into per-split weights
+// The cross-split merge of a head-dim-128 tile: every (m, l) pair of the tile is loaded once (split = lane, one wave per row) and turned into per-split weights
 // 2^(m - M) and the row's total by reductions inside the wave (a thread per row looping over the splits took ~0.6 us),
 // while the accumulator columns come in 16-byte device-scope loads, each column's splits striped over SF threads and
 // the stripes summed through LDS. Half the bytes of the per-pair merge through the merging CU, whose threads would
 // each load their row's (m, l) for every split: Llama-3-8B at 8192 keys (32 splits) 13.85 -> 13.44 us per launch.
-// With few splits the two extra barriers cost more than the bytes saved, so the per-pair merge stays there; it also
-// stays in the 4-wave and head-dim-64 kernels (batch 4 +0.1 us; at head dim 64 the path's registers cost a wave of
-// occupancy: 112 -> 136 VGPRs).
+// It serves every head-dim-128 tile of more than one split, in the 4- and 8-wave kernels (Llama-3-8B batch 4 at 8192
+// keys 33.6 -> 32.7 us, 1024 keys 7.07 -> 7.00 us). The head-dim-64 kernels keep the per-pair merge: there the path's
+// registers cost a wave of occupancy (112 -> 136 VGPRs), +0.4 us on Qwen2.5-0.5B and the Whisper shapes; head dim 256
+// has no registers to spare.
 template <int HD, int RT, bool F32, int NW, size_t LDS_BYTES>
 __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float * part_tile, int ns, int rt, int g, int G,
                                            int64_t seq_row0, char * lds) {
@@ -572,8 +572,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     // chunk's splits; the row's (m, l) loads of a wave coalesce), then folds them with a running maximum. One memory
     // round trip per chunk, no LDS, no barrier. ----
     const int ns = n_split;
-    if constexpr (HD >= 128 && NW == 8) {
-        if (ns > kMergeChunk) {
+    if constexpr (HD == 128) {
+        if (ns > 1) {
             merge_wide<HD, RT, F32, NW, sizeof s_v>(p, part_tile, ns, rt, g, G, seq_row0, reinterpret_cast<char *>(s_v));
             if (threadIdx.x == 0)
                 __hip_atomic_store(p.counters + tile * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
