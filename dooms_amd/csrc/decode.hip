@@ -585,45 +585,56 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         }
     }
     constexpr int PPT = (NP + kThreads - 1) / kThreads;  // output pairs per thread
+    // CH: splits whose loads are in flight at once, the smallest of 4, 6, 8, 12, 16 that holds them all (beyond 16,
+    // chunks of 16); past the last split the loads repeat it and weigh 0, so every CH >= ns gives the same sums
+    auto merge_pairs = [&](auto CHC) __attribute__((always_inline)) {
+        constexpr int CH = decltype(CHC)::value;
 #pragma unroll
-    for (int j = 0; j < PPT; j++) {
-        const int idx = threadIdx.x + j * kThreads;
-        if (idx >= NP) break;
-        const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
-        const int row = rt * RT + r;
-        if (row >= p.rows) continue;
-        const float * pr = part_tile + (int64_t)r * (HD + 4);
-        float M = kNegInf, tot = 0.f, a0 = 0.f, a1 = 0.f;
-        for (int k0 = 0; k0 < ns; k0 += kMergeChunk) {
-            float m[kMergeChunk], l[kMergeChunk], u[kMergeChunk], v[kMergeChunk];
+        for (int j = 0; j < PPT; j++) {
+            const int idx = threadIdx.x + j * kThreads;
+            if (idx >= NP) break;
+            const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
+            const int row = rt * RT + r;
+            if (row >= p.rows) continue;
+            const float * pr = part_tile + (int64_t)r * (HD + 4);
+            float M = kNegInf, tot = 0.f, a0 = 0.f, a1 = 0.f;
+            for (int k0 = 0; k0 < ns; k0 += CH) {
+                float m[CH], l[CH], u[CH], v[CH];
 #pragma unroll
-            for (int e = 0; e < kMergeChunk; e++) {
-                const int k = min(k0 + e, ns - 1);  // past the end: repeat the last split, weighted 0 below
-                collect2(pr + k * SS + HD, m[e], l[e]);
-                collect2(pr + k * SS + d, u[e], v[e]);
+                for (int e = 0; e < CH; e++) {
+                    const int k = min(k0 + e, ns - 1);  // past the end: repeat the last split, weighted 0 below
+                    collect2(pr + k * SS + HD, m[e], l[e]);
+                    collect2(pr + k * SS + d, u[e], v[e]);
+                }
+                float cm = M;
+#pragma unroll
+                for (int e = 0; e < CH; e++)
+                    if (k0 + e < ns && l[e] > 0.f) cm = fmaxf(cm, m[e]);
+                const float c = cm == M ? 1.f : exp2_fast(M - cm);  // rescale of what was summed so far
+                tot *= c;
+                a0 *= c;
+                a1 *= c;
+                M = cm;
+#pragma unroll
+                for (int e = 0; e < CH; e++) {
+                    const float w = (k0 + e < ns && l[e] > 0.f) ? exp2_fast(m[e] - M) : 0.f;
+                    tot = __builtin_fmaf(l[e], w, tot);
+                    a0 = __builtin_fmaf(u[e], w, a0);
+                    a1 = __builtin_fmaf(v[e], w, a1);
+                }
             }
-            float cm = M;
-#pragma unroll
-            for (int e = 0; e < kMergeChunk; e++)
-                if (k0 + e < ns && l[e] > 0.f) cm = fmaxf(cm, m[e]);
-            const float c = cm == M ? 1.f : exp2_fast(M - cm);  // rescale of what was summed so far
-            tot *= c;
-            a0 *= c;
-            a1 *= c;
-            M = cm;
-#pragma unroll
-            for (int e = 0; e < kMergeChunk; e++) {
-                const float w = (k0 + e < ns && l[e] > 0.f) ? exp2_fast(m[e] - M) : 0.f;
-                tot = __builtin_fmaf(l[e], w, tot);
-                a0 = __builtin_fmaf(u[e], w, a0);
-                a1 = __builtin_fmaf(v[e], w, a1);
-            }
+            const int t = row / G, h = g * G + row % G;
+            const float inv = 1.f / tot;
+            store_pair<F32>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 * inv, a1 * inv);
+            if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
         }
-        const int t = row / G, h = g * G + row % G;
-        const float inv = 1.f / tot;
-        store_pair<F32>(p, (seq_row0 + t) * p.out_stride + (int64_t)h * HD + d, a0 * inv, a1 * inv);
-        if (d == 0 && p.lse) p.lse[(seq_row0 + t) * p.n_head + h] = (M + log2_fast(tot)) * kLn2;
-    }
+    };
+    static_assert(kMergeChunk == 16, "the chunk sizes below");
+    if (ns <= 4) merge_pairs(std::integral_constant<int, 4>{});
+    else if (ns <= 6) merge_pairs(std::integral_constant<int, 6>{});
+    else if (ns <= 8) merge_pairs(std::integral_constant<int, 8>{});
+    else if (ns <= 12) merge_pairs(std::integral_constant<int, 12>{});
+    else merge_pairs(std::integral_constant<int, 16>{});
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef MX_ATTN_TRACE
     __syncthreads();
