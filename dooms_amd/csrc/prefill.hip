@@ -72,14 +72,18 @@ struct PrefillSmem {
 //      a read's chunk index (its 32-byte half) additive: two per-lane bases, the rest instruction offsets;
 //   V: no swizzle: each 32-lane phase of the transposing read takes 4 consecutive rows x 64 bytes, 256 contiguous bytes.
 // Three buffers: the loads of step i + 2 go out while step i is multiplied, with no registers in between.
-constexpr int kDLBuf = 3;  // a fourth buffer (three steps ahead) measured the same
+// buffers: three (two steps ahead) for the 8-wave plan, where a fourth measured the same; four (three steps ahead) for
+// the short-prompt key-split plan, whose steps are short against a memory round trip
 template <int HD, int W, int KSP, int SA>
-constexpr bool prefill_dl() { return HD == 128 && W == 8 && KSP == 1 && SA == 0; }
+constexpr bool prefill_dl() {
+    return SA == 0 && ((HD == 128 && W == 8 && KSP == 1) || (HD == 64 && W == 4 && KSP == 2));
+}
 
 template <int HD, int KSP>
 struct PrefillSmem<HD, KSP, true> {
-    half_t k[kDLBuf][KSP * kBK * HD];
-    half_t v[kDLBuf][KSP * kBK * HD];
+    static constexpr int NBUF = KSP == 2 ? 4 : 3;
+    half_t k[NBUF][KSP * kBK * HD];
+    half_t v[NBUF][KSP * kBK * HD];
 };
 
 // Work order of the prefill grid (o = 0 .. n_qtiles * n_head - 1), cut by xcd_remap into one contiguous range per XCD:
@@ -135,6 +139,8 @@ template <int HD, bool POS, int W, bool ROPE, int KSP, int SA, bool SK>
 __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>()> & sm,
                                              int kvh, int gi, int qt, const SkSegment & seg) {
     constexpr bool DL = prefill_dl<HD, W, KSP, SA>();
+    constexpr int DLB = DL ? PrefillSmem<HD, KSP, true>::NBUF : 1;  // direct-to-LDS buffers
+    constexpr int RB = KSP * kBK / 16;                              // 16-row blocks per chunk group of a step's tile
     constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
     static_assert(W % KSP == 0, "whole row tiles");
     static_assert(!(ROPE && SA), "the rotated prompt path reads f16 operands");
@@ -240,7 +246,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     if constexpr (DL) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int j = i * kWaves + wave, rb = j % 4, cb = j / 4;  // this instruction's block
+            const int j = i * kWaves + wave, rb = j % RB, cb = j / RB;  // this instruction's block
             dl_row[i] = 16 * rb + lane / 4;                             // the row this lane fills
             dl_ko[i] = dl_row[i] * row_bytes + 16 * (4 * cb + ((lane % 4) ^ (lane / 16)));
             dl_vo[i] = dl_row[i] * row_bytes + 16 * (4 * cb + lane % 4);
@@ -316,7 +322,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
         // the query went out first; steps 0 and 1 follow straight into LDS (the wait for the query leaves them in flight)
         if (nb > 0) issue_tile(ib0 * KB, 0);
 #pragma unroll
-        for (int a = 1; a < kDLBuf - 1; a++)
+        for (int a = 1; a < DLB - 1; a++)
             if (nb > a) issue_tile((ib0 + a) * KB, a);
         if constexpr (!ROPE) {
 #pragma unroll
@@ -393,16 +399,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
         const int kb = ib * KB + kh * kBK;  // this wave's block of the step
         int buf;
         if constexpr (DL) {
-            buf = jb % kDLBuf;
-            // this wave's loads of step ib are complete (those of step ib + 1 may still be in flight), then every
-            // wave's are: step ib is in buffer `buf`, and buffer (jb + 2) % 3 was last read in the previous step
-            static_assert(kDLBuf == 3, "the waits below keep one later step in flight");
-            if (jb + 1 < nb) __builtin_amdgcn_s_waitcnt(0x0F70 | NI * 2);          // vmcnt(2 NI)
-            else __builtin_amdgcn_s_waitcnt(0x0F70);                                     // vmcnt(0)
+            buf = jb % DLB;
+            // this wave's loads of step ib are complete (those of up to DLB - 2 later steps may be in flight), then
+            // every wave's are: step ib is in buffer `buf`, and the buffer refilled below was last read in step ib - 1
+            const int later = min(DLB - 2, nb - 1 - jb);
+            static_for<0, DLB - 1>([&](auto R) __attribute__((always_inline)) {
+                constexpr int r = decltype(R)::value;
+                if (later == r) __builtin_amdgcn_s_waitcnt(0x0F70 | (r * 2 * NI));  // vmcnt(r steps' loads)
+            });
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (jb + kDLBuf - 1 < nb) issue_tile((ib + kDLBuf - 1) * KB, (jb + kDLBuf - 1) % kDLBuf);
+            if (jb + DLB - 1 < nb) issue_tile((ib + DLB - 1) * KB, (jb + DLB - 1) % DLB);
         } else {
             buf = jb & 1;
             __syncthreads();  // step ib is in LDS buffer `buf`; buffer buf ^ 1 is no longer read
@@ -431,14 +439,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
             for (int v = 0; v < 16; v++) sc[0][v] = sc[1][v] = 0.f;
             u32x4 kf[DL ? NS : 1];
             const uint32_t kb0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ks_;
-            const uint32_t ka0 = kb0 + 2 * dl_k[0], ka1 = kb0 + 2 * dl_k[1];
+            const uint32_t ka0 = kb0 + 2 * (dl_k[0] + 2048 * kh), ka1 = kb0 + 2 * (dl_k[1] + 2048 * kh);
             if constexpr (DL) {
                 // every K fragment of the block in flight at once (inline asm, as the V reads below), each product
                 // waiting for its own: LDS reads complete in order, so product i needs lgkmcnt(NS - 1 - i)
                 static_assert(NS <= 16, "lgkmcnt counts at most 15 later reads");
                 static_for<0, NS>([&](auto I) __attribute__((always_inline)) {
                     constexpr int i = decltype(I)::value;
-                    constexpr int off = 2 * (2048 * (i / 4) + 1024 * (i % 2));
+                    constexpr int off = 2 * (512 * RB * (i / 4) + 1024 * (i % 2));
                     const uint32_t a = (i / 2) % 2 ? ka1 : ka0;
                     u32x4 t;
                     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(t) : "v"(a), "i"(off));
@@ -546,14 +554,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                 // The transposing reads as inline asm with their own waits: the compiler cannot tell the intrinsic's
                 // LDS read from the direct loads still writing another buffer, and would drain them (vmcnt(0)) before
                 // the first read of every block. Rows 16 u + 8 s8 + 4 hgrp + (lane % 16) / 4 of block (dt, u).
-                const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)vs_ + 2 * dl_v;
+                const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)vs_ +
+                                    2 * (dl_v + 2048 * kh);
                 // products whose reads are in flight ahead of the one multiplied (1: cfg5 -0.6 %, 3: -0.5 %)
                 constexpr int VA = 2;
                 short4_t vr[VA + 1][2];
                 static_for<0, NP + VA>([&](auto I) __attribute__((always_inline)) {
                     constexpr int t = decltype(I)::value;
                     if constexpr (t < NP) {
-                        constexpr int off = 2 * (512 * (4 * (t % DT) + t / DT));
+                        constexpr int off = 2 * (512 * (RB * (t % DT) + t / DT));
                         short4_t r0, r1;
                         asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
                                      : "=&v"(r0), "=&v"(r1)
