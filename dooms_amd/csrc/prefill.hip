@@ -73,15 +73,16 @@ struct PrefillSmem {
 //   V: no swizzle: each 32-lane phase of the transposing read takes 4 consecutive rows x 64 bytes, 256 contiguous bytes.
 // Three buffers: the loads of step i + 2 go out while step i is multiplied, with no registers in between.
 // buffers: three (two steps ahead) for the 8-wave plan, where a fourth measured the same; four (three steps ahead) for
-// the short-prompt key-split plan, whose steps are short against a memory round trip
+// the head-dim-64 short-prompt key-split plan, whose steps are short against a memory round trip; two for its
+// head-dim-128 form (64 KB steps, 128 KB of LDS)
 template <int HD, int W, int KSP, int SA>
 constexpr bool prefill_dl() {
-    return SA == 0 && ((HD == 128 && W == 8 && KSP == 1) || (HD == 64 && W == 4 && KSP == 2));
+    return SA == 0 && ((HD == 128 && W == 8 && KSP == 1) || (W == 4 && KSP == 2 && (HD == 64 || HD == 128)));
 }
 
 template <int HD, int KSP>
 struct PrefillSmem<HD, KSP, true> {
-    static constexpr int NBUF = KSP == 2 ? 4 : 3;
+    static constexpr int NBUF = KSP == 2 ? (HD == 64 ? 4 : 2) : 3;
     half_t k[NBUF][KSP * kBK * HD];
     half_t v[NBUF][KSP * kBK * HD];
 };
