@@ -55,7 +55,7 @@ __device__ __forceinline__ float get_f32(const float * a) {
 // 32 bytes that each 16-lane group reads through the transposing read, for both groups of a 32-lane phase, land on 64
 // distinct banks; the tile store writes 4 rows x 4 chunks per 16 lanes, also 16 distinct 4-bank groups). Every read
 // address is a per-lane base plus a compile-time offset, so the loop spends no ALU on addressing.
-template <int HD, int KSP, bool DL = false>
+template <int HD, int KSP, bool DL = false, int W = 8>
 struct PrefillSmem {
     static constexpr int KP = HD + 8;
     static constexpr int VP = HD + 32;
@@ -72,17 +72,18 @@ struct PrefillSmem {
 //      a read's chunk index (its 32-byte half) additive: two per-lane bases, the rest instruction offsets;
 //   V: no swizzle: each 32-lane phase of the transposing read takes 4 consecutive rows x 64 bytes, 256 contiguous bytes.
 // Three buffers: the loads of step i + 2 go out while step i is multiplied, with no registers in between.
-// buffers: three (two steps ahead) for the 8-wave plan, where a fourth measured the same; four (three steps ahead) for
-// the head-dim-64 short-prompt key-split plan, whose steps are short against a memory round trip; two for its
-// head-dim-128 form (64 KB steps, 128 KB of LDS)
+// buffers (PrefillSmem::NBUF): three (two steps ahead) for the 8-wave plan, where a fourth measured the same; in the
+// 4-wave plans four at head dim 64 (their steps are short against a memory round trip) and two at head dim 128 (the
+// key-split plan's 64 KB steps; the 32-row plan's two workgroups per CU)
 template <int HD, int W, int KSP, int SA>
 constexpr bool prefill_dl() {
-    return SA == 0 && ((HD == 128 && W == 8 && KSP == 1) || (W == 4 && KSP == 2 && (HD == 64 || HD == 128)));
+    return SA == 0 && ((HD == 128 && W == 8 && KSP == 1) || (W == 4 && (HD == 64 || HD == 128)));
 }
 
-template <int HD, int KSP>
-struct PrefillSmem<HD, KSP, true> {
-    static constexpr int NBUF = KSP == 2 ? (HD == 64 ? 4 : 2) : 3;
+template <int HD, int KSP, int W>
+struct PrefillSmem<HD, KSP, true, W> {
+    // 8 waves (one workgroup per CU): 3; 4 waves: 4 at head dim 64, 2 at 128 (64 KB, two workgroups per CU)
+    static constexpr int NBUF = W == 8 ? 3 : (HD == 64 ? 4 : 2);
     half_t k[NBUF][KSP * kBK * HD];
     half_t v[NBUF][KSP * kBK * HD];
 };
@@ -137,10 +138,10 @@ struct SkSegment {
 };
 
 template <int HD, bool POS, int W, bool ROPE, int KSP, int SA, bool SK>
-__device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>()> & sm,
+__device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>(), W> & sm,
                                              int kvh, int gi, int qt, const SkSegment & seg) {
     constexpr bool DL = prefill_dl<HD, W, KSP, SA>();
-    constexpr int DLB = DL ? PrefillSmem<HD, KSP, true>::NBUF : 1;  // direct-to-LDS buffers
+    constexpr int DLB = DL ? PrefillSmem<HD, KSP, true, W>::NBUF : 1;  // direct-to-LDS buffers
     constexpr int RB = KSP * kBK / 16;                              // 16-row blocks per chunk group of a step's tile
     constexpr int kWaves = W, RPW = W / KSP, kPrefillRows = 32 * RPW;  // RPW: 32-row query tiles per workgroup
     static_assert(W % KSP == 0, "whole row tiles");
@@ -731,7 +732,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
 template <int HD, bool POS, int W, bool ROPE, int KSP, int SA>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(KSP == 1 && HD <= 128 ? 2 : 1, KSP == 1 && HD <= 128 ? 2 : 1)))
 void prefill_kernel(PrefillParams p) {
-    __shared__ PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>()> sm;
+    __shared__ PrefillSmem<HD, KSP, prefill_dl<HD, W, KSP, SA>(), W> sm;
     // ---- work item: each XCD a contiguous range of a kv-head-major order, heavy query tiles first ----
     const uint32_t n_work = (uint32_t)p.n_qtiles * p.n_head;
     int kvh, gi, qt_order;
@@ -748,7 +749,7 @@ void prefill_kernel(PrefillParams p) {
 template <int HD, bool POS, bool ROPE>
 __global__ __launch_bounds__(8 * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_sk_kernel(PrefillParams p) {
-    __shared__ PrefillSmem<HD, 1, prefill_dl<HD, 8, 1, 0>()> sm;
+    __shared__ PrefillSmem<HD, 1, prefill_dl<HD, 8, 1, 0>(), 8> sm;
     const int32_t R = p.sk_ranges;
     const int32_t r = (int32_t)(blockIdx.x % 8) * (R / 8) + (int32_t)(blockIdx.x / 8);
     const int64_t total = p.sk_total, lo = sk_lo(total, R, r), hi = sk_lo(total, R, r + 1);
