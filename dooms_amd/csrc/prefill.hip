@@ -9,11 +9,11 @@
 //   * One workgroup = 8 waves = 256 query rows of one query head (4 waves = 128 rows for short prompts); each wave owns
 //     32 rows. When even those would leave most CUs idle, two waves share a 32-row tile and split its key blocks. The register budget is held to 256 per lane, so each SIMD interleaves two waves: one wave's softmax runs
 //     on the vector ALU while the other's products run on the matrix core; all waves of a CU share each K/V tile.
-//   * Key/value blocks of 64 rows pass through LDS. The 8-wave head-dim-128 plan on f16 operands loads them straight
-//     into LDS (global_load_lds_dwordx4) into three buffers, two steps ahead, as 1 KB blocks of 16 rows x 64 bytes with
-//     a bank swizzle chosen by which bytes each lane fetches; the other plans double-buffer: block i + 1 goes from
-//     registers into the free LDS buffer and block i + 2 is loaded into registers while block i is multiplied, in
-//     row-major tiles with padded rows. Either way the K reads and the transposing V reads are free of bank conflicts
+//   * Key/value blocks of 64 rows pass through LDS. Every plan on f16 operands at head dims 64 and 128 loads them
+//     straight into LDS (global_load_lds_dwordx4), two to four buffers deep, as 1 KB blocks of 16 rows x 64 bytes with
+//     a bank swizzle chosen by which bytes each lane fetches; the IR self-attention's converted rows and head dim 256
+//     double-buffer through registers: block i + 1 goes from registers into the free LDS buffer and block i + 2 is
+//     loaded into registers while block i is multiplied, in row-major tiles with padded rows. Either way the K reads and the transposing V reads are free of bank conflicts
 //     and address with per-lane bases plus compile-time offsets; one barrier per block.
 //   * Transposed scores: S^T (keys x queries) = K Q^T on v_mfma_f32_32x32x16_f16. In the result each lane holds 16 keys
 //     of ONE query (the lane 32 away the other 16), so the row max and sum need one cross-lane step, and the
