@@ -674,7 +674,7 @@ def main():
                 ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1, False, "gemv_kernel"),
                 ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1, False, "gemv_kernel"),
                 ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, False,
-                 "stage_kernel + gemm_big_kernel"),
+                 "stage_kernel + gemm_w192_kernel"),
                 ("plan_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, True,
                  "stage_kernel + hipBLASLt (mx_linear_plan)"),
                 ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8, False,

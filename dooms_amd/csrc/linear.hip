@@ -429,20 +429,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
 // instruction each; 16-byte chunk c of row r sits at 16 (c ^ ((r % 16) / 4)) within its row's 64 bytes, so the 16-byte
 // operand reads of 16 consecutive rows at one chunk land on 16 distinct 4-bank groups. 96 KB of LDS: one workgroup per
 // CU, two waves per SIMD.
-// BN = 128 (256 x 128 tiles, 8 waves of 64 x 64) serves products whose 256 x 256 tiles would leave CUs idle.
+// BN = 128 (256 x 128 tiles, 8 waves of 64 x 64) and BN = 192 (256 x 192, 8 waves of 64 x 96) serve products whose
+// 256 x 256 tiles would leave CUs idle.
 constexpr int kBM = 256, kBK = 32;
 constexpr int kGemmCUs = 256;
 constexpr int kBigWaves = 8, kBigThreads = kBigWaves * kWave;
 constexpr int kBigBufs = 3;
 constexpr int kBigLoads = kBM * kBK * 2 / 1024 / kBigWaves;    // 1 KB direct loads of A per wave and step (2)
 
-template <bool OUT16, int BN>
+// WC: columns per wave (64, or 96 for 256 x 192 tiles: 8 waves of 64 x 96)
+template <bool OUT16, int BN, int WC = 64>
 __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
     constexpr int kBN = BN;
-    constexpr int WN = BN / 64, WM = kBigWaves / WN;   // waves along N (64 columns each) and along M
-    constexpr int kBigMI = kBM / WM / 32, kBigNJ = 2;  // 32 x 32 MFMA tiles per wave
-    constexpr int BLoads = BN * kBK * 2 / 1024 / kBigWaves;  // 1 KB direct loads of B per wave and step
-    static_assert(BLoads >= 1 && kBigMI >= 1, "whole loads and tiles per wave");
+    constexpr int WN = BN / WC, WM = kBigWaves / WN;         // waves along N and along M
+    constexpr int kBigMI = kBM / WM / 32, kBigNJ = WC / 32;  // 32 x 32 MFMA tiles per wave
+    constexpr int BBlocks = BN * kBK * 2 / 1024;             // 1 KB blocks of a step's B tile
+    constexpr int BLoads = (BBlocks + kBigWaves - 1) / kBigWaves;  // direct loads of B per wave and step; past the
+                                                                   // tile's blocks a wave reloads one it already loads
+    static_assert(BLoads >= 1 && kBigMI >= 1 && WN * WM == kBigWaves, "whole loads and tiles per wave");
     __shared__ __attribute__((aligned(1024))) half_t xs[kBigBufs][kBM * kBK];
     __shared__ __attribute__((aligned(1024))) half_t ws[kBigBufs][BN * kBK];
     const int n_tiles = (p.N + kBN - 1) / kBN, m_tiles = (p.M + kBM - 1) / kBM;
@@ -467,7 +471,8 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
     }
 #pragma unroll
     for (int i = 0; i < BLoads; i++) {
-        const int row = 16 * (i * kBigWaves + wave) + lane / 4;
+        const int j = i * kBigWaves + wave, jb = j < BBlocks ? j : j - kBigWaves;  // (identical bytes written twice)
+        const int row = 16 * jb + lane / 4;
         b_off[i] = (uint32_t)(min(n0 + row, p.N - 1) - n0) * p.K * 2 + 16 * c;
     }
     auto issue = [&](int step, int buf) __attribute__((always_inline)) {
@@ -478,10 +483,11 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
             __builtin_amdgcn_global_load_lds(a_base + k0 + a_off[i],
                                              (__attribute__((address_space(3))) void *)&xs[buf][512 * (i * kBigWaves + wave)],
                                              16, 0, 0);
-            if (i < BLoads)
+            if (i < BLoads) {
+                const int j = i * kBigWaves + wave, jb = j < BBlocks ? j : j - kBigWaves;
                 __builtin_amdgcn_global_load_lds(b_base + k0 + b_off[i],
-                                                 (__attribute__((address_space(3))) void *)&ws[buf][512 * (i * kBigWaves + wave)],
-                                                 16, 0, 0);
+                                                 (__attribute__((address_space(3))) void *)&ws[buf][512 * jb], 16, 0, 0);
+            }
         }
     };
 
@@ -515,7 +521,7 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
         // the operand reads as inline asm (the compiler cannot tell them from the direct loads in flight, and would
         // wait for those), all of the step's in flight, the products of each 16-column slice behind their reads
         const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)xs[buf] + 2 * 32 * (kBM / WM) * wm;
-        const uint32_t wa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ws[buf] + 2 * 2048 * wn;
+        const uint32_t wa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ws[buf] + 2 * 32 * WC * wn;
         u32x4 fa[2][kBigMI], fb[2][kBigNJ];
         static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
             constexpr int ks = decltype(KS)::value;
@@ -537,8 +543,16 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
             constexpr int ks = decltype(KS)::value;
             // slice 0 waits for its reads (slice 1's in flight), slice 1 for all: one wait per slice, tied to the
             // slice's fragments
-            static_assert(kBigNJ == 2 && (kBigMI == 4 || kBigMI == 2), "the waits below name every fragment");
-            if constexpr (kBigMI == 4) {
+            static_assert((kBigNJ == 2 && (kBigMI == 4 || kBigMI == 2)) || (kBigNJ == 3 && kBigMI == 2),
+                          "the waits below name every fragment");
+            if constexpr (kBigNJ == 3) {
+                if constexpr (ks == 0)
+                    asm volatile("s_waitcnt lgkmcnt(5)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fb[0][0]), "+v"(fb[0][1]),
+                                 "+v"(fb[0][2]));
+                else
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fb[1][0]), "+v"(fb[1][1]),
+                                 "+v"(fb[1][2]));
+            } else if constexpr (kBigMI == 4) {
                 if constexpr (ks == 0)
                     asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fa[0][2]), "+v"(fa[0][3]),
                                  "+v"(fb[0][0]), "+v"(fb[0][1]));
@@ -560,12 +574,12 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
         });
     }
 
-    // lane holds Y[m0 + (256 / WM) wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + 64 wn + 32 j + l32]
+    // lane holds Y[m0 + (256 / WM) wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + WC wn + 32 j + l32]
 #pragma unroll
     for (int i = 0; i < kBigMI; i++)
 #pragma unroll
         for (int j = 0; j < kBigNJ; j++) {
-            const int n = n0 + 64 * wn + 32 * j + l32;
+            const int n = n0 + WC * wn + 32 * j + l32;
             if (n >= p.N) continue;
 #pragma unroll
             for (int v = 0; v < 16; v++) {
@@ -579,6 +593,8 @@ template <bool OUT16>
 __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p) { gemm_big_tile<OUT16, 256>(p); }
 template <bool OUT16>
 __global__ __launch_bounds__(kBigThreads, 1) void gemm_mid_kernel(LinearParams p) { gemm_big_tile<OUT16, 128>(p); }
+template <bool OUT16>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_w192_kernel(LinearParams p) { gemm_big_tile<OUT16, 192, 96>(p); }
 
 // Waves per workgroup: the (matrix, 4-row group) items spread evenly over the CUs, one workgroup per CU (the weight
 // stream of each CU then ends at the same time), up to 8 waves; beyond 2048 items, several workgroups of 8 per CU.
@@ -624,19 +640,29 @@ hipError_t launch_linear(const LinearParams & p, hipStream_t stream) {
 }
 
 hipError_t launch_gemm(const LinearParams & p, hipStream_t stream) {
-    // 256 x 256 tiles when they give at least 3/4 of the CUs a tile (one workgroup per CU), else 256 x 128 tiles on the
-    // same terms, else 128 x 128 tiles (three workgroups per CU)
+    // 256-row tiles 256, 192 or 128 columns wide (one workgroup per CU), whichever costs the fewest rounds on the CUs
+    // times its width, the narrower tiles weighted for their lower efficiency (measured: the Llama-3-8B q|k|v chunk,
+    // 2048 x 6144, as 256 tiles of 256 x 192 rather than 192 of 256 x 256); when even the 256 x 128 tiles leave a
+    // quarter of the CUs idle, 128 x 128 tiles (three workgroups per CU)
     const int mtl = (p.M + kBM - 1) / kBM;
-    const int big = p.count * ((p.N + 255) / 256) * mtl, mid = p.count * ((p.N + 127) / 128) * mtl;
+    const int64_t t256 = (int64_t)p.count * ((p.N + 255) / 256) * mtl, t192 = (int64_t)p.count * ((p.N + 191) / 192) * mtl,
+                  t128 = (int64_t)p.count * ((p.N + 127) / 128) * mtl;
     const bool f16 = p.flags & kLinearOutF16;
-    if (4 * big >= 3 * kGemmCUs) {
-        if (f16) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
-        else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3((uint32_t)big), dim3(kBigThreads), 0, stream, p);
-        return hipGetLastError();
-    }
-    if (4 * mid >= 3 * kGemmCUs) {
-        if (f16) hipLaunchKernelGGL(gemm_mid_kernel<true>, dim3((uint32_t)mid), dim3(kBigThreads), 0, stream, p);
-        else hipLaunchKernelGGL(gemm_mid_kernel<false>, dim3((uint32_t)mid), dim3(kBigThreads), 0, stream, p);
+    if (4 * t128 >= 3 * kGemmCUs || 4 * t256 >= 3 * kGemmCUs) {
+        auto rounds = [](int64_t t) { return (double)((t + kGemmCUs - 1) / kGemmCUs); };
+        const double c256 = rounds(t256) * 256 * (4 * t256 >= 3 * kGemmCUs ? 1.0 : 1.35);  // a partial round idles CUs
+        const double c192 = rounds(t192) * 192 * 1.05 * (4 * t192 >= 3 * kGemmCUs ? 1.0 : 1.35);
+        const double c128 = rounds(t128) * 128 * 1.15;
+        if (c256 <= c192 && c256 <= c128) {
+            if (f16) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3((uint32_t)t256), dim3(kBigThreads), 0, stream, p);
+            else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3((uint32_t)t256), dim3(kBigThreads), 0, stream, p);
+        } else if (c192 <= c128) {
+            if (f16) hipLaunchKernelGGL(gemm_w192_kernel<true>, dim3((uint32_t)t192), dim3(kBigThreads), 0, stream, p);
+            else hipLaunchKernelGGL(gemm_w192_kernel<false>, dim3((uint32_t)t192), dim3(kBigThreads), 0, stream, p);
+        } else {
+            if (f16) hipLaunchKernelGGL(gemm_mid_kernel<true>, dim3((uint32_t)t128), dim3(kBigThreads), 0, stream, p);
+            else hipLaunchKernelGGL(gemm_mid_kernel<false>, dim3((uint32_t)t128), dim3(kBigThreads), 0, stream, p);
+        }
         return hipGetLastError();
     }
     const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);

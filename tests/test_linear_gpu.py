@@ -151,6 +151,12 @@ def test_gemm_mid_tiles_ragged(device):
     run(device, 11, 1900, 3896, 96, bias=True, out_f16=True, rows=[0, 1, 255, 256, 1023, 1536, 1791, 1792, 1899])
 
 
+def test_gemm_w192_tiles_ragged(device):
+    """A product that takes the 256 x 192 tiles (8 waves of 64 x 96 columns, the B tile's 12 load blocks spread over
+    16 loads): ragged M and N, 3 steps of 32 columns, accumulation."""
+    run(device, 12, 1900, 5700, 96, accumulate=True, rows=[0, 1, 255, 256, 1023, 1536, 1791, 1792, 1899])
+
+
 def test_gemm_llama3_attn_output_chunk(device):
     run(device, 7, 300, 4096, 4096, accumulate=True, rows=[0, 1, 127, 128, 255, 299])
 
