@@ -431,16 +431,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
 // CU, two waves per SIMD.
 // BN = 128 (256 x 128 tiles, 8 waves of 64 x 64) and BN = 192 (256 x 192, 8 waves of 64 x 96) serve products whose
 // 256 x 256 tiles would leave CUs idle.
-constexpr int kBM = 256, kBK = 32;
+constexpr int kBM = 256;
 constexpr int kGemmCUs = 256;
 constexpr int kBigWaves = 8, kBigThreads = kBigWaves * kWave;
-constexpr int kBigBufs = 3;
-constexpr int kBigLoads = kBM * kBK * 2 / 1024 / kBigWaves;    // 1 KB direct loads of A per wave and step (2)
-
-// WC: columns per wave (64, or 96 for 256 x 192 tiles: 8 waves of 64 x 96)
-template <bool OUT16, int BN, int WC = 64>
+// WC: columns per wave (64, or 96 for 256 x 192 tiles: 8 waves of 64 x 96). BK: columns per step, 32 (three buffers)
+// or 64 (two buffers, half the barriers and load instructions per product; K a multiple of 64).
+template <bool OUT16, int BN, int WC = 64, int BK = 32>
 __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
-    constexpr int kBN = BN;
+    constexpr int kBN = BN, kBK = BK;
+    constexpr int kBigBufs = BK == 32 ? 3 : 2;
+    constexpr int kBigLoads = kBM * kBK * 2 / 1024 / kBigWaves;  // 1 KB direct loads of A per wave and step
+    constexpr int RA = kBM / 16, RBB = BN / 16;                  // 16-row blocks per chunk group of A and of B
     constexpr int WN = BN / WC, WM = kBigWaves / WN;         // waves along N and along M
     constexpr int kBigMI = kBM / WM / 32, kBigNJ = WC / 32;  // 32 x 32 MFMA tiles per wave
     constexpr int BBlocks = BN * kBK * 2 / 1024;             // 1 KB blocks of a step's B tile
@@ -463,17 +464,19 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
     const char * a_base = reinterpret_cast<const char *>(p.xh + (int64_t)m0 * kp);
     const char * b_base = reinterpret_cast<const char *>(p.w[mi] + (int64_t)n0 * p.K);
     uint32_t a_off[kBigLoads], b_off[BLoads];
-    const int c = (lane % 4) ^ (lane / 16);  // the chunk a lane fetches for position lane % 4 of its row
+    const int c = (lane % 4) ^ (lane / 16);  // the chunk a lane fetches for position lane % 4 of its row's 64 bytes
+    // block j of a tile: chunk group j / R (64-byte column group), rows 16 (j % R) ..
 #pragma unroll
     for (int i = 0; i < kBigLoads; i++) {
-        const int row = 16 * (i * kBigWaves + wave) + lane / 4;  // the row this lane fills in block i W + wave
-        a_off[i] = (uint32_t)(min(m0 + row, p.M - 1) - m0) * kp * 2 + 16 * c;
+        const int j = i * kBigWaves + wave;
+        const int row = 16 * (j % RA) + lane / 4;  // the row this lane fills
+        a_off[i] = (uint32_t)(min(m0 + row, p.M - 1) - m0) * kp * 2 + 64 * (j / RA) + 16 * c;
     }
 #pragma unroll
     for (int i = 0; i < BLoads; i++) {
         const int j = i * kBigWaves + wave, jb = j < BBlocks ? j : j - kBigWaves;  // (identical bytes written twice)
-        const int row = 16 * jb + lane / 4;
-        b_off[i] = (uint32_t)(min(n0 + row, p.N - 1) - n0) * p.K * 2 + 16 * c;
+        const int row = 16 * (jb % RBB) + lane / 4;
+        b_off[i] = (uint32_t)(min(n0 + row, p.N - 1) - n0) * p.K * 2 + 64 * (jb / RBB) + 16 * c;
     }
     auto issue = [&](int step, int buf) __attribute__((always_inline)) {
         const int64_t k0 = (int64_t)step * kBK * 2;  // bytes
@@ -506,72 +509,109 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) rd[ks] = 512 * (l32 / 16) + 32 * (l32 % 16) + 8 * ((2 * ks + hi) ^ ((l32 % 16) / 4));
     const int nk = p.K / kBK;
-    issue(0, 0);
-    if (nk > 1) issue(1, 1);
+#pragma unroll
+    for (int a = 0; a < kBigBufs - 1; a++)
+        if (a < nk) issue(a, a);
     for (int s = 0; s < nk; s++) {
         const int buf = s % kBigBufs;
-        // this wave's loads of step s are complete (step s + 1's may be in flight), then every wave's are; buffer
-        // (s + 2) % 3 was last read in step s - 1
-        if (s + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | (kBigLoads + BLoads));  // vmcnt(the next step's loads)
-        else __builtin_amdgcn_s_waitcnt(0x0F70);                              // vmcnt(0)
+        // this wave's loads of step s are complete (those of up to kBigBufs - 2 later steps may be in flight), then
+        // every wave's are; the buffer refilled below was last read in step s - 1
+        if (kBigBufs > 2 && s + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | (kBigLoads + BLoads));  // vmcnt(next step)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                                                     // vmcnt(0)
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 2 < nk) issue(s + 2, (s + 2) % kBigBufs);
+        if (s + kBigBufs - 1 < nk) issue(s + kBigBufs - 1, (s + kBigBufs - 1) % kBigBufs);
         // the operand reads as inline asm (the compiler cannot tell them from the direct loads in flight, and would
         // wait for those), all of the step's in flight, the products of each 16-column slice behind their reads
         const uint32_t xa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)xs[buf] + 2 * 32 * (kBM / WM) * wm;
         const uint32_t wa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)ws[buf] + 2 * 32 * WC * wn;
-        u32x4 fa[2][kBigMI], fb[2][kBigNJ];
-        static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
-            constexpr int ks = decltype(KS)::value;
-            const uint32_t ra_ = xa + 2 * rd[ks], rb_ = wa + 2 * rd[ks];
-            static_for<0, kBigMI>([&](auto I) __attribute__((always_inline)) {
-                constexpr int i = decltype(I)::value;
-                u32x4 r;
-                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(ra_), "i"(2 * 1024 * i));
-                fa[ks][i] = r;
-            });
-            static_for<0, kBigNJ>([&](auto J) __attribute__((always_inline)) {
-                constexpr int j = decltype(J)::value;
-                u32x4 r;
-                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(rb_), "i"(2 * 1024 * j));
-                fb[ks][j] = r;
-            });
-        });
-        static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
-            constexpr int ks = decltype(KS)::value;
-            // slice 0 waits for its reads (slice 1's in flight), slice 1 for all: one wait per slice, tied to the
-            // slice's fragments
-            static_assert((kBigNJ == 2 && (kBigMI == 4 || kBigMI == 2)) || (kBigNJ == 3 && kBigMI == 2),
-                          "the waits below name every fragment");
-            if constexpr (kBigNJ == 3) {
-                if constexpr (ks == 0)
-                    asm volatile("s_waitcnt lgkmcnt(5)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fb[0][0]), "+v"(fb[0][1]),
-                                 "+v"(fb[0][2]));
-                else
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fb[1][0]), "+v"(fb[1][1]),
-                                 "+v"(fb[1][2]));
-            } else if constexpr (kBigMI == 4) {
-                if constexpr (ks == 0)
-                    asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fa[0][2]), "+v"(fa[0][3]),
-                                 "+v"(fb[0][0]), "+v"(fb[0][1]));
-                else
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fa[1][2]), "+v"(fa[1][3]),
-                                 "+v"(fb[1][0]), "+v"(fb[1][1]));
-            } else {
-                if constexpr (ks == 0)
-                    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fb[0][0]), "+v"(fb[0][1]));
-                else
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fb[1][0]), "+v"(fb[1][1]));
-            }
+        if constexpr (BK == 64) {
+            // 4 slices of 16 columns: slices s + 1's reads in flight behind slice s's products (at most 2 slices of
+            // reads outstanding, within the 15 that lgkmcnt counts); the waits are ordered by sched_barrier
+            constexpr int R = kBigMI + kBigNJ;  // reads per slice
+            u32x4 fa[4][kBigMI], fb[4][kBigNJ];
+            auto reads = [&](auto KS) __attribute__((always_inline)) {
+                constexpr int ks = decltype(KS)::value;
+                const uint32_t ra_ = xa + 2 * (rd[ks % 2] + 512 * RA * (ks / 2)), rb_ = wa + 2 * (rd[ks % 2] + 512 * RBB * (ks / 2));
+                static_for<0, kBigMI>([&](auto I) __attribute__((always_inline)) {
+                    u32x4 r;
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(ra_), "i"(2 * 1024 * decltype(I)::value));
+                    fa[ks][decltype(I)::value] = r;
+                });
+                static_for<0, kBigNJ>([&](auto J) __attribute__((always_inline)) {
+                    u32x4 r;
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(rb_), "i"(2 * 1024 * decltype(J)::value));
+                    fb[ks][decltype(J)::value] = r;
+                });
+            };
+            reads(std::integral_constant<int, 0>{});
+            reads(std::integral_constant<int, 1>{});
+            static_for<0, 4>([&](auto KS) __attribute__((always_inline)) {
+                constexpr int ks = decltype(KS)::value;
+                if constexpr (ks < 3) asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(R) : "memory");
+                else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < kBigMI; i++)
+                for (int i = 0; i < kBigMI; i++)
 #pragma unroll
-                for (int j = 0; j < kBigNJ; j++)
-                    acc[i][j] = mfma32x32x16(as_half8(fa[ks][i]), as_half8(fb[ks][j]), acc[i][j]);
-            __builtin_amdgcn_sched_barrier(0);
-        });
+                    for (int j = 0; j < kBigNJ; j++)
+                        acc[i][j] = mfma32x32x16(as_half8(fa[ks][i]), as_half8(fb[ks][j]), acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (ks + 2 < 4) reads(std::integral_constant<int, ks + 2>{});
+            });
+        } else {
+            u32x4 fa[2][kBigMI], fb[2][kBigNJ];
+            static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
+                constexpr int ks = decltype(KS)::value;
+                const uint32_t ra_ = xa + 2 * rd[ks], rb_ = wa + 2 * rd[ks];
+                static_for<0, kBigMI>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value;
+                    u32x4 r;
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(ra_), "i"(2 * 1024 * i));
+                    fa[ks][i] = r;
+                });
+                static_for<0, kBigNJ>([&](auto J) __attribute__((always_inline)) {
+                    constexpr int j = decltype(J)::value;
+                    u32x4 r;
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(rb_), "i"(2 * 1024 * j));
+                    fb[ks][j] = r;
+                });
+            });
+            static_for<0, 2>([&](auto KS) __attribute__((always_inline)) {
+                constexpr int ks = decltype(KS)::value;
+                // slice 0 waits for its reads (slice 1's in flight), slice 1 for all: one wait per slice, tied to the
+                // slice's fragments
+                static_assert((kBigNJ == 2 && (kBigMI == 4 || kBigMI == 2)) || (kBigNJ == 3 && kBigMI == 2),
+                              "the waits below name every fragment");
+                if constexpr (kBigNJ == 3) {
+                    if constexpr (ks == 0)
+                        asm volatile("s_waitcnt lgkmcnt(5)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fb[0][0]), "+v"(fb[0][1]),
+                                     "+v"(fb[0][2]));
+                    else
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fb[1][0]), "+v"(fb[1][1]),
+                                     "+v"(fb[1][2]));
+                } else if constexpr (kBigMI == 4) {
+                    if constexpr (ks == 0)
+                        asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fa[0][2]), "+v"(fa[0][3]),
+                                     "+v"(fb[0][0]), "+v"(fb[0][1]));
+                    else
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fa[1][2]), "+v"(fa[1][3]),
+                                     "+v"(fb[1][0]), "+v"(fb[1][1]));
+                } else {
+                    if constexpr (ks == 0)
+                        asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(fa[0][0]), "+v"(fa[0][1]), "+v"(fb[0][0]), "+v"(fb[0][1]));
+                    else
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[1][0]), "+v"(fa[1][1]), "+v"(fb[1][0]), "+v"(fb[1][1]));
+                }
+#pragma unroll
+                for (int i = 0; i < kBigMI; i++)
+#pragma unroll
+                    for (int j = 0; j < kBigNJ; j++)
+                        acc[i][j] = mfma32x32x16(as_half8(fa[ks][i]), as_half8(fb[ks][j]), acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
     }
 
     // lane holds Y[m0 + (256 / WM) wm + 32 i + 8 (v / 4) + 4 hi + v % 4][n0 + WC wn + 32 j + l32]
@@ -589,12 +629,13 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
         }
 }
 
-template <bool OUT16>
-__global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p) { gemm_big_tile<OUT16, 256>(p); }
-template <bool OUT16>
-__global__ __launch_bounds__(kBigThreads, 1) void gemm_mid_kernel(LinearParams p) { gemm_big_tile<OUT16, 128>(p); }
-template <bool OUT16>
-__global__ __launch_bounds__(kBigThreads, 1) void gemm_w192_kernel(LinearParams p) { gemm_big_tile<OUT16, 192, 96>(p); }
+// K in steps of 64 columns when K is a multiple of 64 (BK = 64), else 32
+template <bool OUT16, int BK>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_big_kernel(LinearParams p) { gemm_big_tile<OUT16, 256, 64, BK>(p); }
+template <bool OUT16, int BK>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_mid_kernel(LinearParams p) { gemm_big_tile<OUT16, 128, 64, BK>(p); }
+template <bool OUT16, int BK>
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_w192_kernel(LinearParams p) { gemm_big_tile<OUT16, 192, 96, BK>(p); }
 
 // Waves per workgroup: the (matrix, 4-row group) items spread evenly over the CUs, one workgroup per CU (the weight
 // stream of each CU then ends at the same time), up to 8 waves; beyond 2048 items, several workgroups of 8 per CU.
@@ -653,16 +694,20 @@ hipError_t launch_gemm(const LinearParams & p, hipStream_t stream) {
         const double c256 = rounds(t256) * 256 * (4 * t256 >= 3 * kGemmCUs ? 1.0 : 1.35);  // a partial round idles CUs
         const double c192 = rounds(t192) * 192 * 1.05 * (4 * t192 >= 3 * kGemmCUs ? 1.0 : 1.35);
         const double c128 = rounds(t128) * 128 * 1.15;
-        if (c256 <= c192 && c256 <= c128) {
-            if (f16) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3((uint32_t)t256), dim3(kBigThreads), 0, stream, p);
-            else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3((uint32_t)t256), dim3(kBigThreads), 0, stream, p);
-        } else if (c192 <= c128) {
-            if (f16) hipLaunchKernelGGL(gemm_w192_kernel<true>, dim3((uint32_t)t192), dim3(kBigThreads), 0, stream, p);
-            else hipLaunchKernelGGL(gemm_w192_kernel<false>, dim3((uint32_t)t192), dim3(kBigThreads), 0, stream, p);
-        } else {
-            if (f16) hipLaunchKernelGGL(gemm_mid_kernel<true>, dim3((uint32_t)t128), dim3(kBigThreads), 0, stream, p);
-            else hipLaunchKernelGGL(gemm_mid_kernel<false>, dim3((uint32_t)t128), dim3(kBigThreads), 0, stream, p);
-        }
+        const bool k64 = p.K % 64 == 0;
+        const int sel = 2 * (k64 ? 1 : 0) + (f16 ? 1 : 0);
+        void (*const big[4])(LinearParams) = {gemm_big_kernel<false, 32>, gemm_big_kernel<true, 32>,
+                                              gemm_big_kernel<false, 64>, gemm_big_kernel<true, 64>};
+        void (*const w192[4])(LinearParams) = {gemm_w192_kernel<false, 32>, gemm_w192_kernel<true, 32>,
+                                               gemm_w192_kernel<false, 64>, gemm_w192_kernel<true, 64>};
+        void (*const mid[4])(LinearParams) = {gemm_mid_kernel<false, 32>, gemm_mid_kernel<true, 32>,
+                                              gemm_mid_kernel<false, 64>, gemm_mid_kernel<true, 64>};
+        if (c256 <= c192 && c256 <= c128)
+            hipLaunchKernelGGL(big[sel], dim3((uint32_t)t256), dim3(kBigThreads), 0, stream, p);
+        else if (c192 <= c128)
+            hipLaunchKernelGGL(w192[sel], dim3((uint32_t)t192), dim3(kBigThreads), 0, stream, p);
+        else
+            hipLaunchKernelGGL(mid[sel], dim3((uint32_t)t128), dim3(kBigThreads), 0, stream, p);
         return hipGetLastError();
     }
     const int tiles = p.count * ((p.N + kTN - 1) / kTN) * ((p.M + kTM - 1) / kTM);
