@@ -11,6 +11,8 @@
 //   MetalWhisperDecoder::Impl::cross_attention(cache_off, M)                   WhisperAttention::cross_attention(layer, q, out, M)
 //     (src/backend/metal/metal_whisper_decoder.mm:167-225); each also on the reference's own f32 buffers (overloads
 //     taking float q|k|v rows and float output: the cache write of the step / prompt happens in the library)
+//   MetalLlamaDecoder::profile_pass / MetalWhisperDecoder::profile_step      set_profile(&times) + the calls; KernelTime
+//     (metal_llama_decoder.mm:789-812, metal_whisper_decoder.mm:613-626)
 //   Status / Code (src/core/status.h:13-81)                                     Status / Code below (same numbering)
 //
 // The caches keep the reference's layout: per layer [n_ctx][n_head_kv * head_dim] f16, layer l at l * n_ctx rows
@@ -18,7 +20,7 @@
 // metal_whisper_decoder.mm:460-461). The caller owns them. Rotary embedding is the caller's (the reference's
 // rope_store, llama_kernels.h:520-545) for prompt chunks: q arrives rotated, and append() copies rotated keys/values
 // into the cache rows; decode_step() is the reference's fused_rope decode (rotation and cache write in the kernel). Like the reference's decoders these objects are not thread-safe; all work is
-// ordered on the stream given at create, and nothing synchronizes with the host except create/destroy.
+// ordered on the stream given at create, and nothing synchronizes with the host except create/destroy and calls made while profiling.
 //
 // Header-only: include it, link libmx_attn.so and the HIP runtime.
 #pragma once
@@ -31,6 +33,7 @@
 #include <memory>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "mx_attn.h"
 
@@ -82,6 +85,54 @@ public:
 private:
     void * ptr_ = nullptr;
     size_t bytes_ = 0;
+};
+
+// GPU time of one kind of call over a profiling pass (MetalLlamaDecoder::KernelTime, metal_llama_decoder.h:99).
+struct KernelTime {
+    std::string kind;
+    int32_t dispatches = 0;
+    double gpu_ms = 0.0;
+};
+
+// Per-kind timing of a decoder's calls, for profiling passes in the manner of the reference's after_dispatch
+// (metal_llama_decoder.mm:118-135) and cut (metal_whisper_decoder.mm:98-103): while a vector is attached, every call
+// is bracketed by two events on the decoder's stream and waited for (so it runs alone), and its time is added to its
+// kind's entry. Detached (the default) it creates no events and adds no waits.
+class DispatchTimer {
+public:
+    DispatchTimer() = default;
+    DispatchTimer(const DispatchTimer &) = delete;
+    DispatchTimer & operator=(const DispatchTimer &) = delete;
+    ~DispatchTimer() {
+        for (hipEvent_t e : ev_)
+            if (e) (void)hipEventDestroy(e);
+    }
+    void attach(std::vector<KernelTime> * out) { out_ = out; }
+    bool attached() const { return out_ != nullptr; }
+
+    template <class F> Status run(const char * kind, hipStream_t stream, F && call) {
+        if (!out_) return call();
+        for (hipEvent_t & e : ev_)
+            if (!e)
+                if (Status st = Status::hip(hipEventCreate(&e), "profiling event"); !st.is_ok()) return st;
+        if (Status st = Status::hip(hipEventRecord(ev_[0], stream), "profiling event"); !st.is_ok()) return st;
+        if (Status st = call(); !st.is_ok()) return st;
+        if (Status st = Status::hip(hipEventRecord(ev_[1], stream), "profiling event"); !st.is_ok()) return st;
+        if (Status st = Status::hip(hipEventSynchronize(ev_[1]), "profiling wait"); !st.is_ok()) return st;
+        float ms = 0.f;
+        if (Status st = Status::hip(hipEventElapsedTime(&ms, ev_[0], ev_[1]), "profiling time"); !st.is_ok()) return st;
+        auto it = std::find_if(out_->begin(), out_->end(), [&](const KernelTime & k) { return k.kind == kind; });
+        if (it == out_->end()) out_->push_back({kind, 1, (double)ms});
+        else {
+            it->dispatches++;
+            it->gpu_ms += ms;
+        }
+        return {};
+    }
+
+private:
+    std::vector<KernelTime> * out_ = nullptr;
+    hipEvent_t ev_[2] = {nullptr, nullptr};
 };
 
 // ---- llama / Qwen2 ----
@@ -137,6 +188,10 @@ public:
     }
 
     const LlamaAttentionConfig & config() const { return cfg_; }
+    // Profiling (null: off): the calls made meanwhile add their GPU time under "cache k/v" (append), "attention"
+    // (attention, decode_step) and "rope_store + attention" (prompt), as MetalLlamaDecoder::profile_pass reports by
+    // kind (metal_llama_decoder.mm:789-812).
+    void set_profile(std::vector<KernelTime> * out) { timer_.attach(out); }
     int32_t kv_width() const { return cfg_.n_head_kv * cfg_.head_dim; }
     int32_t q_width() const { return cfg_.n_head * cfg_.head_dim; }
     uint16_t * k_layer(int32_t l) const { return k_ + (size_t)l * cfg_.n_ctx * kv_width(); }
@@ -150,12 +205,14 @@ public:
             return {Code::InvalidArgument, "append: bad layer, rows, position or pointer"};
         if ((int64_t)p0 + M > cfg_.n_ctx) return {Code::ResourceExhausted, "append: the context would overflow"};
         const size_t w = (size_t)kv_width() * 2;
-        if (Status st = Status::hip(hipMemcpy2DAsync(k_layer(layer) + (size_t)p0 * kv_width(), w, k, (size_t)k_stride * 2, w, M,
-                                                     hipMemcpyDeviceToDevice, stream_), "append k");
-            !st.is_ok())
-            return st;
-        return Status::hip(hipMemcpy2DAsync(v_layer(layer) + (size_t)p0 * kv_width(), w, v, (size_t)v_stride * 2, w, M,
-                                            hipMemcpyDeviceToDevice, stream_), "append v");
+        return timer_.run("cache k/v", stream_, [&]() -> Status {
+            if (Status st = Status::hip(hipMemcpy2DAsync(k_layer(layer) + (size_t)p0 * kv_width(), w, k, (size_t)k_stride * 2, w,
+                                                         M, hipMemcpyDeviceToDevice, stream_), "append k");
+                !st.is_ok())
+                return st;
+            return Status::hip(hipMemcpy2DAsync(v_layer(layer) + (size_t)p0 * kv_width(), w, v, (size_t)v_stride * 2, w, M,
+                                                hipMemcpyDeviceToDevice, stream_), "append v");
+        });
     }
 
     // Attention of M query rows at positions p0 .. p0 + M - 1 of layer l over cache rows 0 .. p0 + M - 1 (already
@@ -173,12 +230,16 @@ public:
             mx_attn_desc d = desc(1, q_stride, out_stride);
             d.causal = 0;
             const int32_t n = p0 + 1;
-            return Status::from(mx_attn_decode(&d, 1, &n, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+            return timer_.run("attention", stream_, [&] {
+                return Status::from(mx_attn_decode(&d, 1, &n, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+            });
         }
         mx_attn_desc d = desc(M, q_stride, out_stride);
         d.p0 = p0;
         d.causal = 1;
-        return Status::from(mx_attn_prefill_ws(&d, q, k, v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        return timer_.run("attention", stream_, [&] {
+            return Status::from(mx_attn_prefill_ws(&d, q, k, v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        });
     }
 
     // A prompt chunk of M tokens at positions p0 .. p0 + M - 1 on the reference's buffers (rope_store + attention with
@@ -192,8 +253,10 @@ public:
         d.p0 = p0;
         d.causal = 1;
         const mx_attn_rope rope{cfg_.rope_neox ? 1 : 0, cfg_.rope_base};
-        return Status::from(mx_attn_prefill_rope_ws(&d, &rope, qkv, k_layer(layer), v_layer(layer), out, nullptr,
-                                                    ws_.data(), ws_.size(), stream_));
+        return timer_.run("rope_store + attention", stream_, [&] {
+            return Status::from(mx_attn_prefill_rope_ws(&d, &rope, qkv, k_layer(layer), v_layer(layer), out, nullptr,
+                                                        ws_.data(), ws_.size(), stream_));
+        });
     }
 
     // One decode step of layer l at position p, the reference's attention(enc, cache_off, 1, p, fused_rope = true)
@@ -210,7 +273,9 @@ public:
         const int32_t n = p + 1;
         uint16_t * k = k_layer(layer);
         uint16_t * v = v_layer(layer);
-        return Status::from(mx_attn_decode_rope(&d, &rope, 1, &n, qkv, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        return timer_.run("attention", stream_, [&] {
+            return Status::from(mx_attn_decode_rope(&d, &rope, 1, &n, qkv, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        });
     }
 
 private:
@@ -233,6 +298,7 @@ private:
     uint16_t * v_;
     hipStream_t stream_;
     Workspace ws_;
+    DispatchTimer timer_;
 };
 
 // ---- Whisper (MHA: n_head_kv = n_head, head_dim = n_state / n_head) ----
@@ -276,6 +342,9 @@ public:
     }
 
     int32_t head_dim() const { return cfg_.n_state / cfg_.n_head; }
+    // Profiling (null: off): the calls made meanwhile add their GPU time under "self attention" and "cross
+    // attention", the kinds MetalWhisperDecoder::profile_step reports (metal_whisper_decoder.mm:179, 218, 613-626).
+    void set_profile(std::vector<KernelTime> * out) { timer_.attach(out); }
     const WhisperAttentionConfig & config() const { return cfg_; }
     uint16_t * self_k(int32_t l) const { return sk_ + (size_t)l * cfg_.n_text_ctx * cfg_.n_state; }
     uint16_t * self_v(int32_t l) const { return sv_ + (size_t)l * cfg_.n_text_ctx * cfg_.n_state; }
@@ -309,7 +378,9 @@ public:
         const int32_t n = p + 1;
         uint16_t * k = self_k(layer);
         uint16_t * v = self_v(layer);
-        return Status::from(mx_attn_decode_rope(&d, &none, 1, &n, qkv, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        return timer_.run("self attention", stream_, [&] {
+            return Status::from(mx_attn_decode_rope(&d, &none, 1, &n, qkv, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        });
     }
     Status self_attention_prompt(int32_t layer, const float * qkv, float * out, int32_t p0, int32_t M) {
         if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
@@ -318,7 +389,9 @@ public:
         d.q_stride = 3 * cfg_.n_state;
         d.p0 = p0;
         const mx_attn_rope none{2, 0.f};
-        return Status::from(mx_attn_prefill_rope(&d, &none, qkv, self_k(layer), self_v(layer), out, nullptr, stream_));
+        return timer_.run("self attention", stream_, [&] {
+            return Status::from(mx_attn_prefill_rope(&d, &none, qkv, self_k(layer), self_v(layer), out, nullptr, stream_));
+        });
     }
     Status cross_attention(int32_t layer, const float * q, float * out, int32_t M) {
         if (layer < 0 || layer >= cfg_.n_layer) return {Code::InvalidArgument, "layer out of range"};
@@ -328,7 +401,9 @@ public:
         const int32_t n = cfg_.n_audio_ctx;
         const uint16_t * k = cross_k(layer);
         const uint16_t * v = cross_v(layer);
-        return Status::from(mx_attn_decode_f32(&d, 1, &n, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        return timer_.run("cross attention", stream_, [&] {
+            return Status::from(mx_attn_decode_f32(&d, 1, &n, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        });
     }
 
 private:
@@ -354,7 +429,9 @@ private:
         if (M < 1 || M > cfg_.max_rows) return {Code::InvalidArgument, "rows must be in [1, max_rows]"};
         mx_attn_desc d = desc(M, causal);
         if (cross) d.tuning = &cross_tuning_;
-        return Status::from(mx_attn_decode(&d, 1, &n_keys, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        return timer_.run(cross ? "cross attention" : "self attention", stream_, [&] {
+            return Status::from(mx_attn_decode(&d, 1, &n_keys, q, &k, &v, out, nullptr, ws_.data(), ws_.size(), stream_));
+        });
     }
     WhisperAttentionConfig cfg_;
     uint16_t * sk_;
@@ -364,6 +441,7 @@ private:
     hipStream_t stream_;
     mx_attn_tuning cross_tuning_;
     Workspace ws_;
+    DispatchTimer timer_;
 };
 
 }  // namespace dooms_amd

@@ -217,6 +217,69 @@ TEST(llama_f32_prompt_then_fused_decode_steps) {
     (void)hipFree(dout);
 }
 
+// Profiling by kind (profile_pass, metal_llama_decoder.mm:789-812): every call made while a vector is attached is
+// counted under its kind with a positive GPU time; detached, nothing more is recorded and results stay correct.
+TEST(profile_by_kind) {
+    using namespace dooms_amd;
+    const int n_ctx = 256, nh = 8, nkv = 2, hd = 128, qw = nh * hd, kw = nkv * hd, rw = qw + 2 * kw;
+    Dev kc((size_t)n_ctx * kw), vc((size_t)n_ctx * kw), dq((size_t)64 * qw), dout((size_t)64 * qw);
+    std::unique_ptr<LlamaAttention> attn;
+    EXPECT(LlamaAttention::create({1, n_ctx, nh, nkv, hd}, kc.p, vc.p, nullptr, attn).is_ok());
+    if (!attn) return;
+    float *dqkv = nullptr, *dof = nullptr;
+    HIP_OK(hipMalloc(&dqkv, (size_t)64 * rw * 4));
+    HIP_OK(hipMalloc(&dof, (size_t)64 * qw * 4));
+    HIP_OK(hipMemset(dqkv, 0, (size_t)64 * rw * 4));
+    HIP_OK(hipMemset(dq.p, 0, (size_t)64 * qw * 2));
+    std::vector<KernelTime> times;
+    attn->set_profile(&times);
+    EXPECT(attn->prompt(0, dqkv, dof, 64, 0).is_ok());
+    for (int p = 64; p < 67; p++) EXPECT(attn->decode_step(0, dqkv, dof, p).is_ok());
+    EXPECT(attn->append(0, kc.p, kw, vc.p, kw, 4, 67).is_ok());
+    EXPECT(attn->attention(0, dq.p, qw, dout.p, qw, 1, 70).is_ok());
+    auto find = [&](const char * kind) -> const KernelTime * {
+        for (const KernelTime & k : times)
+            if (k.kind == kind) return &k;
+        return nullptr;
+    };
+    const KernelTime * pr = find("rope_store + attention");
+    const KernelTime * at = find("attention");
+    const KernelTime * ca = find("cache k/v");
+    EXPECT(times.size() == 3);
+    EXPECT(pr && pr->dispatches == 1 && pr->gpu_ms > 0);
+    EXPECT(at && at->dispatches == 4 && at->gpu_ms > 0);
+    EXPECT(ca && ca->dispatches == 1 && ca->gpu_ms > 0);
+    attn->set_profile(nullptr);
+    EXPECT(attn->decode_step(0, dqkv, dof, 71).is_ok());
+    HIP_OK(hipDeviceSynchronize());
+    EXPECT(at && at->dispatches == 4);
+    // Whisper: self and cross kinds
+    const int ns = 256, wh = 4, n_audio = 96;
+    Dev sk((size_t)32 * ns), sv((size_t)32 * ns), ck((size_t)n_audio * ns), cv((size_t)n_audio * ns);
+    HIP_OK(hipMemset(ck.p, 0, (size_t)n_audio * ns * 2));
+    HIP_OK(hipMemset(cv.p, 0, (size_t)n_audio * ns * 2));
+    WhisperAttentionConfig wc{};
+    wc.n_layer = 1;
+    wc.n_state = ns;
+    wc.n_head = wh;
+    wc.n_text_ctx = 32;
+    wc.n_audio_ctx = n_audio;
+    wc.max_rows = 5;
+    std::unique_ptr<WhisperAttention> w;
+    EXPECT(WhisperAttention::create(wc, sk.p, sv.p, ck.p, cv.p, nullptr, w).is_ok());
+    if (!w) return;
+    std::vector<KernelTime> wt;
+    w->set_profile(&wt);
+    EXPECT(w->self_attention_prompt(0, dqkv, dof, 0, 3).is_ok());
+    EXPECT(w->self_attention(0, dqkv, dof, 3).is_ok());
+    EXPECT(w->cross_attention(0, dq.p, dout.p, 5).is_ok());
+    EXPECT(wt.size() == 2);
+    EXPECT(wt.size() == 2 && wt[0].kind == "self attention" && wt[0].dispatches == 2 && wt[0].gpu_ms > 0);
+    EXPECT(wt.size() == 2 && wt[1].kind == "cross attention" && wt[1].dispatches == 1 && wt[1].gpu_ms > 0);
+    (void)hipFree(dqkv);
+    (void)hipFree(dof);
+}
+
 TEST(llama_errors) {
     using namespace dooms_amd;
     Dev kc(1024), vc(1024);
