@@ -157,6 +157,18 @@ def test_gemm_w192_tiles_ragged(device):
     run(device, 12, 1900, 5700, 96, accumulate=True, rows=[0, 1, 255, 256, 1023, 1536, 1791, 1792, 1899])
 
 
+@pytest.mark.parametrize("K", [64, 192, 320])
+@pytest.mark.parametrize("M,N,opts", [
+    (1300, 8300, dict(norm=True, bias=True, accumulate=True)),  # 256 x 256 tiles
+    (1900, 3896, dict(bias=True, out_f16=True)),                # 256 x 128 tiles
+    (1900, 5700, dict(accumulate=True)),                        # 256 x 192 tiles
+])
+def test_gemm_tiles_ragged_k64_steps(device, M, N, opts, K):
+    """The same ragged products with K a multiple of 64, which the tiled GEMMs walk in steps of 64 columns through
+    two LDS buffers: one step, three and five (the buffer ring wrapping at an odd count)."""
+    run(device, 13 + K, M, N, K, rows=[0, 1, 255, 256, 1023, 1024, M - 2, M - 1], **opts)
+
+
 def test_gemm_llama3_attn_output_chunk(device):
     run(device, 7, 300, 4096, 4096, accumulate=True, rows=[0, 1, 127, 128, 255, 299])
 
