@@ -249,6 +249,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     asm volatile("" : "+s"(seq_k), "+s"(seq_v), "+s"(L), "+s"(n_split), "+s"(T), "+s"(max_split), "+s"(n_head_kv),
                  "+s"(chunk), "+s"(G), "+s"(seq0), "+s"(n_q), "+s"(rows), "+s"(causal), "+s"(xcd_heads), "+s"(q_stride),
                  "+s"(kv_stride), "+s"(qp));
+    // fused step: this thread's rotary frequency (threads 0 .. HD / 2 - 1 use theirs) as one vector load of the
+    // kernel arguments, issued before the first K/V block so that it returns ahead of it (loads return in order) and
+    // is waited for with the new key and value. As uniform-index scalar loads the compiler issued them after the block
+    // and waited for them behind the whole chip's burst; pinned here as scalar loads they took three dependent batches.
+    float freq = 0.f;
+    if constexpr (F32) freq = p.rope_freq[threadIdx.x % (HD / 2)];
 
     // Work item. The row tiles of one (sequence, kv head, split) read the same keys and values, so they run as
     // consecutive workgroups of one XCD (workgroups are dealt to the 8 XCDs round-robin: ids 8 apart share one), where
@@ -325,9 +331,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     const bool wave_new = F32 && p.append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % NW == wave;
     const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
     const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
-    // The fused step's own loads (the new key and value, the rotary frequencies) go out before the first block of keys
+    // The fused step's own loads (the new key and value) go out before the first block of keys
     // and values: a wait for them then leaves that block's loads in flight (loads complete in the order issued).
-    float x[F32 ? KS : 1][8], xv[8], freq = 0.f;
+    float x[F32 ? KS : 1][8], xv[8];
     if constexpr (F32) {
         const float * row = p.qkv + seq_row0 * p.q_stride;
         if (k_lane_new) {
@@ -336,11 +342,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
             for (int ks = 0; ks < KS; ks++) load8f(kr + 32 * ks, x[ks]);
         }
         if (v_lane_new) load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, xv);
-        // uniform indices: scalar loads from the kernel arguments (an index per lane would make it a vector load,
-        // which waits behind the whole chip's K/V burst)
-#pragma unroll
-        for (int i = 0; i < HD / 2; i++)
-            if (threadIdx.x == i) freq = p.rope_freq[i];
     }
 
     // the first block of keys and values goes out right behind the query (unconditionally: keys past the split are
@@ -359,7 +360,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (F32) {
-        // the new key and value are used only from here on, so any wait for them leaves the block's loads in flight
+        // the new key and value (and the frequency) are used only from here on, so any wait for them leaves the block's
+        // loads in flight
+        asm volatile("" : "+v"(freq)::"memory");
 #pragma unroll
         for (int e = 0; e < 8; e++) asm volatile("" : "+v"(xv[e])::"memory");
 #pragma unroll
