@@ -136,6 +136,45 @@ __device__ __forceinline__ void store_y(const LinearParams & p, int mi, int m, i
     }
 }
 
+// Epilogue of the tiled GEMMs: the lane's 16 outputs of column n of an MFMA tile (rows mbase + 8 (v / 4) + v % 4),
+// y (+)= acc (+ bias), the same sums as store_y. The bias and the previous outputs are all loaded before the first
+// store: a store to y may alias them as far as the compiler can tell, so with loads and stores interleaved each
+// element waited for one or two memory round trips in turn. Rows past M read row M - 1 (a valid address) and store
+// nothing.
+template <bool OUT16>
+__device__ __forceinline__ void store_col16(const LinearParams & p, int mi, int n, int mbase, const float16_t & acc) {
+    const float * b = (p.flags & kLinearBias) ? p.bias[mi] : nullptr;
+    const float bv = b ? b[n] : 0.f;
+    const bool accum = p.flags & kLinearAccumulate;
+    float prev[16];
+    if (accum) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = min(mbase + 8 * (v / 4) + v % 4, p.M - 1);
+            const int64_t o = (int64_t)m * p.y_stride + n;
+            if constexpr (OUT16) prev[v] = (float)static_cast<const half_t *>(p.y[mi])[o];
+            else prev[v] = static_cast<const float *>(p.y[mi])[o];
+        }
+    }
+    // every sum before the first store, so that no loaded value is used behind a store (the compiler's waits at the
+    // stores' branches would otherwise drain the stores before it)
+    float x[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        x[v] = acc[v];
+        if (b) x[v] += bv;
+        if (accum) x[v] += prev[v];
+    }
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int m = mbase + 8 * (v / 4) + v % 4;
+        if (m >= p.M) continue;
+        const int64_t o = (int64_t)m * p.y_stride + n;
+        if constexpr (OUT16) static_cast<half_t *>(p.y[mi])[o] = (half_t)x[v];
+        else static_cast<float *>(p.y[mi])[o] = x[v];
+    }
+}
+
 // ---- M <= 8: f32 input rows in LDS, 4 weight rows per wave ----
 constexpr int kGemvRows = 4;       // weight rows per wave
 constexpr int kGemvMaxWaves = 8;   // waves per workgroup (the launch sizes workgroups so that each CU gets one)
@@ -411,12 +450,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(LinearParams p) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int n = n0 + 64 * wn + 32 * j + l32;
-            if (n >= p.N) continue;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int m = m0 + 64 * wm + 32 * i + 8 * (v / 4) + 4 * hi + v % 4;
-                if (m < p.M) store_y<OUT16>(p, mi, m, n, acc[i][j][v]);
-            }
+            if (n < p.N) store_col16<OUT16>(p, mi, n, m0 + 64 * wm + 32 * i + 4 * hi, acc[i][j]);
         }
 }
 
@@ -620,12 +654,7 @@ __device__ __forceinline__ void gemm_big_tile(const LinearParams & p) {
 #pragma unroll
         for (int j = 0; j < kBigNJ; j++) {
             const int n = n0 + WC * wn + 32 * j + l32;
-            if (n >= p.N) continue;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int m = m0 + (kBM / WM) * wm + 32 * i + 8 * (v / 4) + 4 * hi + v % 4;
-                if (m < p.M) store_y<OUT16>(p, mi, m, n, acc[i][j][v]);
-            }
+            if (n < p.N) store_col16<OUT16>(p, mi, n, m0 + (kBM / WM) * wm + 32 * i + 4 * hi, acc[i][j]);
         }
 }
 
