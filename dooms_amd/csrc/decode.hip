@@ -106,7 +106,7 @@ __device__ __forceinline__ void store_pair(const DecodeParams & p, int64_t off, 
 // keys 33.6 -> 32.7 us, 1024 keys 7.07 -> 7.00 us). The head-dim-64 kernels keep the per-pair merge: there the path's
 // registers cost a wave of occupancy (112 -> 136 VGPRs), +0.4 us on Qwen2.5-0.5B and the Whisper shapes; head dim 256
 // has no registers to spare.
-template <int HD, int RT, bool F32, int NW, size_t LDS_BYTES>
+template <int HD, int RT, bool F32, int NW, size_t LDS_BYTES, int MCR>
 __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float * part_tile, int ns, int rt, int g, int G,
                                            int64_t seq_row0, char * lds) {
     constexpr int kThreads = NW * kWave;
@@ -114,7 +114,10 @@ __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float *
     constexpr int NC = RT * HD / 4;                         // float4 columns of the tile
     constexpr int SF = kThreads >= NC ? kThreads / NC : 1;  // threads per column (stripes of the splits)
     constexpr int CPT = NC > kThreads ? NC / kThreads : 1;  // columns per thread
-    constexpr int MC = 16 / CPT > 0 ? 16 / CPT : 1;         // splits of each column loaded per round
+    // splits of each column loaded per round: MCR (the caller's choice, enough to cover the tile's splits in one
+    // round where the registers allow) up to 16 / CPT. A round that covered 64 split slots for at most 32 splits
+    // loaded each column of the last split up to 32 times over (clamped addresses), doubling the merging CU's bytes.
+    constexpr int MC = (16 / CPT > 0 ? 16 / CPT : 1) < MCR ? (16 / CPT > 0 ? 16 / CPT : 1) : MCR;
     constexpr int NPAIR = kMaxSplitsPerTile * RT;           // weight slots: [split][row]
     constexpr int RPW = (RT + NW - 1) / NW;                 // rows per wave for the (m, l) reductions
     static_assert(kMaxSplitsPerTile <= kWave, "one lane per split");
@@ -577,7 +580,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     const int ns = n_split;
     if constexpr (HD == 128) {
         if (ns > 1) {
-            merge_wide<HD, RT, F32, NW, sizeof s_v>(p, part_tile, ns, rt, g, G, seq_row0, reinterpret_cast<char *>(s_v));
+            // the smallest round (splits per column and stripe) that covers the tile's splits
+            constexpr int SFW = NW * kWave >= RT * HD / 4 ? NW * kWave / (RT * HD / 4) : 1;
+            char * lds = reinterpret_cast<char *>(s_v);
+            if (ns <= 2 * SFW) merge_wide<HD, RT, F32, NW, sizeof s_v, 2>(p, part_tile, ns, rt, g, G, seq_row0, lds);
+            else if (ns <= 4 * SFW) merge_wide<HD, RT, F32, NW, sizeof s_v, 4>(p, part_tile, ns, rt, g, G, seq_row0, lds);
+            else if (ns <= 8 * SFW) merge_wide<HD, RT, F32, NW, sizeof s_v, 8>(p, part_tile, ns, rt, g, G, seq_row0, lds);
+            else merge_wide<HD, RT, F32, NW, sizeof s_v, 16>(p, part_tile, ns, rt, g, G, seq_row0, lds);
             if (threadIdx.x == 0)
                 __hip_atomic_store(p.counters + tile * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef MX_ATTN_TRACE
