@@ -78,6 +78,15 @@ def summarize(path, kernel, last):
         for c in sel[0][1]:
             vals = [v[c] for _, v in sel]
             print(f"  {c}: avg {sum(vals) / len(vals):.2f}  min {min(vals):.2f}  max {max(vals):.2f}")
+        ts = {}
+        for r in rows:
+            if "Start_Timestamp" in r and "End_Timestamp" in r:
+                ts[(r["Dispatch_Id"], r["Kernel_Name"])] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        if "GRBM_GUI_ACTIVE" in sel[0][1] and ts:
+            # GRBM_GUI_ACTIVE sums the busy cycles of the 8 XCDs: cycles per XCD / duration is the shader clock
+            cyc = sum(v["GRBM_GUI_ACTIVE"] / 8 for _, v in sel)
+            ns = sum(ts[k] for k, _ in sel)
+            print(f"  clock over the summarized dispatches (GRBM_GUI_ACTIVE / 8 / duration): {cyc / ns:.3f} GHz")
         if copies:
             for c in copies[-1]:
                 print(f"  copyBuffer (1 GiB copy of the same run) {c}: {copies[-1][c]:.2f}")
@@ -126,6 +135,19 @@ def measured_traffic(key):
             return json.load(f)["workloads"][key]["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def measured_clock(key):
+    """The shader clock (GHz) that a rocprofv3 --pmc GRBM_GUI_ACTIVE run measured over a headline kernel's timed
+    dispatches, as committed in profiles/clock.json (with the command), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "clock.json")) as f:
+            return json.load(f)["workloads"][key]["clock_GHz"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+PEAK_CLOCK_GHZ = 2.4  # the engine clock MI355X's published dense f16 peak assumes
 
 
 def decode_bytes(L, n_head, n_kv, hd):
@@ -241,10 +263,9 @@ class PrefillProblem:
 class LinearProblem:
     """mx_linear launches over `layers` distinct weight sets (so that weights stream from HBM), one input."""
 
-    def __init__(self, torch, gen, M, N, K, flags, layers, count=1, plan=False):
+    def __init__(self, torch, gen, M, N, K, flags, layers, count=1):
         from dooms_amd import _lib
         self.torch, self._lib = torch, _lib
-        self.plan = None
         self.M, self.N, self.K, self.flags, self.layers, self.count = M, N, K, flags, layers, count
         dev = "cuda"
         self.x = torch.randn(M, K, generator=gen, device=dev)
@@ -258,23 +279,11 @@ class LinearProblem:
         nb = _lib.linear_workspace_bytes(self.desc)
         self.ws = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
         self.nb = nb
-        if plan:  # mx_linear_plan (hipBLASLt), made here, outside the timed region
-            self.plan = _lib.linear_plan_create(self.desc)
-
-    def __del__(self):
-        if self.plan:
-            self._lib.linear_plan_destroy(self.plan)
 
     def step(self):
         _lib = self._lib
         stream = self.torch.cuda.current_stream().cuda_stream
         for l in range(self.layers):
-            if self.plan:
-                _lib.check(_lib.linear_plan_run(self.plan, self.w[l][0].data_ptr(), self.x.data_ptr(),
-                                                self.y[0].data_ptr(), self.gamma.data_ptr(),
-                                                self.bias[0].data_ptr() if self.flags & _lib.LINEAR_BIAS else 0,
-                                                self.ws.data_ptr(), self.nb, stream))
-                continue
             _lib.check(_lib.linear_raw(self.desc, [w.data_ptr() for w in self.w[l]], self.x.data_ptr(),
                                        [y.data_ptr() for y in self.y], self.gamma.data_ptr(),
                                        [b.data_ptr() for b in self.bias] if self.flags & _lib.LINEAR_BIAS else None,
@@ -533,7 +542,9 @@ def main():
             "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,4,false,8>", "achieved": round(achieved, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic, "bytes_per_launch": bpl, "avg_launch_us": round(avg_us, 3),
-                         "launch_timing": "graph-timed region / launches (includes the gaps between launches)"},
+                         "launch_timing": "graph-timed region / launches (includes the gaps between launches)",
+                         "copy_GBps": extra["copy_GBps"], "frac_of_copy": round(achieved / extra["copy_GBps"], 4),
+                         "copy_note": "same-run 1 GiB device-to-device copy (read + write bytes / time)"},
         })
         if not args.no_cpu:
             v1, n1, t1 = cpu_decode_baseline(torch, dp, args.cpu_seconds, threads)
@@ -613,6 +624,14 @@ def main():
                             "traffic": measured_traffic("prefill_qwen7b_32k"), "avg_launch_us": round(avg_us, 2),
                             "launch_timing": "graph-timed region / launches; FLOPs per launch differ by chunk, so "
                                              "achieved = all FLOPs / all launch time"}}
+        clk = measured_clock("prefill_qwen7b_32k")
+        if clk:
+            # the same peak at the shader clock the chip holds under this load (published peak x clock / 2.4 GHz)
+            pk = F16_PEAK_TFLOPS * clk / PEAK_CLOCK_GHZ
+            pre["roofline"].update({"clock_GHz": clk, "peak_at_clock": round(pk, 1),
+                                    "frac_at_clock": round(tflops / pk, 4)})
+        pre["roofline"]["same_run_gemm_TFLOPs"] = extra["f16_gemm_8192_TFLOPs"]
+        pre["roofline"]["frac_of_same_run_gemm"] = round(tflops / extra["f16_gemm_8192_TFLOPs"], 4)
         if not args.no_cpu:
             v1, rows, t1 = cpu_prefill_baseline(torch, pp, args.cpu_seconds, threads)
             pre["cpu_baseline"] = {"value": round(v1, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
@@ -668,18 +687,15 @@ def main():
         # ---- the projections either side of the attention (mx_linear): Llama-3-8B shapes, Whisper cross cache ----
         from dooms_amd import _lib as L
         lin = {}
-        # kernel: which code produced the figure ("gemv_kernel" / "stage_kernel + gemm_*kernel": this library's, the
-        # mx_linear path; "stage_kernel + hipBLASLt": an mx_linear_plan, the vendor GEMM chosen at plan creation)
-        for name, M, N, Kd, flags, layers, count, plan, kernel in [
-                ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1, False, "gemv_kernel"),
-                ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1, False, "gemv_kernel"),
-                ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, False,
+        # kernel: this library's kernels that produced the figure (mx_linear loads no vendor GEMM library)
+        for name, M, N, Kd, flags, layers, count, kernel in [
+                ("gemv_qkv_llama3_8b", 1, 6144, 4096, L.LINEAR_RMS_NORM, 32, 1, "gemv_kernel"),
+                ("gemv_attn_output_llama3_8b", 1, 4096, 4096, L.LINEAR_ACCUMULATE, 32, 1, "gemv_kernel"),
+                ("gemm_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1,
                  "stage_kernel + gemm_w192_kernel"),
-                ("plan_qkv_llama3_8b_chunk2048", 2048, 6144, 4096, L.LINEAR_RMS_NORM, 4, 1, True,
-                 "stage_kernel + hipBLASLt (mx_linear_plan)"),
-                ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8, False,
+                ("whisper_cross_kv_1500x1280_4layers", 1500, 1280, 1280, L.LINEAR_OUT_F16 | L.LINEAR_BIAS, 1, 8,
                  "stage_kernel + gemm_big_kernel")]:
-            lp = LinearProblem(torch, gen, M, N, Kd, flags, layers, count, plan=plan)
+            lp = LinearProblem(torch, gen, M, N, Kd, flags, layers, count)
             ms_l, _ = time_graph(torch, lp.step, max(5, K), max(1, W))
             us = ms_l * 1e3 / layers
             e = {"M": M, "N": N, "K": Kd, "count": count, "kernel": kernel, "us_per_launch": round(us, 2)}
@@ -694,6 +710,22 @@ def main():
             lin[name] = e
             del lp
             torch.cuda.empty_cache()
+        # the vendor GEMM on the same chunk shape for comparison only (torch.matmul -> hipBLASLt, f16 in and out, no
+        # norm or staging): not part of this library
+        xa = torch.randn(2048, 4096, generator=gen, device="cuda").half()
+        wv = [torch.randn(6144, 4096, generator=gen, device="cuda").half() for _ in range(4)]
+        yv = torch.empty(2048, 6144, dtype=torch.float16, device="cuda")
+
+        def vendor_step():
+            for w_ in wv:
+                torch.matmul(xa, w_.t(), out=yv)
+        ms_v, _ = time_graph(torch, vendor_step, max(5, K), max(1, W))
+        us_v = ms_v * 1e3 / len(wv)
+        lin["vendor_torch_matmul_qkv_chunk2048"] = {
+            "M": 2048, "N": 6144, "K": 4096, "us_per_launch": round(us_v, 2),
+            "TFLOPs": round(2 * 2048 * 6144 * 4096 / (us_v * 1e-6) / 1e12, 1),
+            "note": "torch.matmul (hipBLASLt) on f16 operands of the same shape, for comparison; not this library"}
+        del xa, wv, yv
         extra["linear"] = lin
 
     if args.only in ("self-attention", "all"):

@@ -23,7 +23,6 @@ CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", UNSUPPORTED: "UNSU
 EXPORTS = ("mx_attn_abi_version", "mx_attn_last_error", "mx_attn_prefill", "mx_attn_prefill_ws",
            "mx_attn_prefill_workspace_bytes", "mx_attn_prefill_rope", "mx_attn_prefill_rope_ws", "mx_attn_decode",
            "mx_attn_decode_f32", "mx_attn_decode_noalloc", "mx_attn_decode_rope", "mx_linear", "mx_linear_workspace_bytes",
-           "mx_linear_plan_create", "mx_linear_plan_run", "mx_linear_plan_destroy",
            "mx_attn_decode_workspace_bytes", "mx_attn_decode_workspace_init", "mx_self_attention",
            "mx_self_attention_workspace_bytes")
 
@@ -123,12 +122,6 @@ def lib() -> ctypes.CDLL:
         L.mx_linear.restype = ctypes.c_int32
         L.mx_linear.argtypes = [ctypes.POINTER(MxLinearDesc), ctypes.c_int32, ctypes.POINTER(P), P, ctypes.POINTER(P),
                                 P, ctypes.POINTER(P), P, ctypes.c_size_t, P]
-        L.mx_linear_plan_create.restype = ctypes.c_int32
-        L.mx_linear_plan_create.argtypes = [ctypes.POINTER(MxLinearDesc), ctypes.POINTER(P)]
-        L.mx_linear_plan_run.restype = ctypes.c_int32
-        L.mx_linear_plan_run.argtypes = [P, P, P, P, P, P, P, ctypes.c_size_t, P]
-        L.mx_linear_plan_destroy.restype = None
-        L.mx_linear_plan_destroy.argtypes = [P]
         L.mx_attn_decode_workspace_bytes.restype = ctypes.c_size_t
         L.mx_attn_decode_workspace_bytes.argtypes = [ctypes.POINTER(MxAttnDesc), ctypes.c_int32, ctypes.c_int32]
         L.mx_attn_decode_workspace_init.restype = ctypes.c_int32
@@ -276,18 +269,3 @@ def self_attention_raw(desc: MxSelfAttnDesc, qkv: int, y: int, ws: int, ws_bytes
     """mx_self_attention on raw device addresses; returns the code."""
     return lib().mx_self_attention(ctypes.byref(desc), qkv, y, ws or None, ws_bytes, stream or None)
 
-
-def linear_plan_create(desc: MxLinearDesc) -> int:
-    """mx_linear_plan_create; returns the plan handle (raises MxAttnError)."""
-    h = ctypes.c_void_p()
-    check(lib().mx_linear_plan_create(ctypes.byref(desc), ctypes.byref(h)))
-    return h.value
-
-
-def linear_plan_run(plan: int, w: int, x: int, y: int, gamma: int, bias: int, ws: int, ws_bytes: int,
-                    stream: int) -> int:
-    return lib().mx_linear_plan_run(plan, w, x, y, gamma or None, bias or None, ws or None, ws_bytes, stream or None)
-
-
-def linear_plan_destroy(plan: int) -> None:
-    lib().mx_linear_plan_destroy(plan)

@@ -225,39 +225,6 @@ def linear(x, weights, *, out=None, gamma=None, bias=None, eps=1e-5, accumulate=
     return outs[0] if single else outs
 
 
-class LinearPlan:
-    """mx_linear_plan_*: a hipBLASLt GEMM plan for one prompt-chunk projection shape (M > 8, one matrix), made here
-    (loading hipBLASLt, choosing its algorithm); run() then only stages the input and enqueues the product."""
-
-    def __init__(self, M, N, K, *, norm=False, bias=False, accumulate=False, out_f16=False, x_stride=None,
-                 y_stride=None, eps=1e-5):
-        flags = ((_lib.LINEAR_RMS_NORM if norm else 0) | (_lib.LINEAR_ACCUMULATE if accumulate else 0) |
-                 (_lib.LINEAR_BIAS if bias else 0) | (_lib.LINEAR_OUT_F16 if out_f16 else 0))
-        self.desc = _lib.MxLinearDesc(M=M, N=N, K=K, flags=flags, x_stride=K if x_stride is None else x_stride,
-                                      y_stride=N if y_stride is None else y_stride, eps=eps, reserved=0)
-        self.handle = None
-        self.handle = _lib.linear_plan_create(self.desc)
-        self.ws_bytes = _lib.linear_workspace_bytes(self.desc)
-        self.out_f16 = out_f16
-
-    def run(self, x, w, out, gamma=None, bias=None, workspace=None):
-        d = self.desc
-        if x.shape[0] != d.M or x.stride(0) != d.x_stride or out.stride(0) != d.y_stride or tuple(w.shape) != (d.N, d.K):
-            raise ValueError("tensors do not match the plan's shape")
-        ws = workspace if workspace is not None else torch.empty(max(self.ws_bytes, 256), dtype=torch.uint8,
-                                                                 device=x.device)
-        _lib.check(_lib.linear_plan_run(self.handle, w.data_ptr(), x.data_ptr(), out.data_ptr(),
-                                        gamma.data_ptr() if gamma is not None else 0,
-                                        bias.data_ptr() if bias is not None else 0, ws.data_ptr(), ws.numel(),
-                                        _stream()))
-        return out
-
-    def __del__(self):
-        if self.handle:
-            _lib.linear_plan_destroy(self.handle)
-            self.handle = None
-
-
 _SA_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
 
 

@@ -7,7 +7,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libmx_attn.so")
-SOURCES = ["api.hip", "decode.hip", "prefill.hip", "rope.hip", "small.hip", "linear.hip", "linear_plan.hip"]
+SOURCES = ["api.hip", "decode.hip", "prefill.hip", "rope.hip", "small.hip", "linear.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops off: the compiler must not emit packed f32 arithmetic (its host pass warns that it does not know
@@ -41,7 +41,7 @@ def build(verbose: bool = False, out: str = LIB, defines=()) -> str:
     msgs = "\n".join(m for _, m in results if m.strip())
     if any(rc != 0 for rc, _ in results):
         raise RuntimeError(f"hipcc failed:\n{msgs}")
-    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-ldl", "-o", out + ".tmp"])
+    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", out + ".tmp"])
     if rc != 0:
         raise RuntimeError(f"link failed ({rc}):\n{msg}")
     if verbose and (msgs + msg).strip():
@@ -103,7 +103,7 @@ def build_sanitized_abi_check() -> str:
     if any(rc != 0 for rc, _ in results):
         raise RuntimeError("hipcc failed:\n" + "\n".join(m for _, m in results))
     exe = os.path.join(SAN_DIR, "abi_checks_sanitized")
-    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-fsanitize=address,undefined", *objs, dobj, "-ldl", "-o", exe])
+    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-fsanitize=address,undefined", *objs, dobj, "-o", exe])
     if rc != 0:
         raise RuntimeError(f"link failed ({rc}):\n{msg}")
     return exe

@@ -362,18 +362,17 @@ int32_t check_rope(const mx_attn_desc & d, const mx_attn_rope * rope) {
     return MX_ATTN_OK;
 }
 
-// Shared by mx_attn_decode (half q rows and output), mx_attn_decode_f32 (f32 q rows and output) and
-// mx_attn_decode_rope (f32 q|k|v rows and output, the new token's key and value appended to the caches by the kernel).
-int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const void * q,
-                    const void * const * k_caches, const void * const * v_caches, void * out, float * lse,
-                    void * workspace, size_t ws_bytes, mx_attn_stream stream, const mx_attn_rope * rope, bool f32) {
+// The decode entry points' checks of everything but the workspace (the descriptor and batch already checked): pointers,
+// alignment, every kv_len, and whether a launch holds one sequence's rows. Sets max_len, the longest kv_len.
+int32_t check_decode_args(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const void * q,
+                          const void * const * k_caches, const void * const * v_caches, const void * out,
+                          const float * lse, int32_t & max_len) {
     const mx_attn_desc & d = *desc;
-
     if (!kv_len || !k_caches || !v_caches) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len, k_caches and v_caches must not be null");
     if (!q || !out) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must not be null");
     if (!aligned16(q) || !aligned16(out)) return fail(MX_ATTN_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
     if (lse && (reinterpret_cast<uintptr_t>(lse) & 3u)) return fail(MX_ATTN_INVALID_ARGUMENT, "lse must be 4-byte aligned");
-    int32_t max_len = 0;
+    max_len = 0;
     for (int32_t b = 0; b < batch; b++) {
         const int32_t n = kv_len[b];
         if (n < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len[%d] = %d: every sequence needs at least one key", b, n);
@@ -384,6 +383,20 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
             return fail(MX_ATTN_INVALID_ARGUMENT, "cache pointers of sequence %d must be 16-byte aligned", b);
         max_len = std::max(max_len, n);
     }
+    if (d.head_dim >= kMfmaMinHeadDim && decode_seqs_per_launch(desc, decode_shape(desc).n_rowtiles) < 1)
+        return fail(MX_ATTN_UNSUPPORTED, "n_head * n_q (%lld query rows per sequence) is too large for one decode launch",
+                    (long long)d.n_head * d.n_q);
+    return MX_ATTN_OK;
+}
+
+// Shared by mx_attn_decode (half q rows and output), mx_attn_decode_f32 (f32 q rows and output) and
+// mx_attn_decode_rope (f32 q|k|v rows and output, the new token's key and value appended to the caches by the kernel).
+int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv_len, const void * q,
+                    const void * const * k_caches, const void * const * v_caches, void * out, float * lse,
+                    void * workspace, size_t ws_bytes, mx_attn_stream stream, const mx_attn_rope * rope, bool f32) {
+    const mx_attn_desc & d = *desc;
+    int32_t max_len = 0;
+    if (int32_t rc = check_decode_args(desc, batch, kv_len, q, k_caches, v_caches, out, lse, max_len)) return rc;
     const size_t need = decode_ws_bytes(desc, batch, max_len);
     if (need > 0 && !workspace) return fail(MX_ATTN_INVALID_ARGUMENT, "workspace is null but %zu bytes are needed", need);
     if (ws_bytes < need) return fail(MX_ATTN_RESOURCE_EXHAUSTED, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
@@ -413,10 +426,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
     }
     // one launch holds at most kMaxTilesPerLaunch (sequence, kv head, row tile) tiles (so its 1-D grid of up to 32
     // splits per tile stays far inside the grid's range)
-    const int32_t seq_per_launch = (int32_t)decode_seqs_per_launch(desc, s.n_rowtiles);
-    if (seq_per_launch < 1)
-        return fail(MX_ATTN_UNSUPPORTED, "n_head * n_q (%lld query rows per sequence) is too large for one decode launch",
-                    (long long)d.n_head * d.n_q);
+    const int32_t seq_per_launch = (int32_t)decode_seqs_per_launch(desc, s.n_rowtiles);  // >= 1: checked above
     const hipStream_t st = static_cast<hipStream_t>(stream);
     for (int32_t b0 = 0; b0 < batch; b0 += seq_per_launch) {
         const int n_seq = std::min<int32_t>(seq_per_launch, batch - b0);
@@ -648,12 +658,6 @@ int32_t linear_params(const mx_linear_desc * desc, int32_t count, const uint16_t
 
 }  // namespace
 
-// A library GEMM plan (include/mx_linear.h): the descriptor it was made for and its hipBLASLt objects.
-struct mx_linear_plan {
-    mx_linear_desc desc;
-    mx::BlasPlan * blas;
-};
-
 extern "C" {
 
 MX_ATTN_API size_t mx_self_attention_workspace_bytes(const mx_self_attn_desc * desc) {
@@ -881,9 +885,11 @@ MX_ATTN_API int32_t mx_attn_decode_noalloc(const mx_attn_desc * desc, int32_t ba
     if (int32_t rc = check_desc(desc)) return rc;
     if (batch < 1) return fail(MX_ATTN_INVALID_ARGUMENT, "batch (%d) must be >= 1", batch);
     if (desc->n_q == 0) return MX_ATTN_OK;
-    if (!kv_len) return fail(MX_ATTN_INVALID_ARGUMENT, "kv_len must not be null");
+    // every argument check of mx_attn_decode first, so that a call refused for its arguments enqueues nothing
     int32_t max_len = 0;
-    for (int32_t b = 0; b < batch; b++) max_len = std::max(max_len, kv_len[b]);
+    if (int32_t rc = check_decode_args(desc, batch, kv_len, q, reinterpret_cast<const void * const *>(k_caches),
+                                       reinterpret_cast<const void * const *>(v_caches), out, lse, max_len))
+        return rc;
     const size_t need = decode_ws_bytes(desc, batch, max_len);
     if (need > kScratchBytes)
         return fail(MX_ATTN_RESOURCE_EXHAUSTED,
@@ -938,51 +944,6 @@ MX_ATTN_API int32_t mx_linear(const mx_linear_desc * desc, int32_t count, const 
     if (int32_t rc = linear_params(desc, count, W, X, Y, gamma, bias, workspace, ws_bytes, p)) return rc;
     if (desc->M == 0) return MX_ATTN_OK;
     return hip_status(mx::launch_linear(p, static_cast<hipStream_t>(stream)), "linear launch");
-}
-
-MX_ATTN_API int32_t mx_linear_plan_create(const mx_linear_desc * desc, mx_linear_plan ** plan) {
-    if (!plan) return fail(MX_ATTN_INVALID_ARGUMENT, "plan is null");
-    *plan = nullptr;
-    if (int32_t rc = check_linear_desc(desc, 1)) return rc;
-    if (desc->M <= mx::kLinearGemvMaxRows)
-        return fail(MX_ATTN_INVALID_ARGUMENT, "a plan is for prompt chunks (M > %d, got %d): mx_linear runs fewer rows",
-                    mx::kLinearGemvMaxRows, desc->M);
-    int dev = 0;
-    if (int32_t rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
-    mx::LinearParams shape{};
-    shape.M = desc->M;
-    shape.N = desc->N;
-    shape.K = desc->K;
-    shape.count = 1;
-    shape.flags = desc->flags;
-    shape.x_stride = desc->x_stride;
-    shape.y_stride = desc->y_stride;
-    std::string err;
-    mx::BlasPlan * b = mx::blas_plan_create(shape, dev, err);
-    if (!b) return fail(MX_ATTN_UNSUPPORTED, "linear plan: %s", err.c_str());
-    *plan = new mx_linear_plan{*desc, b};
-    return MX_ATTN_OK;
-}
-
-MX_ATTN_API void mx_linear_plan_destroy(mx_linear_plan * plan) {
-    if (!plan) return;
-    mx::blas_plan_destroy(plan->blas);
-    delete plan;
-}
-
-MX_ATTN_API int32_t mx_linear_plan_run(mx_linear_plan * plan, const uint16_t * W, const float * X, void * Y,
-                                       const float * gamma, const float * bias, void * workspace, size_t ws_bytes,
-                                       mx_attn_stream stream) {
-    if (!plan) return fail(MX_ATTN_INVALID_ARGUMENT, "plan is null");
-    int dev = 0;
-    if (int32_t rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
-    if (dev != mx::blas_plan_device(plan->blas))
-        return fail(MX_ATTN_INVALID_ARGUMENT, "the plan belongs to device %d, the current device is %d",
-                    mx::blas_plan_device(plan->blas), dev);
-    mx::LinearParams p;
-    if (int32_t rc = linear_params(&plan->desc, 1, &W, X, &Y, gamma, bias ? &bias : nullptr, workspace, ws_bytes, p))
-        return rc;
-    return hip_status(mx::blas_plan_run(plan->blas, p, static_cast<hipStream_t>(stream)), "linear plan run");
 }
 
 }  // extern "C"

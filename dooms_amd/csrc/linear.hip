@@ -20,8 +20,7 @@
 //     consecutive rows hit 16 distinct 4-bank groups), the step after next loading while the current step multiplies.
 //     Each wave owns a 64 x 64 block (2 x 2 MFMA tiles); two workgroups per CU.
 //   * Several matrices with the same input and shape (the cross cache's K and V of every layer) run in one launch.
-//   * mx_linear runs these kernels only. A caller may instead create a plan (linear_plan.hip) that runs a single matrix's
-//     GEMM after the staging on hipBLASLt, chosen and set up at create time.
+//   * mx_linear runs these kernels only: no vendor GEMM library is loaded or linked.
 
 #include <algorithm>
 #include <cstdlib>

@@ -214,12 +214,6 @@ hipError_t launch_prefill(const PrefillParams & p, int head_dim, hipStream_t str
 hipError_t launch_linear(const LinearParams & p, hipStream_t stream);
 hipError_t launch_stage(const LinearParams & p, hipStream_t stream);  // M > 8: the staged half input rows
 hipError_t launch_gemm(const LinearParams & p, hipStream_t stream);   // M > 8: gemm_kernel on the staged rows
-// hipBLASLt plans (linear_plan.hip): created for one shape (count 1, M > 8) on one device
-struct BlasPlan;
-BlasPlan * blas_plan_create(const LinearParams & shape, int device, std::string & err);
-void blas_plan_destroy(BlasPlan * plan);
-int blas_plan_device(const BlasPlan * plan);
-hipError_t blas_plan_run(BlasPlan * plan, const LinearParams & p, hipStream_t stream);
 hipError_t launch_rope_store(const RopeStoreParams & p, int head_dim, hipStream_t stream);
 hipError_t launch_small_attn(const SmallAttnParams & p, int head_dim, int n_seq, hipStream_t stream);
 // n_batch problems of the prefill kernel along blockIdx.y, offsets from p.*_batch

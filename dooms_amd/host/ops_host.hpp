@@ -103,36 +103,25 @@ private:
     DeviceBuffer ws_;
 };
 
-// One projection Y = X W^T of a decoder layer (flags MX_LINEAR_*), for up to max_rows input rows. With plan_rows > 8
-// the library GEMM plan for exactly that many contiguous rows (x_stride K, y_stride N, one matrix) is made at create:
-// chunks of that shape then run on hipBLASLt, everything else on mx_linear's own kernels. Nothing allocates in run().
+// One projection Y = X W^T of a decoder layer (flags MX_LINEAR_*), for up to max_rows input rows, on mx_linear's
+// kernels. Nothing allocates in run().
 class Projection {
 public:
     static Status create(int32_t N, int32_t K, uint32_t flags, float eps, int32_t max_rows, hipStream_t stream,
-                         std::unique_ptr<Projection> & out, int32_t plan_rows = 0) {
+                         std::unique_ptr<Projection> & out) {
         if (N < 1 || K < 1 || max_rows < 1) return {Code::InvalidArgument, "N, K and max_rows must be >= 1"};
-        if (plan_rows < 0 || plan_rows > max_rows) return {Code::InvalidArgument, "plan_rows must be in [0, max_rows]"};
         std::unique_ptr<Projection> p(new Projection(N, K, flags, eps, stream));
         const mx_linear_desc d = p->desc(max_rows, K, N);
         if (Status st = p->ws_.reserve(mx_linear_workspace_bytes(&d)); !st.is_ok()) return st;
-        if (plan_rows > 0) {
-            const mx_linear_desc dp = p->desc(plan_rows, K, N);
-            if (Status st = Status::from(mx_linear_plan_create(&dp, &p->plan_)); !st.is_ok()) return st;
-            p->plan_rows_ = plan_rows;
-        }
         out = std::move(p);
         return {};
     }
-    ~Projection() { mx_linear_plan_destroy(plan_); }
 
     // X f32 [M][x_stride], Y[i] [M][y_stride] (f32, or f16 with MX_LINEAR_OUT_F16); count matrices W[i] [N][K] f16
     // sharing X; gamma f32 [K] with MX_LINEAR_RMS_NORM; bias[i] f32 [N] with MX_LINEAR_BIAS. All device memory; the
     // pointer arrays are host arrays.
     Status run(int32_t M, int32_t count, const uint16_t * const * W, const float * X, int64_t x_stride, void * const * Y,
                int64_t y_stride, const float * gamma = nullptr, const float * const * bias = nullptr) {
-        if (plan_ && M == plan_rows_ && count == 1 && x_stride == K_ && y_stride == N_)
-            return Status::from(mx_linear_plan_run(plan_, W[0], X, Y[0], gamma, bias ? bias[0] : nullptr, ws_.data(),
-                                                   ws_.size(), stream_));
         mx_linear_desc d = desc(M, x_stride, y_stride);
         return Status::from(mx_linear(&d, count, W, X, Y, gamma, bias, ws_.data(), ws_.size(), stream_));
     }
@@ -157,8 +146,6 @@ private:
     float eps_;
     hipStream_t stream_;
     DeviceBuffer ws_;
-    mx_linear_plan * plan_ = nullptr;
-    int32_t plan_rows_ = 0;
 };
 
 // The Whisper decoder's cross-attention cache producer: for every layer l, K_l = X W_k[l]^T and V_l = X W_v[l]^T + b_v[l]

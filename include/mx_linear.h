@@ -73,31 +73,6 @@ MX_ATTN_API int32_t mx_linear(const mx_linear_desc * desc, int32_t count, const 
                               void * const * Y, const float * gamma, const float * const * bias, void * workspace,
                               size_t ws_bytes, mx_attn_stream stream);
 
-/*
- * Library GEMM plans. mx_linear runs only this library's own kernels and never allocates, locks or searches. A caller
- * who wants a prompt chunk's single-matrix product on the vendor GEMM (hipBLASLt) instead creates a plan for the exact
- * shape first: hipBLASLt is loaded then (the library does not link it), and its handle, matrix descriptors and the
- * algorithm its heuristic picks are made and kept in the plan, on the current device. No counterpart in the reference,
- * whose matmul kernels are its own (llama_kernels.h:418-450); the plan exists so that everything that allocates or
- * searches happens at create time, as the reference creates its pipelines when a decoder is made.
- *
- *   mx_linear_plan_create  desc->M > 8 (fewer rows run mx_linear's GEMV), count 1. MX_ATTN_UNSUPPORTED when hipBLASLt
- *                          cannot be loaded or offers no algorithm for the shape (mx_linear runs every shape).
- *   mx_linear_plan_run     mx_linear with count 1 and the plan's descriptor: the input staged as mx_linear stages it,
- *                          then one hipblasLtMatmul (the library's own GEMM if hipBLASLt refuses the operands at run
- *                          time); same workspace (mx_linear_workspace_bytes), same results within its tolerance. Runs
- *                          on the device the plan was made on, from one thread at a time (the bias pointer is set on
- *                          the plan's descriptor for each run). Never allocates.
- *   mx_linear_plan_destroy frees the plan (NULL is allowed); work already enqueued with it does not need it, so it
- *                          may be destroyed as soon as its last run has returned.
- */
-typedef struct mx_linear_plan mx_linear_plan;
-MX_ATTN_API int32_t mx_linear_plan_create(const mx_linear_desc * desc, mx_linear_plan ** plan);
-MX_ATTN_API int32_t mx_linear_plan_run(mx_linear_plan * plan, const uint16_t * W, const float * X, void * Y,
-                                       const float * gamma, const float * bias, void * workspace, size_t ws_bytes,
-                                       mx_attn_stream stream);
-MX_ATTN_API void mx_linear_plan_destroy(mx_linear_plan * plan);
-
 #ifdef __cplusplus
 }
 #endif

@@ -487,17 +487,13 @@ TEST(projection_decode_and_prompt_rows) {
     HIP_OK(hipMemcpy(db, bias.data(), bias.size() * 4, hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(dw, w.data(), w.size() * 2, hipMemcpyHostToDevice));
     const uint32_t flags = MX_LINEAR_RMS_NORM | MX_LINEAR_BIAS;
-    std::unique_ptr<Projection> proj, planned;
+    std::unique_ptr<Projection> proj;
     EXPECT(Projection::create(N, K, flags, 1e-5f, maxM, nullptr, proj).is_ok());
-    // the same projection with a library GEMM plan for 20-row chunks (hipBLASLt, made at create)
-    EXPECT(Projection::create(N, K, flags, 1e-5f, maxM, nullptr, planned, maxM).is_ok());
     const uint16_t * W[1] = {dw};
     void * Y[1] = {dy};
     const float * B[1] = {db};
-    for (int M : {3, maxM, -maxM}) {
-        Projection * use = M < 0 ? planned.get() : proj.get();
-        M = M < 0 ? -M : M;
-        EXPECT(use->run(M, 1, W, dx, K, Y, N, dg, B).is_ok());
+    for (int M : {3, 9, maxM}) {
+        EXPECT(proj->run(M, 1, W, dx, K, Y, N, dg, B).is_ok());
         HIP_OK(hipDeviceSynchronize());
         std::vector<float> got((size_t)M * N);
         HIP_OK(hipMemcpy(got.data(), dy, got.size() * 4, hipMemcpyDeviceToHost));

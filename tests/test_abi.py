@@ -368,21 +368,6 @@ def test_self_attention_checks():
     assert call(odd, ws=A + 16, ws_bytes=n) == _lib.INVALID_ARGUMENT and "256-byte" in _lib.last_error()
 
 
-def test_linear_plan_checks():
-    L = _lib.lib()
-    h = ctypes.c_void_p()
-    ld = lambda **kw: _lib.MxLinearDesc(**{**dict(M=64, N=64, K=128, flags=0, x_stride=128, y_stride=64, eps=1e-5,
-                                                     reserved=0), **kw})
-    assert L.mx_linear_plan_create(None, ctypes.byref(h)) == _lib.INVALID_ARGUMENT
-    assert L.mx_linear_plan_create(ctypes.byref(ld()), None) == _lib.INVALID_ARGUMENT
-    assert L.mx_linear_plan_create(ctypes.byref(ld(M=8)), ctypes.byref(h)) == _lib.INVALID_ARGUMENT
-    assert "M > 8" in _lib.last_error() and h.value is None
-    assert L.mx_linear_plan_create(ctypes.byref(ld(K=48, x_stride=48)), ctypes.byref(h)) == _lib.UNSUPPORTED
-    assert L.mx_linear_plan_create(ctypes.byref(ld(reserved=1)), ctypes.byref(h)) == _lib.INVALID_ARGUMENT
-    assert L.mx_linear_plan_run(None, A, A, A, None, None, A, 1 << 20, None) == _lib.INVALID_ARGUMENT
-    L.mx_linear_plan_destroy(None)  # allowed
-
-
 def test_host_code_under_address_and_undefined_behaviour_sanitizers():
     """The library's host code (every .hip source's host side, device code unchanged) built with -fsanitize=address,
     undefined and driven through every entry point's argument checks and the workspace-size arithmetic over many

@@ -21,18 +21,6 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-_PATH = {"gemm": "hip"}
-
-
-@pytest.fixture(autouse=True, params=["hip", "plan"])
-def gemm_path(request):
-    """Prompt chunks (M > 8) of one matrix run either through mx_linear (the library's gemm_kernel) or through an
-    mx_linear_plan (hipBLASLt, set up at create time); every test here covers both."""
-    _PATH["gemm"] = request.param
-    yield request.param
-    _PATH["gemm"] = "hip"
-
-
 def check(got, x, w, gamma, bias, eps, half_input, accumulate_from=None, out_f16=False, rows=None, what=""):
     rows = np.arange(x.shape[0]) if rows is None else np.asarray(rows)
     flags = (1 if gamma is not None else 0) | (4 if bias is not None else 0) | (2 if accumulate_from is not None else 0)
@@ -72,13 +60,8 @@ def run(device, seed, M, N, K, norm=False, bias=False, accumulate=False, out_f16
     dgamma = None if gamma is None else torch.from_numpy(gamma).to(device)
     dbias = None if biases is None else [torch.from_numpy(b).to(device) for b in biases]
     xin = dx[:, :K] if x_pad == 0 else dx
-    if _PATH["gemm"] == "plan" and M > 8 and count == 1:
-        plan = A.LinearPlan(M, N, K, norm=norm, bias=bias, accumulate=accumulate, out_f16=out_f16,
-                            x_stride=xin.stride(0), y_stride=douts[0].stride(0), eps=eps)
-        plan.run(xin, dws[0], douts[0][:, :N], gamma=dgamma, bias=None if dbias is None else dbias[0])
-    else:
-        A.linear(xin, dws, out=[o[:, :N] for o in douts], gamma=dgamma, bias=dbias, eps=eps, accumulate=accumulate,
-                 out_f16=out_f16)
+    A.linear(xin, dws, out=[o[:, :N] for o in douts], gamma=dgamma, bias=dbias, eps=eps, accumulate=accumulate,
+             out_f16=out_f16)
     torch.cuda.synchronize()
     half_input = M > 8
     for i in range(count):
@@ -204,17 +187,3 @@ def test_linear_rejects_mismatched_shapes(device):
     with pytest.raises(ValueError):
         A.linear(x, [torch.zeros(8, 64, dtype=torch.float16, device=device),
                      torch.zeros(16, 64, dtype=torch.float16, device=device)])
-
-
-def test_plan_checks(device):
-    from dooms_amd import _lib
-    with pytest.raises(_lib.MxAttnError) as e:
-        A.LinearPlan(4, 64, 64)  # the GEMV's rows: mx_linear, not a plan
-    assert e.value.code == _lib.INVALID_ARGUMENT
-    with pytest.raises(_lib.MxAttnError) as e:
-        A.LinearPlan(64, 64, 48)  # K not a multiple of 32
-    assert e.value.code == _lib.UNSUPPORTED
-    plan = A.LinearPlan(16, 64, 64)
-    x = torch.zeros(16, 64, device=device)
-    with pytest.raises(ValueError):
-        plan.run(x[:8], torch.zeros(64, 64, dtype=torch.float16, device=device), torch.zeros(8, 64, device=device))

@@ -61,7 +61,11 @@ def test_noalloc_rejects_beyond_scratch(device):
     d = _lib.make_desc(32, 8, 128, 1, 4096, 1024, 4096, 1.0 / math.sqrt(128), causal=0)
     need = _lib.decode_workspace_bytes(d, 32, 8192)
     assert need > _lib.SCRATCH_BYTES
-    x = torch.empty(256, dtype=torch.float16, device=device)
-    code = _lib.decode_noalloc_raw(d, [8192] * 32, x.data_ptr(), [x.data_ptr()] * 32, [x.data_ptr()] * 32,
-                                   x.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
+    # buffers that hold the declared shape (one 8192 x 1024 cache shared by every sequence), so that a regression of
+    # the size check would compute on valid memory and fail the assertion rather than read out of bounds
+    cache = torch.zeros(8192, 1024, dtype=torch.float16, device=device)
+    q = torch.zeros(32, 4096, dtype=torch.float16, device=device)
+    out = torch.empty_like(q)
+    code = _lib.decode_noalloc_raw(d, [8192] * 32, q.data_ptr(), [cache.data_ptr()] * 32, [cache.data_ptr()] * 32,
+                                   out.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
     assert code == _lib.RESOURCE_EXHAUSTED and "scratch" in _lib.last_error()
