@@ -40,6 +40,9 @@ constexpr int kBK = 64;  // keys per block
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef half_t half2_t __attribute__((ext_vector_type(2)));
 constexpr half2_t kOnes2 = {(half_t)1.f, (half_t)1.f};
+// The largest per-lane sum of a block's half probabilities (32 of them) at the kept reference maximum before the
+// exact update runs: below it every probability is below 2^8.
+constexpr float kProbSumMax = 256.f;
 
 // Relaxed device-scope accesses of the stream-K partials: coherent across the XCDs without cache maintenance.
 __device__ __forceinline__ void put_f32(float * a, float v) {
@@ -381,8 +384,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
         for (int v = 0; v < 16; v++) o[dt][v] = 0.f;
-    float m_run = kNegInf, l_run = 0.f;
-    float m_thr = kNegInf, nm_use = 0.f;  // m_run + 8 (the lazy rescale's threshold) and -m_run (0 while m_run = -inf)
+    float m_run = kNegInf, l_run = 0.f;  // reference maximum (base 2, scaled) and row sum of this lane's keys
+    float nm_use = 0.f;                   // -m_run (0 while m_run = -inf)
 
     // per-lane LDS read bases (halves); everything else is a compile-time offset
     const int k_base = l32 * KP + 8 * hgrp;  // K[32 mt + l32][16 kk + 8 hgrp]
@@ -471,11 +474,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                 }
             }
         }
-        // block max (raw scores when the scale is positive); the mask only where a block crosses the diagonal or the
-        // end of the cache (a wave-uniform branch)
+        // The mask only where a block crosses the diagonal or the end of the cache (a wave-uniform branch).
         const bool need_mask = (p.causal && kb + kBK - 1 > p.p0 + q0 + 32 * rt) || kb + kBK > p.n_kv;
         const float c = p.scale_log2;
-        float bmax = kNegInf;
         if (need_mask) {
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
@@ -483,43 +484,58 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                 for (int v = 0; v < 16; v++) {
                     const int key = kb + 32 * mt + 8 * (v / 4) + 4 * hgrp + (v % 4);
                     const bool hide = key >= p.n_kv || (p.causal && key > qpos);
-                    const float x = hide ? kNegInf : (POS ? sc[mt][v] : sc[mt][v] * c);
-                    sc[mt][v] = x;
-                    bmax = fmaxf(bmax, x);
+                    sc[mt][v] = hide ? kNegInf : (POS ? sc[mt][v] : sc[mt][v] * c);
                 }
-        } else {
+        } else if constexpr (!POS) {
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const float x = POS ? sc[mt][v] : sc[mt][v] * c;
-                    sc[mt][v] = x;
-                    bmax = fmaxf(bmax, x);
-                }
+                for (int v = 0; v < 16; v++) sc[mt][v] *= c;
         }
-        bmax = xor32_max(bmax);
-        // lazy rescale: the reference maximum moves only when the block's maximum exceeds it by more than 8 (base 2);
-        // the probabilities then stay below 2^8, well inside f16, and the O rescale below is rare
-        // (one compare and a ballot per block; the new maximum, the factor and the rescale of O and l only when it moves)
-        const float bm = POS ? bmax * c : bmax;
-        if (__builtin_amdgcn_ballot_w64(bm > m_thr)) {  // the running max moves in some row of the wave
-            const float m_new = bm > m_thr ? bm : m_run;
+        // Probabilities at the kept reference maximum m_run, straight to half (the P^T operand: step u takes values
+        // 8 (u % 2) .. + 8 of score tile u / 2), and their per-lane sum on v_dot2_f32_f16. The block's maximum is not
+        // computed on this path: a sum above 2^8 (some probability above 2^8, or an overflow to inf) or a row that has
+        // no reference yet sends the wave to the exact update below, which moves m_run to the running maximum, rescales
+        // O and l, and recomputes the block. While the sum stays below 2^8 every probability is below 2^8, well inside
+        // half; a block whose scores sit a few units (base 2) above the reference takes the exact update once, so the
+        // common path is the exponentials alone (cfg5: 16 v_max3 and a cross-lane step fewer per block).
+        half8_t pb[4];
+        float bs;
+        auto probs = [&]() __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float x = sc[u / 2][8 * (u % 2) + e];
+                    pb[u][e] = (half_t)exp2_fast(POS ? __builtin_fmaf(x, c, nm_use) : x + nm_use);
+                }
+            bs = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) bs = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, bs, false);
+        };
+        probs();
+        if (__builtin_amdgcn_ballot_w64(bs > kProbSumMax || m_run == kNegInf)) {
+            float bmax = kNegInf;
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) bmax = fmaxf(bmax, sc[mt][v]);
+            bmax = xor32_max(bmax);
+            const float bm = POS ? bmax * c : bmax;
+            const float m_new = fmaxf(m_run, bm);
             const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
             m_run = m_new;
-            m_thr = m_new + 8.f;
             nm_use = m_new == kNegInf ? 0.f : -m_new;  // no visible key yet: every exponent below is 2^-inf = 0
             l_run *= corr;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+            probs();
         }
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                sc[mt][v] = exp2_fast(POS ? __builtin_fmaf(sc[mt][v], c, nm_use) : sc[mt][v] + nm_use);
-            }
+        l_run += bs;
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
         // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V. The reads of
@@ -535,17 +551,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                     t[s8] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)a);
                 }
             };
-            half8_t pb[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) pb[u][e] = (half_t)sc[u / 2][8 * (u % 2) + e];
-            // the row sum of the half probabilities that multiply V, on v_dot2_f32_f16 (two per instruction, f32 sum)
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int e = 0; e < 8; e += 2)
-                    l_run = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, l_run, false);
             auto pv = [&](int i, const short4_t (&t)[2]) __attribute__((always_inline)) {
                 const short4_t lo = t[0], hi = t[1];
                 const half8_t a = __builtin_bit_cast(half8_t, (short __attribute__((ext_vector_type(8)))){
