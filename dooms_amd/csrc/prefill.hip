@@ -493,49 +493,64 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                 for (int v = 0; v < 16; v++) sc[mt][v] *= c;
         }
         // Probabilities at the kept reference maximum m_run, straight to half (the P^T operand: step u takes values
-        // 8 (u % 2) .. + 8 of score tile u / 2), and their per-lane sum on v_dot2_f32_f16. The block's maximum is not
+        // 8 (u % 2) .. + 8 of score tile u / 2), and their per-lane sum on v_dot2_f32_f16, in two halves of 32 keys. The block's maximum is not
         // computed on this path: a sum above 2^8 (some probability above 2^8, or an overflow to inf) or a row that has
         // no reference yet sends the wave to the exact update below, which moves m_run to the running maximum, rescales
         // O and l, and recomputes the block. While the sum stays below 2^8 every probability is below 2^8, well inside
         // half; a block whose scores sit a few units (base 2) above the reference takes the exact update once, so the
         // common path is the exponentials alone (cfg5: 16 v_max3 and a cross-lane step fewer per block).
         half8_t pb[4];
-        float bs;
-        auto probs = [&]() __attribute__((always_inline)) {
+        // score tiles H0 .. H1 - 1 (32 keys each): their probabilities at a valid reference, added to l. With
+        // kSplitHalves the second half runs between the P V products of the first (the matrix cores busy with those
+        // while the vector ALUs compute these); an exact update there rescales O with the first half's products
+        // already in it, as for any earlier block.
+        auto settle = [&](auto H0C, auto H1C) __attribute__((always_inline)) {
+            constexpr int H0 = decltype(H0C)::value, H1 = decltype(H1C)::value;  // score tiles H0 .. H1 - 1
+            float bs;
+            auto probs = [&]() __attribute__((always_inline)) {
 #pragma unroll
-            for (int u = 0; u < 4; u++)
+                for (int u = 2 * H0; u < 2 * H1; u++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float x = sc[u / 2][8 * (u % 2) + e];
-                    pb[u][e] = (half_t)exp2_fast(POS ? __builtin_fmaf(x, c, nm_use) : x + nm_use);
-                }
-            bs = 0.f;
+                    for (int e = 0; e < 8; e++) {
+                        const float x = sc[u / 2][8 * (u % 2) + e];
+                        pb[u][e] = (half_t)exp2_fast(POS ? __builtin_fmaf(x, c, nm_use) : x + nm_use);
+                    }
+                bs = 0.f;
 #pragma unroll
-            for (int u = 0; u < 4; u++)
+                for (int u = 2 * H0; u < 2 * H1; u++)
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) bs = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, bs, false);
-        };
-        probs();
-        if (__builtin_amdgcn_ballot_w64(bs > kProbSumMax || m_run == kNegInf)) {
-            float bmax = kNegInf;
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) bmax = fmaxf(bmax, sc[mt][v]);
-            bmax = xor32_max(bmax);
-            const float bm = POS ? bmax * c : bmax;
-            const float m_new = fmaxf(m_run, bm);
-            const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
-            m_run = m_new;
-            nm_use = m_new == kNegInf ? 0.f : -m_new;  // no visible key yet: every exponent below is 2^-inf = 0
-            l_run *= corr;
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+                    for (int e = 0; e < 8; e += 2) bs = __builtin_amdgcn_fdot2(half2_t{pb[u][e], pb[u][e + 1]}, kOnes2, bs, false);
+            };
             probs();
-        }
-        l_run += bs;
+            if (__builtin_amdgcn_ballot_w64(bs > kProbSumMax || m_run == kNegInf)) {
+                float bmax = kNegInf;
+#pragma unroll
+                for (int mt = H0; mt < H1; mt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) bmax = fmaxf(bmax, sc[mt][v]);
+                bmax = xor32_max(bmax);
+                const float bm = POS ? bmax * c : bmax;
+                const float m_new = fmaxf(m_run, bm);
+                const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
+                m_run = m_new;
+                nm_use = m_new == kNegInf ? 0.f : -m_new;  // no visible key yet: every exponent below is 2^-inf = 0
+                l_run *= corr;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+                probs();
+            }
+            l_run += bs;
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        // Split at head dims 64 and 256 (Qwen2.5-0.5B 4096-token prompt 352 -> 366 TFLOP/s, a head-dim-256 2048-token
+        // prompt 108 -> 125); at 128 both halves come first (cfg5 1013 -> 997 split).
+        constexpr bool kSplitHalves = HD != 128;
+        if constexpr (kSplitHalves) settle(I0{}, I1{});
+        else settle(I0{}, I2{});
 
         // O^T += V^T P^T: 4 steps of 16 keys; step u takes values 8 (u % 2) .. + 8 of score tile u / 2, which are keys
         // 16 u + 8 (e / 4) + 4 hgrp + e % 4 for e = 0..7; two transposing reads fetch the same keys of V. The reads of
@@ -579,6 +594,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                     }
                     if constexpr (t >= VA) {  // product j: its two reads done, those of the later products in flight
                         constexpr int j = t - VA;
+                        if constexpr (kSplitHalves && j == NP / 2) settle(I1{}, I2{});
                         constexpr int later = 2 * ((t < NP - 1 ? t : NP - 1) - j);
                         asm volatile("s_waitcnt lgkmcnt(%2)"
                                      : "+v"(vr[j % (VA + 1)][0]), "+v"(vr[j % (VA + 1)][1])
@@ -589,7 +605,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
             } else {
                 vread(0, vt[0]);
 #pragma unroll
-                for (int i = 0; i < NP; i++) {
+                for (int i = 0; i < NP / 2; i++) {
+                    vread(i + 1, vt[(i + 1) & 1]);
+                    pv(i, vt[i & 1]);
+                }
+                if constexpr (kSplitHalves) settle(I1{}, I2{});
+#pragma unroll
+                for (int i = NP / 2; i < NP; i++) {
                     if (i + 1 < NP) vread(i + 1, vt[(i + 1) & 1]);
                     pv(i, vt[i & 1]);
                 }
