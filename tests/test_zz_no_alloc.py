@@ -69,3 +69,33 @@ def test_noalloc_rejects_beyond_scratch(device):
     code = _lib.decode_noalloc_raw(d, [8192] * 32, q.data_ptr(), [cache.data_ptr()] * 32, [cache.data_ptr()] * 32,
                                    out.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
     assert code == _lib.RESOURCE_EXHAUSTED and "scratch" in _lib.last_error()
+
+
+def test_noalloc_two_streams_ordered_by_caller(device):
+    """Calls on two streams share the GPU's one array; the contract is that the caller orders them. Two calls in a row
+    on two streams, the second made to wait for the first with an event, each match mx_attn_decode bit for bit."""
+    rng = np.random.default_rng(11)
+    n_head, n_kv, hd = 32, 8, 128
+    d = _lib.make_desc(n_head, n_kv, hd, 1, n_head * hd, n_kv * hd, n_head * hd, 1.0 / math.sqrt(hd), causal=0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    probs = []
+    for lens in ([8192], [3000, 129]):
+        B = len(lens)
+        q = torch.from_numpy(normal_f16(rng, (B, n_head * hd))).to(device)
+        k, v = caches(rng, lens, n_kv * hd, device)
+        out = torch.full((B, n_head * hd), float("nan"), dtype=torch.float16, device=device)
+        probs.append((lens, q, k, v, out))
+    torch.cuda.synchronize()
+    ev = torch.cuda.Event()
+    for (lens, q, k, v, out), st in zip(probs, (s1, s2)):
+        if st is s2:
+            st.wait_event(ev)
+        _lib.check(_lib.decode_noalloc_raw(d, lens, q.data_ptr(), [t.data_ptr() for t in k], [t.data_ptr() for t in v],
+                                           out.data_ptr(), 0, st.cuda_stream))
+        if st is s1:
+            ev.record(s1)
+    torch.cuda.synchronize()
+    for lens, q, k, v, out in probs:
+        ref, _ = A.decode(q, k, v, lens, n_head=n_head, n_head_kv=n_kv, head_dim=hd)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.cpu().numpy().view(np.uint16)), lens
