@@ -76,6 +76,13 @@ __device__ __forceinline__ u32x4 load16_dev(__amdgpu_buffer_rsrc_t r, int byte_o
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
 }
 
+// K/V loads; NT: non-temporal (the cache lines are not kept), for launches whose keys and values stream from HBM once
+template <bool NT>
+__device__ __forceinline__ u32x4 load16_kv(const void * p) {
+    if constexpr (NT) return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4 *)(p));
+    else return load16(p);
+}
+
 template <int HD>
 struct KvBlock {
     static constexpr int KS = HD / 32;            // MFMA steps along head_dim
@@ -221,7 +228,8 @@ __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float *
 // With p.append it is the fused decode step (one query row per sequence): q, k and v of the new token come unrotated
 // from the q|k|v row; q and the new key are rotated for position kv_len - 1 and rounded to half, the new key and value
 // are used from registers for that position and written into the caches by the one workgroup whose split holds it.
-template <int HD, int RT, bool F32, int NW>
+// NT: the keys and values are loaded non-temporally (one sequence whose K/V stream from HBM, p.kv_nt).
+template <int HD, int RT, bool F32, int NW, bool NT = false>
 __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     using B = KvBlock<HD>;
     constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
@@ -301,12 +309,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
             const int key = min(jb + 16 * mt + srow, L - 1);
             const half_t * kp = kbase + (int64_t)key * kv_stride + 8 * sgrp;
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) blk.k[mt][ks] = load16(kp + 32 * ks);
+            for (int ks = 0; ks < KS; ks++) blk.k[mt][ks] = load16_kv<NT>(kp + 32 * ks);
         }
 #pragma unroll
         for (int i = 0; i < NLV; i++) {
             const int key = min(jb + KPL * i + vslot, L - 1);
-            blk.v[i] = load16(vbase + (int64_t)key * kv_stride + vcol);
+            blk.v[i] = load16_kv<NT>(vbase + (int64_t)key * kv_stride + vcol);
         }
     };
 
@@ -659,6 +667,15 @@ hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream
     // x: groups of (split, kv head), 8 per round of XCDs, each group's row tiles on one XCD; y: the sequence
     const int64_t groups = (int64_t)p.max_split * p.n_head_kv;
     const dim3 grid((uint32_t)(((groups + 7) / 8) * 8 * p.n_rowtiles), (uint32_t)n_seq);
+    if constexpr (HD == 128 && RT == 4 && NW == 8) {  // the one-sequence long-cache plan
+        if (p.kv_nt) {
+            if (p.f32)
+                hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW, true>), grid, dim3(NW * kWave), 0, stream, p);
+            else
+                hipLaunchKernelGGL((decode_kernel<HD, RT, false, NW, true>), grid, dim3(NW * kWave), 0, stream, p);
+            return hipGetLastError();
+        }
+    }
     if (p.f32)
         hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW>), grid, dim3(NW * kWave), 0, stream, p);
     else
