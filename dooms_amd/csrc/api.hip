@@ -457,8 +457,11 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         // Non-temporal K/V loads for one long sequence (K/V streamed from HBM once per step in a decoder): Llama-3-8B
         // batch 1 at 8192 keys 11.93 -> 11.76 us per launch, batch 16 x 8192 keys -3.5 %; but slower where the bench's
         // caches stay in the Infinity Cache between replays (Qwen2.5-0.5B +8 %, Whisper cross-attention +10 %) and
-        // on the batch-4 shape (+4 %), hence one sequence and at least 16 MB of K/V only.
-        p.kv_nt = p.xcd_heads && (int64_t)kv_len[b0] * d.kv_stride * 2 * 2 >= ((int64_t)16 << 20);
+        // on the batch-4 shape (55 MB of K/V, +4 %), hence one sequence with at least 16 MB, or at least 256 MB.
+        int64_t kv_keys = 0;
+        for (int i = 0; i < n_seq; i++) kv_keys += kv_len[b0 + i];
+        const int64_t kv_bytes = kv_keys * d.kv_stride * 2 * 2;
+        p.kv_nt = (p.xcd_heads && kv_bytes >= ((int64_t)16 << 20)) || kv_bytes >= ((int64_t)256 << 20);
         p.scale_log2 = d.scale * 1.4426950408889634f;
         // split plan (see workgroup_cap)
         const int64_t quantum = mx::kDecodeChunkQuantum;

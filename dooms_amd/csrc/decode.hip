@@ -667,7 +667,7 @@ hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream
     // x: groups of (split, kv head), 8 per round of XCDs, each group's row tiles on one XCD; y: the sequence
     const int64_t groups = (int64_t)p.max_split * p.n_head_kv;
     const dim3 grid((uint32_t)(((groups + 7) / 8) * 8 * p.n_rowtiles), (uint32_t)n_seq);
-    if constexpr (HD == 128 && RT == 4 && NW == 8) {  // the one-sequence long-cache plan
+    if constexpr (HD == 128 && RT == 4) {  // one query row per Llama-3-8B-shaped sequence (4 query heads per kv head)
         if (p.kv_nt) {
             if (p.f32)
                 hipLaunchKernelGGL((decode_kernel<HD, RT, true, NW, true>), grid, dim3(NW * kWave), 0, stream, p);
