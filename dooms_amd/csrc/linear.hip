@@ -255,6 +255,22 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     // later wait assume that the input loads are the newest ones
 #pragma unroll
     for (int j = 0; j < kGemvDepth; j++) load_sweep(j, lane + kWave * j);
+    // what the epilogue adds to lane i MT + m's output (row r0 + i, input row m): the bias and the previous output,
+    // loaded here behind the weights (by every lane, at clamped valid addresses) rather than after the reduction,
+    // where each was one more memory round trip at the end of the kernel
+    float y_prev = 0.f, y_bias = 0.f;
+    {
+        const int i = min(lane / MT, kGemvRows - 1), m = min(lane % MT, M - 1), n = min(r0 + i, p.N - 1);
+        if (p.flags & kLinearAccumulate) {
+            const int64_t o = (int64_t)m * p.y_stride + n;
+            if constexpr (OUT16) y_prev = (float)static_cast<const half_t *>(p.y[mi])[o];
+            else y_prev = static_cast<const float *>(p.y[mi])[o];
+        }
+        if (p.flags & kLinearBias) {
+            const float * b = p.bias[mi];
+            if (b) y_bias = b[n];
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (STAGE || NORM) xstage(0);
     for (int b = 1; b < nxb; b++) {  // inputs longer than one batch (the waits of these drain the weight loads too)
@@ -342,7 +358,14 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
         }
     if (lane < kGemvRows * MT) {
         const int i = lane / MT, m = lane % MT, n = r0 + i;
-        if (m < M && n < p.N) store_y<OUT16>(p, mi, m, n, norm ? mine * s_scale[m] : mine);
+        if (m < M && n < p.N) {  // store_y's sums, with the bias and the previous output loaded above
+            float v = norm ? mine * s_scale[m] : mine;
+            if (p.flags & kLinearBias) v += y_bias;
+            if (p.flags & kLinearAccumulate) v += y_prev;
+            const int64_t o = (int64_t)m * p.y_stride + n;
+            if constexpr (OUT16) static_cast<half_t *>(p.y[mi])[o] = (half_t)v;
+            else static_cast<float *>(p.y[mi])[o] = v;
+        }
     }
 }
 
