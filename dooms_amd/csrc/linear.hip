@@ -351,9 +351,7 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     for (int i = 0; i < kGemvRows; i++)
 #pragma unroll
         for (int m = 0; m < MT; m++) {
-            float s = acc[i][m];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) s += shfl_xor(s, o);
+            const float s = wave_sum(acc[i][m]);
             if (lane == i * MT + m) mine = s;
         }
     if (lane < kGemvRows * MT) {

@@ -75,6 +75,22 @@ __device__ __forceinline__ float xor16_add(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Sum over the 64 lanes of a wave, in every lane, without LDS: within each row of 16 lanes row_mirror (lane i with
+// 15 - i), row_half_mirror (i with 7 - i inside each half) and two quad permutations (xor 2, xor 1) pair distinct lanes
+// at each step, so after four DPP moves every lane holds its row's sum; then the xor-16 and xor-32 swaps. Every lane of
+// the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_pair_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = dpp_pair_add<0x140>(v);  // row_mirror
+    v = dpp_pair_add<0x141>(v);  // row_half_mirror
+    v = dpp_pair_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v = dpp_pair_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    return xor32_add(xor16_add(v));
+}
+
 // f(std::integral_constant<int, i>) for i = B .. E - 1, each i a compile-time constant (immediate operands of inline asm)
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F && f) {
