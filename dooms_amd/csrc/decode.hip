@@ -163,14 +163,10 @@ __device__ __forceinline__ void merge_wide(const DecodeParams & p, const float *
         if (r >= RT) break;
         const bool ok = lane < ns && ml[i].y > 0.f;
         const float m = ok ? ml[i].x : kNegInf, l = ok ? ml[i].y : 0.f;
-        float M = xor16_max(xor32_max(m));
-#pragma unroll
-        for (int o = 8; o >= 1; o /= 2) M = vmax_raw(M, shfl_xor(M, o));
+        const float M = row16_max(xor16_max(xor32_max(m)));  // in-register steps: no LDS round trips in the tail
         const float Mu = M == kNegInf ? 0.f : M;
         const float w = exp2_fast(m - Mu);
-        float tot = xor16_add(xor32_add(l * w));
-#pragma unroll
-        for (int o = 8; o >= 1; o /= 2) tot += shfl_xor(tot, o);
+        const float tot = row16_sum(xor16_add(xor32_add(l * w)));
         if (lane < kMaxSplitsPerTile) s_w[lane * RT + r] = w;
         if (lane == 0) s_row[r] = make_float2(M, tot);
     }

@@ -83,12 +83,26 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_pair_add(float v) {
     return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+template <int CTRL>
+__device__ __forceinline__ float dpp_pair_max(float v) {
+    return vmax_raw(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false)));
+}
+// the maximum over each row of 16 lanes, in every lane of the row (the same pairing as wave_sum)
+__device__ __forceinline__ float row16_max(float v) {
+    v = dpp_pair_max<0x140>(v);
+    v = dpp_pair_max<0x141>(v);
+    v = dpp_pair_max<0x4E>(v);
+    return dpp_pair_max<0xB1>(v);
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v = dpp_pair_add<0x140>(v);
+    v = dpp_pair_add<0x141>(v);
+    v = dpp_pair_add<0x4E>(v);
+    return dpp_pair_add<0xB1>(v);
+}
 __device__ __forceinline__ float wave_sum(float v) {
-    v = dpp_pair_add<0x140>(v);  // row_mirror
-    v = dpp_pair_add<0x141>(v);  // row_half_mirror
-    v = dpp_pair_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-    v = dpp_pair_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-    return xor32_add(xor16_add(v));
+    // row_mirror (0x140), row_half_mirror (0x141), quad_perm [2, 3, 0, 1] (0x4E), quad_perm [1, 0, 3, 2] (0xB1)
+    return xor32_add(xor16_add(row16_sum(v)));
 }
 
 // f(std::integral_constant<int, i>) for i = B .. E - 1, each i a compile-time constant (immediate operands of inline asm)
