@@ -75,6 +75,9 @@ constexpr int kCpolSc1 = 16;  // the cache-policy bit that makes a buffer access
 __device__ __forceinline__ u32x4 load16_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1));
 }
+__device__ __forceinline__ void store16_dev(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, kCpolSc1);
+}
 
 // K/V loads; NT: non-temporal (the cache lines are not kept), for launches whose keys and values stream from HBM once
 template <bool NT>
@@ -530,7 +533,35 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     float * part_tile = p.part + tile * p.max_split * RT * (HD + 4);
     constexpr int64_t SS = (int64_t)RT * (HD + 4);  // floats between the partials of consecutive splits
     constexpr int NP = RT * HD / 2;                 // output pairs of the tile
-    for (int idx = threadIdx.x; idx < NP; idx += kThreads) {
+    // Head dim 128, several splits: the partial goes out in 16-byte device-scope stores, four outputs per thread (half
+    // the store instructions of the pairs below, whose completion the count then waits for).
+    constexpr bool kQuadPublish = HD == 128;
+    if (kQuadPublish && !single) {
+        constexpr int NQ = RT * HD / 4;
+        const __amdgpu_buffer_rsrc_t prs = dev_rsrc(part_tile + s * SS);
+        for (int idx = threadIdx.x; idx < NQ; idx += kThreads) {
+            const int r = idx / (HD / 4), d = 4 * (idx % (HD / 4));
+            if (rt * RT + r >= p.rows) continue;
+            float mw[NW];
+#pragma unroll
+            for (int w = 0; w < NW; w++) mw[w] = s_m[w][r];
+            float M = kNegInf;
+#pragma unroll
+            for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w]);
+            const float Mu = M == kNegInf ? 0.f : M;
+            float tot = 0.f;
+            float4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const float wt = exp2_fast(mw[w] - Mu);
+                tot += s_l[w][r] * wt;
+                a += *reinterpret_cast<const float4_t *>(s_o(w) + r * HD + d) * wt;
+            }
+            store16_dev(prs, 4 * (r * (HD + 4) + d), a);
+            if (d == 0) publish2(part_tile + s * SS + (int64_t)r * (HD + 4) + HD, M, tot);
+        }
+    }
+    for (int idx = threadIdx.x; idx < ((kQuadPublish && !single) ? 0 : NP); idx += kThreads) {
         const int r = idx / (HD / 2), d = 2 * (idx % (HD / 2));
         const int row = rt * RT + r;
         if (row >= p.rows) continue;
