@@ -41,7 +41,8 @@ struct DecodeParams {
     int32_t max_split;   // max over the launch's sequences of n_split
     int32_t seq0;        // index of the launch's first sequence in the caller's batch (query/output rows)
     int32_t xcd_heads;   // 1: kv head g's splits run on XCD g % 8 (one sequence, n_head_kv a multiple of 8)
-    int32_t kv_nt;       // 1: non-temporal K/V loads (one long sequence with xcd_heads, or at least 256 MB of K/V)
+    int32_t kv_nt;       // 1: non-temporal K/V loads (one long sequence with xcd_heads, or at least 256 MB of K/V);
+                         // honoured by the head-dim-128 kernels with 4-row tiles
     float scale_log2;    // scale * log2(e): scores are kept in base-2 units
     int32_t f32;         // 1: f32 query rows in qkv (q_stride floats apart) and f32 output in out32
     int32_t append;      // 1 (with f32): fused decode step, the rows are q|k|v of each sequence's new token
