@@ -539,7 +539,7 @@ def main():
                                    "K/V (1.07 GB per step)",
                        "batch": 1, "kv_len": L, "layers_per_step": 32, "n_head": 32, "n_head_kv": 8, "head_dim": 128,
                        "timing": "HIP graph replay of the 32-launch step, events on the launch stream"},
-            "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,4,false,8>", "achieved": round(achieved, 1),
+            "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,4,false,8,true>", "achieved": round(achieved, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic, "bytes_per_launch": bpl, "avg_launch_us": round(avg_us, 3),
                          "launch_timing": "graph-timed region / launches (includes the gaps between launches)",
