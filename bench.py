@@ -51,13 +51,16 @@ def parse():
                          "(counters) over the last --last dispatches of the kernels whose names contain --kernel")
     ap.add_argument("--kernel", default="decode_kernel")
     ap.add_argument("--last", type=int, default=0, help="dispatches at the end of the trace to summarize (0: all)")
+    ap.add_argument("--per-dispatch", action="store_true",
+                    help="with --summarize on a counter_collection.csv: one row per dispatch (duration, shader clock "
+                         "from GRBM_GUI_ACTIVE, MFMA busy per SIMD, and each SQ_ counter per SQ_WAVE_CYCLES)")
     ap.add_argument("--trace-decode", action="store_true",
                     help="phase timestamps of the decode kernel (dooms_amd/libmx_attn_trace.so) on the headline and "
                          "short-shape workloads: one JSON line per workload, microseconds from the launch's first start")
     return ap.parse_args()
 
 
-def summarize(path, kernel, last):
+def summarize(path, kernel, last, per_dispatch=False):
     """The timed region of a profiled bench.py run is its last dispatches (graph replays after the warmup), so a
     summary over the last `last` dispatches of `kernel` reconciles with the ms_per_step the same run printed.
     Prints a text summary: durations (kernel trace) or per-dispatch counter averages (counter collection), and for
@@ -82,6 +85,19 @@ def summarize(path, kernel, last):
         for r in rows:
             if "Start_Timestamp" in r and "End_Timestamp" in r:
                 ts[(r["Dispatch_Id"], r["Kernel_Name"])] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        if per_dispatch and ts:
+            # clock = GRBM_GUI_ACTIVE / 8 XCDs / duration; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / the
+            # cycles per XCD; other SQ_ counters as fractions of SQ_WAVE_CYCLES
+            names = [c for c in sel[0][1] if c.startswith("SQ_") and c not in ("SQ_WAVE_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES")]
+            print("dispatch | duration us | clock GHz | MFMA busy | " + " | ".join(n.lower() for n in names))
+            for k, v in sel:
+                ns = ts[k]
+                cyc = v.get("GRBM_GUI_ACTIVE", 0.0) / 8
+                row = [k[0], f"{ns / 1e3:.1f}", f"{cyc / ns:.2f}" if cyc else "-",
+                       f"{v['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024 / cyc:.2f}" if cyc and "SQ_VALU_MFMA_BUSY_CYCLES" in v else "-"]
+                wc = v.get("SQ_WAVE_CYCLES")
+                row += [f"{v[n] / wc:.3f}" if wc else f"{v[n]:.0f}" for n in names]
+                print(" | ".join(row))
         if "GRBM_GUI_ACTIVE" in sel[0][1] and ts:
             # GRBM_GUI_ACTIVE sums the busy cycles of the 8 XCDs: cycles per XCD / duration is the shader clock
             cyc = sum(v["GRBM_GUI_ACTIVE"] / 8 for _, v in sel)
@@ -469,7 +485,7 @@ def trace_decode(args):
 def main():
     args = parse()
     if args.summarize:
-        return summarize(args.summarize, args.kernel, args.last)
+        return summarize(args.summarize, args.kernel, args.last, args.per_dispatch)
     if args.trace_decode:
         return trace_decode(args)
     if args.gpus != 1:
