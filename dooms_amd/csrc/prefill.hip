@@ -477,6 +477,23 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
         // The mask only where a block crosses the diagonal or the end of the cache (a wave-uniform branch).
         const bool need_mask = (p.causal && kb + kBK - 1 > p.p0 + q0 + 32 * rt) || kb + kBK > p.n_kv;
         const float c = p.scale_log2;
+        // DL: the first VA products' transposing V reads go out now, so that the softmax below covers their latency
+        // (no other LDS access comes between them and the products' waits, which count them as before)
+        constexpr int VA = 2;  // products whose V reads are in flight ahead of the one multiplied (1: -0.6 %, 3: -0.5 %)
+        short4_t vr[VA + 1][2];
+        const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)vs_ +
+                            2 * (dl_v + 2048 * kh);
+        auto vread_dl = [&](auto TC) __attribute__((always_inline)) {
+            constexpr int t = decltype(TC)::value;
+            constexpr int off = 2 * (512 * (RB * (t % DT) + t / DT));
+            short4_t r0, r1;
+            asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                         : "=&v"(r0), "=&v"(r1)
+                         : "v"(va), "i"(off), "i"(off + 512));
+            vr[t % (VA + 1)][0] = r0;
+            vr[t % (VA + 1)][1] = r1;
+        };
+        if constexpr (DL) static_for<0, VA>(vread_dl);
         if (need_mask) {
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
@@ -576,22 +593,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams & p, PrefillSme
                 // The transposing reads as inline asm with their own waits: the compiler cannot tell the intrinsic's
                 // LDS read from the direct loads still writing another buffer, and would drain them (vmcnt(0)) before
                 // the first read of every block. Rows 16 u + 8 s8 + 4 hgrp + (lane % 16) / 4 of block (dt, u).
-                const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) half_t *)vs_ +
-                                    2 * (dl_v + 2048 * kh);
-                // products whose reads are in flight ahead of the one multiplied (1: cfg5 -0.6 %, 3: -0.5 %)
-                constexpr int VA = 2;
-                short4_t vr[VA + 1][2];
+                // (the reads of products 0 .. VA - 1 went out before the softmax)
                 static_for<0, NP + VA>([&](auto I) __attribute__((always_inline)) {
                     constexpr int t = decltype(I)::value;
-                    if constexpr (t < NP) {
-                        constexpr int off = 2 * (512 * (RB * (t % DT) + t / DT));
-                        short4_t r0, r1;
-                        asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
-                                     : "=&v"(r0), "=&v"(r1)
-                                     : "v"(va), "i"(off), "i"(off + 512));
-                        vr[t % (VA + 1)][0] = r0;
-                        vr[t % (VA + 1)][1] = r1;
-                    }
+                    if constexpr (t >= VA && t < NP) vread_dl(I);
                     if constexpr (t >= VA) {  // product j: its two reads done, those of the later products in flight
                         constexpr int j = t - VA;
                         if constexpr (kSplitHalves && j == NP / 2) settle(I1{}, I2{});
