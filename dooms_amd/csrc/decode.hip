@@ -91,8 +91,12 @@ struct KvBlock {
     static constexpr int KS = HD / 32;            // MFMA steps along head_dim
     static constexpr int LPR = HD / 8;            // lanes per value row (8 halves per lane)
     static constexpr int KPL = kWave / LPR;       // value rows per wave load
-    static constexpr int NLV = kBlockKeys / KPL;  // value loads per lane per block
-    u32x4 k[2][KS];
+    static constexpr int NLV = kBlockKeys / KPL;  // value (and key) loads per lane per block
+    // Keys and values are both loaded as whole row slices, LPR consecutive lanes per row: a load instruction that
+    // reads 16 rows x 64 bytes (the MFMA operand layout) streams ~10 % slower, and the row slices whose address
+    // bits 8..9 are 01 (two of Llama-3-8B's eight kv heads) ~17 % slower still; the keys reach the operand layout
+    // through LDS.
+    u32x4 k[NLV];
     u32x4 v[NLV];
 };
 
@@ -234,6 +238,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     constexpr int KS = B::KS, LPR = B::LPR, KPL = B::KPL, NLV = B::NLV;
 
     constexpr int VP = HD + 16;  // halves per row of a wave's V block in LDS (conflict-free transposing reads)
+    constexpr int KPD = HD + 8;  // halves per row of its K block (16 rows' 16-byte reads at one column: distinct banks)
+    static_assert(kBlockKeys * KPD <= kBlockKeys * VP, "the K block shares the V block's LDS");
     constexpr int kThreads = NW * kWave;
     static_assert(RT * HD * 4 <= kBlockKeys * VP * 2, "a wave's O rows reuse its V block's LDS");
     __shared__ half_t s_v[NW][kBlockKeys * VP];
@@ -304,11 +310,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
     auto load_block = [&](int jb, B & blk) {
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            const int key = min(jb + 16 * mt + srow, L - 1);
-            const half_t * kp = kbase + (int64_t)key * kv_stride + 8 * sgrp;
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) blk.k[mt][ks] = load16_kv<NT>(kp + 32 * ks);
+        for (int i = 0; i < NLV; i++) {
+            const int key = min(jb + KPL * i + vslot, L - 1);
+            blk.k[i] = load16_kv<NT>(kbase + (int64_t)key * kv_stride + vcol);
         }
 #pragma unroll
         for (int i = 0; i < NLV; i++) {
@@ -436,12 +440,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
         }
         if constexpr (F32) {
             if (wave_new && jb == jb_new) {  // the new key and value replace what the cache held at L - 1
-                const int mt_new = ((L - 1) % kBlockKeys) / 16, i_new = ((L - 1) % kBlockKeys) / KPL;
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)  // constant register indices: a runtime one would go through memory
-#pragma unroll
-                    for (int ks = 0; ks < KS; ks++)
-                        if (k_lane_new && mt == mt_new) cur.k[mt][ks] = kn[ks];
+                const int i_new = ((L - 1) % kBlockKeys) / KPL;
                 // Key slots past L - 1 were clamped to row L - 1, whose memory holds what the cache had before this
                 // step (and which the row-tile-0 workgroup is overwriting). Their scores are masked, but a stale
                 // Inf/NaN there would survive the p = 0 product, so their value operand is zero instead.
@@ -452,13 +451,37 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
                 }
             }
         }
+        // the wave's K block into LDS row-major, read back as the MFMA operand: lane holds K[16 mt + srow][32 ks + 8 sgrp
+        // .. + 8] (the buffer is the V block's, written below once these reads are done)
+#pragma unroll
+        for (int i = 0; i < NLV; i++)
+            *reinterpret_cast<u32x4 *>(vw + (KPL * i + vslot) * KPD + vcol) = cur.k[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        u32x4 kr[2][KS];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                kr[mt][ks] = *reinterpret_cast<const u32x4 *>(vw + (16 * mt + srow) * KPD + 32 * ks + 8 * sgrp);
+        if constexpr (F32) {
+            if (wave_new && jb == jb_new) {  // the new key replaces what the cache held at L - 1
+                const int mt_new = ((L - 1) % kBlockKeys) / 16;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)  // constant register indices: a runtime one would go through memory
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++)
+                        if (k_lane_new && mt == mt_new) kr[mt][ks] = kn[ks];
+            }
+        }
         // S^T = K Q^T, 2 tiles of 16 keys: lane holds keys 16 mt + 4 sgrp + v of row srow
         float sc[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
             float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) acc = mfma16x16x32(as_half8(cur.k[mt][ks]), qb[ks], acc);
+            for (int ks = 0; ks < KS; ks++) acc = mfma16x16x32(as_half8(kr[mt][ks]), qb[ks], acc);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int key = jb + 16 * mt + 4 * sgrp + v;
