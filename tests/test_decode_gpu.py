@@ -74,6 +74,14 @@ def test_one_sequence_heads_per_xcd(device, n_head, n_head_kv, n_q, causal):
     run_decode(device, 77 + n_q, n_head, n_head_kv, 128, [8192], n_q=n_q, causal=causal)
 
 
+@pytest.mark.parametrize("hd,n_head,L", [(64, 16, 3000), (256, 16, 8192), (128, 64, 5000)])
+def test_one_sequence_heads_per_xcd_head_dims(device, hd, n_head, L):
+    # the XCD-mapped grid at the other head dims (the per-pair publish of head dims 64 and 256, the 8-row tiles of a
+    # 64-head model): partials published into the XCD's L2 and counted per XCD
+    run_decode(device, 90 + hd, n_head, 8, hd, [L], check_heads=[0, 5, n_head - 1])
+    run_decode_f32(device, 91 + hd, n_head, 8, hd, [L])
+
+
 def test_llama3_8b_decode_128k(device):
     # a 131072-token context: 32 splits of 4096 keys per kv head, each wave walking 16 blocks before the merge
     run_decode(device, 76, 32, 8, 128, [131072], check_heads=[0, 9, 31])
