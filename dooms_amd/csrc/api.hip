@@ -453,7 +453,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         p.rows = s.rows;
         p.n_rowtiles = s.n_rowtiles;
         p.seq0 = b0;
-        p.xcd_heads = n_seq == 1 && d.n_head_kv % 8 == 0;
+        p.xcd_heads = n_seq == 1 && d.n_head_kv % 8 == 0;  // (widened below for short caches)
         // Non-temporal K/V loads for one long sequence (K/V streamed from HBM once per step in a decoder): Llama-3-8B
         // batch 1 at 8192 keys 11.93 -> 11.76 us per launch, batch 16 x 8192 keys -3.5 %; but slower where the bench's
         // caches stay in the Infinity Cache between replays (Qwen2.5-0.5B +8 %, Whisper cross-attention +10 %) and
@@ -498,6 +498,12 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
             p.max_split = std::max(p.max_split, p.seq[i].n_split);
         }
         for (int i = n_seq; i < mx::kMaxSeqPerLaunch; i++) p.seq[i] = mx::DecodeSeq{nullptr, nullptr, 0, 0};
+        // The XCD-mapped grid (partials published into one XCD's L2) also for one short sequence whatever its kv heads:
+        // a few splits over at most 4 MB of keys and values, where the merge chain outweighs the stream, which the
+        // grid concentrates on min(kv heads, 8) XCDs. Qwen2.5-0.5B at 513 keys 4.99 -> 4.50 us per launch, Whisper
+        // self-attention at 449 keys 5.25 -> 4.89, Qwen2.5-7B at 1024 keys 6.67 -> 6.42; 16 splits (Qwen2.5-0.5B at
+        // 2048 keys, two XCDs streaming) measured 5.87 -> 6.02, Whisper cross-attention (12 splits, 7.7 MB) no gain.
+        if (n_seq == 1 && p.max_split <= 8 && kv_bytes <= ((int64_t)4 << 20)) p.xcd_heads = 1;
         const int waves = decode_waves(d.tuning, p.chunk, launch_wgs(p.chunk));
         if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, waves, st), "decode launch")) return rc;
     }

@@ -775,7 +775,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 template <int HD, int RT, int NW>
 hipError_t launch_decode_t(const DecodeParams & p, int n_seq, hipStream_t stream) {
     // x: groups of (split, kv head), 8 per round of XCDs, each group's row tiles on one XCD; y: the sequence
-    const int64_t groups = (int64_t)p.max_split * p.n_head_kv;
+    // (the XCD-mapped grid: kv head g's splits at ids = g mod 8, so the kv heads round up to a multiple of 8)
+    const int64_t groups = (int64_t)p.max_split * (p.xcd_heads ? (p.n_head_kv + 7) / 8 * 8 : p.n_head_kv);
     const dim3 grid((uint32_t)(((groups + 7) / 8) * 8 * p.n_rowtiles), (uint32_t)n_seq);
     if constexpr (HD == 128 && RT == 4) {  // one query row per Llama-3-8B-shaped sequence (4 query heads per kv head)
         if (p.kv_nt) {
