@@ -453,11 +453,15 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         p.rows = s.rows;
         p.n_rowtiles = s.n_rowtiles;
         p.seq0 = b0;
-        p.xcd_heads = n_seq == 1 && d.n_head_kv % 8 == 0;  // (widened below for short caches)
-        // Non-temporal K/V loads for one long sequence (K/V streamed from HBM once per step in a decoder): Llama-3-8B
-        // batch 1 at 8192 keys 11.93 -> 11.76 us per launch, batch 16 x 8192 keys -3.5 %; but slower where the bench's
-        // caches stay in the Infinity Cache between replays (Qwen2.5-0.5B +8 %, Whisper cross-attention +10 %) and
-        // on the batch-4 shape (55 MB of K/V, +4 %), hence one sequence with at least 16 MB, or at least 256 MB.
+        // The XCD-mapped grid (kv head g's splits on XCD g mod 8, partials published into that XCD's L2) for kv heads in
+        // multiples of 8, also for batches: Llama-3-8B batch 4 (ragged, 55 MB) 16.97 -> 15.7 us, batch 16 ragged 55.3
+        // -> 50.4, 32 x 4096 keys 100.8 -> 97.2 (widened below for short caches)
+        p.xcd_heads = d.n_head_kv % 8 == 0;
+        // Non-temporal K/V loads on the XCD-mapped grid with at least 16 MB of K/V, or any grid with at least 256 MB
+        // (K/V streamed from HBM once per step in a decoder): Llama-3-8B batch 1 at 8192 keys 11.93 -> 11.76 us per
+        // launch, batch 16 x 8192 keys -3.5 %; on the XCD-mapped grid batch 4 (55 MB) 16.7 -> 15.7 us and batch 16
+        // ragged 55.9 -> 50.4; but slower where the bench's caches stay in the Infinity Cache between replays
+        // (Qwen2.5-0.5B +8 %, Whisper cross-attention +10 %), hence the 16 MB floor.
         int64_t kv_keys = 0;
         for (int i = 0; i < n_seq; i++) kv_keys += kv_len[b0 + i];
         const int64_t kv_bytes = kv_keys * d.kv_stride * 2 * 2;

@@ -291,10 +291,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
     // Work item. The row tiles of one (sequence, kv head, split) read the same keys and values, so they run as
     // consecutive workgroups of one XCD (workgroups are dealt to the 8 XCDs round-robin: ids 8 apart share one), where
-    // all but the first read hit that XCD's L2. With one row tile this is the identity. With xcd_heads (one sequence,
-    // a multiple of 8 kv heads) every split of kv head g runs on XCD g % 8 instead: each XCD streams whole kv heads and
-    // the merging workgroup finds the partials of its head written from its own XCD (Llama-3-8B at 8192 keys 13.9 ->
-    // 13.6 us; with many sequences the plain order streams better: batch 16, 57.2 vs 58.3 us).
+    // all but the first read hit that XCD's L2. With one row tile this is the identity. With xcd_heads (kv heads in
+    // multiples of 8, or one short sequence with its kv heads padded to a multiple of 8) every split of kv head g runs
+    // on XCD g % 8 instead (the sequence is blockIdx.y; the grid's x extent is a multiple of 8): each XCD streams whole
+    // kv heads and the merging workgroup finds the partials of its head in its own XCD's L2.
     if (threadIdx.x == 0) {
         MX_TRACE(0);
         MX_TRACE_CLEAR(12);
