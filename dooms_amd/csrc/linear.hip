@@ -10,7 +10,7 @@
 //
 // MI355X design:
 //   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). One workgroup per CU
-//     (1 to 8 waves, as the rows divide) stages the (normalized) input rows in LDS once; each wave owns 4 weight rows and
+//     (1 to 8 waves, as the rows divide) stages the (normalized) input rows in LDS once; each wave owns 2 or 4 weight rows and
 //     streams them in 16-byte non-temporal loads (the weights are read once per step; the cache lines are not kept:
 //     q|k|v 12.9 -> 11.7 us, attn_output 10.1 -> 9.3 us, a 14336-column down projection 26.0 -> 23.2 us), 4 sweeps of 4
 //     loads in flight per lane. The input rows' loads go out first, in one
@@ -177,7 +177,7 @@ __device__ __forceinline__ void store_col16(const LinearParams & p, int mi, int 
 }
 
 // ---- M <= 8: f32 input rows in LDS, 4 weight rows per wave ----
-constexpr int kGemvRows = 4;       // weight rows per wave
+constexpr int kGemvRows = 4;       // weight rows per wave (the most)
 constexpr int kGemvMaxWaves = 8;   // waves per workgroup (the launch sizes workgroups so that each CU gets one)
 constexpr int kGemvDepth = 4;      // 64-lane sweeps of 16-byte weight loads in flight per wave
 
@@ -185,7 +185,7 @@ constexpr int kGemvDepth = 4;      // 64-lane sweeps of 16-byte weight loads in 
 // L2 as it goes (the reference's kStageInput = false variant, metal_llama_decoder.mm:45-47).
 // The wave's first kGemvDepth sweeps of weight loads are issued before the input is staged, so the staging and its
 // barriers overlap the first HBM round trip.
-template <int MT, bool STAGE, bool OUT16, bool NORM>
+template <int MT, bool STAGE, bool OUT16, bool NORM, int RW>
 __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParams p) {
     extern __shared__ float xs[];  // [MT][K]: x (* gamma) of each input row, when staged
     __shared__ float red[MT][kGemvMaxWaves];
@@ -196,21 +196,21 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 
     // work item: (matrix, group of 4 rows) per wave
-    const int groups = (p.N + kGemvRows - 1) / kGemvRows;
+    const int groups = (p.N + RW - 1) / RW;
     const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * nw + wave);  // wave-uniform: scalar loads of p.w[mi]
     const bool active = item < groups * p.count;
     const int mi = active ? item / groups : 0;
-    const int r0 = active ? (item % groups) * kGemvRows : 0;
+    const int r0 = active ? (item % groups) * RW : 0;
     const half_t * w = p.w[mi];
-    const half_t * wr[kGemvRows];
+    const half_t * wr[RW];
 #pragma unroll
-    for (int i = 0; i < kGemvRows; i++) wr[i] = w + (int64_t)min(r0 + i, p.N - 1) * K;
+    for (int i = 0; i < RW; i++) wr[i] = w + (int64_t)min(r0 + i, p.N - 1) * K;
     const int C8 = K / 8;  // 16-byte chunks per row
-    half8_t wv[kGemvDepth][kGemvRows];
+    half8_t wv[kGemvDepth][RW];
     auto load_sweep = [&](int j, int c) __attribute__((always_inline)) {
         const int cc = min(c, C8 - 1);  // past the row: a valid chunk, not used
 #pragma unroll
-        for (int i = 0; i < kGemvRows; i++)  // non-temporal: each weight is read once per step
+        for (int i = 0; i < RW; i++)  // non-temporal: each weight is read once per step
             wv[j][i] = as_half8(__builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4 *)(wr[i] + 8 * cc)));
     };
 
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     // where each was one more memory round trip at the end of the kernel
     float y_prev = 0.f, y_bias = 0.f;
     {
-        const int i = min(lane / MT, kGemvRows - 1), m = min(lane % MT, M - 1), n = min(r0 + i, p.N - 1);
+        const int i = min(lane / MT, RW - 1), m = min(lane % MT, M - 1), n = min(r0 + i, p.N - 1);
         if (p.flags & kLinearAccumulate) {
             const int64_t o = (int64_t)m * p.y_stride + n;
             if constexpr (OUT16) y_prev = (float)static_cast<const half_t *>(p.y[mi])[o];
@@ -295,9 +295,9 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     __syncthreads();
     if (!active) return;  // after the last barrier
 
-    float acc[kGemvRows][MT];
+    float acc[RW][MT];
 #pragma unroll
-    for (int i = 0; i < kGemvRows; i++)
+    for (int i = 0; i < RW; i++)
 #pragma unroll
         for (int m = 0; m < MT; m++) acc[i][m] = 0.f;
     auto sweep = [&](int j, int c) __attribute__((always_inline)) {
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
                 }
             }
 #pragma unroll
-            for (int i = 0; i < kGemvRows; i++) {
+            for (int i = 0; i < RW; i++) {
                 float a = acc[i][m];
 #pragma unroll
                 for (int e = 0; e < 4; e++) a = __builtin_fmaf((float)wv[j][i][e], x0[e], a);
@@ -348,13 +348,13 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     // reduce over the wave; lane i * MT + m stores (row r0 + i, input row m)
     float mine = 0.f;
 #pragma unroll
-    for (int i = 0; i < kGemvRows; i++)
+    for (int i = 0; i < RW; i++)
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             const float s = wave_sum(acc[i][m]);
             if (lane == i * MT + m) mine = s;
         }
-    if (lane < kGemvRows * MT) {
+    if (lane < RW * MT) {
         const int i = lane / MT, m = lane % MT, n = r0 + i;
         if (m < M && n < p.N) {  // store_y's sums, with the bias and the previous output loaded above
             float v = norm ? mine * s_scale[m] : mine;
@@ -689,11 +689,11 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_mid_kernel(LinearParams p
 template <bool OUT16, int BK>
 __global__ __launch_bounds__(kBigThreads, 1) void gemm_w192_kernel(LinearParams p) { gemm_big_tile<OUT16, 192, 96, BK>(p); }
 
-// Waves per workgroup: the (matrix, 4-row group) items spread evenly over the CUs, one workgroup per CU (the weight
+// Waves per workgroup: the (matrix, RW-row group) items spread evenly over the CUs, one workgroup per CU (the weight
 // stream of each CU then ends at the same time), up to 8 waves; beyond 2048 items, several workgroups of 8 per CU.
-template <int MT>
-hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
-    const int64_t items = (int64_t)((p.N + kGemvRows - 1) / kGemvRows) * p.count;
+template <int MT, int RW>
+hipError_t launch_gemv_rw(const LinearParams & p, hipStream_t stream) {
+    const int64_t items = (int64_t)((p.N + RW - 1) / RW) * p.count;
     const int nw = (int)std::min<int64_t>(kGemvMaxWaves, std::max<int64_t>(1, (items + 255) / 256));
     const dim3 grid((uint32_t)((items + nw - 1) / nw));
     const dim3 block((uint32_t)(nw * kWave));
@@ -701,16 +701,28 @@ hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
     const int v = (lds <= kLinearGemvLds ? 4 : 0) | ((p.flags & kLinearOutF16) ? 2 : 0) | ((p.flags & kLinearNorm) ? 1 : 0);
     const size_t dyn = (v & 4) ? lds : 0;
     switch (v) {
-        case 0: hipLaunchKernelGGL((gemv_kernel<MT, false, false, false>), grid, block, dyn, stream, p); break;
-        case 1: hipLaunchKernelGGL((gemv_kernel<MT, false, false, true>), grid, block, dyn, stream, p); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<MT, false, true, false>), grid, block, dyn, stream, p); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<MT, false, true, true>), grid, block, dyn, stream, p); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<MT, true, false, false>), grid, block, dyn, stream, p); break;
-        case 5: hipLaunchKernelGGL((gemv_kernel<MT, true, false, true>), grid, block, dyn, stream, p); break;
-        case 6: hipLaunchKernelGGL((gemv_kernel<MT, true, true, false>), grid, block, dyn, stream, p); break;
-        default: hipLaunchKernelGGL((gemv_kernel<MT, true, true, true>), grid, block, dyn, stream, p); break;
+        case 0: hipLaunchKernelGGL((gemv_kernel<MT, false, false, false, RW>), grid, block, dyn, stream, p); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<MT, false, false, true, RW>), grid, block, dyn, stream, p); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<MT, false, true, false, RW>), grid, block, dyn, stream, p); break;
+        case 3: hipLaunchKernelGGL((gemv_kernel<MT, false, true, true, RW>), grid, block, dyn, stream, p); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<MT, true, false, false, RW>), grid, block, dyn, stream, p); break;
+        case 5: hipLaunchKernelGGL((gemv_kernel<MT, true, false, true, RW>), grid, block, dyn, stream, p); break;
+        case 6: hipLaunchKernelGGL((gemv_kernel<MT, true, true, false, RW>), grid, block, dyn, stream, p); break;
+        default: hipLaunchKernelGGL((gemv_kernel<MT, true, true, true, RW>), grid, block, dyn, stream, p); break;
     }
     return hipGetLastError();
+}
+
+// Rows per wave: 2 where the items still fit one workgroup per CU, i.e. twice the waves streaming the same bytes
+// (A/B on one box, us per launch: Llama-3-8B attention output 8.77 -> 8.41, a 14336-column down projection
+// 23.36 -> 22.69, Whisper attention output 3.73 -> 3.63, Qwen2.5-0.5B 3.33 -> 3.24, eight input rows 21.2 -> 19.7;
+// unchanged at two rows and the q|k|v width, which takes 4 rows per wave to fit). Four input rows keep 4 rows per
+// wave: with 2 they ran 16.5 -> 20.2 us.
+template <int MT>
+hipError_t launch_gemv_t(const LinearParams & p, hipStream_t stream) {
+    const int64_t cap = (int64_t)256 * kGemvMaxWaves;  // one workgroup of at most 8 waves per CU
+    if (MT != 4 && (int64_t)((p.N + 1) / 2) * p.count <= cap) return launch_gemv_rw<MT, 2>(p, stream);
+    return launch_gemv_rw<MT, kGemvRows>(p, stream);
 }
 
 }  // namespace
