@@ -179,17 +179,22 @@ __device__ __forceinline__ void store_col16(const LinearParams & p, int mi, int 
 // ---- M <= 8: f32 input rows in LDS, 4 weight rows per wave ----
 constexpr int kGemvRows = 4;       // weight rows per wave (the most)
 constexpr int kGemvMaxWaves = 8;   // waves per workgroup (the launch sizes workgroups so that each CU gets one)
-constexpr int kGemvDepth = 4;      // 64-lane sweeps of 16-byte weight loads in flight per wave
+// 64-lane sweeps of 16-byte weight loads in flight per wave: 4, and 8 with eight input rows (more arithmetic per
+// weight byte; Llama-3-8B attention output at 8 rows 19.7 -> 17.2 us, while at 1, 2 and 4 rows 8 sweeps were 3-25 %
+// slower than 4)
+template <int MT>
+constexpr int gemv_depth() { return MT == 8 ? 8 : 4; }
 
 // STAGE: the input rows (times gamma) fit the LDS budget and are staged once; otherwise every wave reads them from
 // L2 as it goes (the reference's kStageInput = false variant, metal_llama_decoder.mm:45-47).
-// The wave's first kGemvDepth sweeps of weight loads are issued before the input is staged, so the staging and its
+// The wave's first gemv_depth sweeps of weight loads are issued before the input is staged, so the staging and its
 // barriers overlap the first HBM round trip.
 template <int MT, bool STAGE, bool OUT16, bool NORM, int RW>
 __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParams p) {
     extern __shared__ float xs[];  // [MT][K]: x (* gamma) of each input row, when staged
     __shared__ float red[MT][kGemvMaxWaves];
     __shared__ float s_scale[MT];
+    constexpr int kGemvDepth = gemv_depth<MT>();
     const int K = p.K, M = p.M;
     constexpr bool norm = NORM;  // p.flags & kLinearNorm
     const int nw = blockDim.x / kWave;
