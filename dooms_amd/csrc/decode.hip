@@ -282,6 +282,11 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     asm volatile("" : "+s"(seq_k), "+s"(seq_v), "+s"(L), "+s"(n_split), "+s"(T), "+s"(max_split), "+s"(n_head_kv),
                  "+s"(chunk), "+s"(G), "+s"(seq0), "+s"(n_q), "+s"(rows), "+s"(causal), "+s"(xcd_heads), "+s"(q_stride),
                  "+s"(kv_stride), "+s"(qp));
+    // the fused step's own arguments likewise (fetched behind branches they cost dependent scalar round trips ahead
+    // of the first K/V load)
+    const float * qkv = p.qkv;
+    int32_t n_head = p.n_head, append = p.append, rope_mode = p.rope_mode;
+    if constexpr (F32) asm volatile("" : "+s"(qkv), "+s"(n_head), "+s"(append), "+s"(rope_mode));
     // fused step: this thread's rotary frequency (threads 0 .. HD / 2 - 1 use theirs) as one vector load of the
     // kernel arguments, issued before the first K/V block so that it returns ahead of it (loads return in order) and
     // is waited for with the new key and value. As uniform-index scalar loads the compiler issued them after the block
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
     half8_t qb[KS];
     float xq[F32 ? KS : 1][8] = {};  // the f32 query (fused step: rotated once the first block's loads are out)
     if constexpr (F32) {
-        const float * qrow = p.qkv + (seq_row0 + st) * p.q_stride + (int64_t)sh * HD;
+        const float * qrow = qkv + (seq_row0 + st) * q_stride + (int64_t)sh * HD;
         if (srow_ok) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(qrow + 32 * ks + 8 * sgrp, xq[ks]);
@@ -359,20 +364,20 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
     // fused step: the new position L - 1 lies in the block starting at jb_new, walked by one wave of the last split
     const int jb_new = (L - 1) & ~(kBlockKeys - 1);
-    const bool wave_new = F32 && p.append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % NW == wave;
+    const bool wave_new = F32 && append && j1 == L && jb_new >= j0 && ((jb_new - j0) / kBlockKeys) % NW == wave;
     const bool k_lane_new = wave_new && srow == (L - 1) % 16;       // holds the new key in tile (L - 1) % 32 / 16
     const bool v_lane_new = wave_new && vslot == (L - 1) % KPL;     // holds the new value in load (L - 1) % 32 / KPL
     // The fused step's own loads (the new key and value) go out before the first block of keys
     // and values: a wait for them then leaves that block's loads in flight (loads complete in the order issued).
     float x[F32 ? KS : 1][8], xv[8];
     if constexpr (F32) {
-        const float * row = p.qkv + seq_row0 * p.q_stride;
+        const float * row = qkv + seq_row0 * q_stride;
         if (k_lane_new) {
-            const float * kr = row + (int64_t)(p.n_head + g) * HD + 8 * sgrp;
+            const float * kr = row + (int64_t)(n_head + g) * HD + 8 * sgrp;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) load8f(kr + 32 * ks, x[ks]);
         }
-        if (v_lane_new) load8f(row + (int64_t)(p.n_head + p.n_head_kv + g) * HD + vcol, xv);
+        if (v_lane_new) load8f(row + (int64_t)(n_head + n_head_kv + g) * HD + vcol, xv);
     }
 
     // the first block of keys and values goes out right behind the query (unconditionally: keys past the split are
@@ -404,7 +409,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
 
     u32x4 kn[KS], vn = {0u, 0u, 0u, 0u};
     if constexpr (F32) {  // fused step: the query and the new key rotated, the new key and value rounded to half
-        if (p.append && p.rope_mode != 2) {  // the 64 (hd 128) angles of position L - 1, once per workgroup
+        if (append && rope_mode != 2) {  // the 64 (hd 128) angles of position L - 1, once per workgroup
             if (threadIdx.x < HD / 2) {
                 float sn, cs;
                 sincos_rope((float)(L - 1) * freq, sn, cs);
@@ -412,11 +417,11 @@ __global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeParams p) {
             }
             __syncthreads();
         }
-        if (srow_ok && p.append) rope_rotate<KS, 32>(xq, 8 * sgrp, p.rope_mode, [&](int i) { return s_cs[i]; });
+        if (srow_ok && append) rope_rotate<KS, 32>(xq, 8 * sgrp, rope_mode, [&](int i) { return s_cs[i]; });
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qb[ks] = as_half8(to_half8(xq[ks]));
         if (k_lane_new) {
-            rope_rotate<KS, 32>(x, 8 * sgrp, p.rope_mode, [&](int i) { return s_cs[i]; });
+            rope_rotate<KS, 32>(x, 8 * sgrp, rope_mode, [&](int i) { return s_cs[i]; });
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) kn[ks] = to_half8(x[ks]);
             if (rt == 0) {

@@ -185,8 +185,9 @@ __device__ __forceinline__ void rope_rotate(float (&x)[N][8], int off, int mode,
     }
 }
 
-__device__ __forceinline__ void load8f(const float * src, float (&x)[8]) {
-    const float4_t a = *reinterpret_cast<const float4_t *>(src), b = *reinterpret_cast<const float4_t *>(src + 4);
+__device__ __forceinline__ void load8f(const float * src, float (&x)[8]) {  // global memory (global loads, not flat)
+    typedef const __attribute__((address_space(1))) float4_t * gp;
+    const float4_t a = *(gp)(src), b = *(gp)(src + 4);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         x[e] = a[e];
