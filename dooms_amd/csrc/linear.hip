@@ -12,8 +12,8 @@
 //   * M <= 8 (decode): gemv_kernel, HBM-bound on the weights (2 N K bytes, each read once). One workgroup per CU
 //     (1 to 8 waves, as the rows divide) stages the (normalized) input rows in LDS once; each wave owns 2 or 4 weight rows and
 //     streams them in 16-byte non-temporal loads (the weights are read once per step; the cache lines are not kept:
-//     q|k|v 12.9 -> 11.7 us, attn_output 10.1 -> 9.3 us, a 14336-column down projection 26.0 -> 23.2 us), 4 sweeps of 4
-//     loads in flight per lane. The input rows' loads go out first, in one
+//     q|k|v 12.9 -> 11.7 us, attn_output 10.1 -> 9.3 us, a 14336-column down projection 26.0 -> 23.2 us), 4 sweeps
+//     (8 with eight input rows) of 2 or 4 loads in flight per lane. The input rows' loads go out first, in one
 //     batch, then the first sweeps of weight loads, so that the staging waits only for the input; the dot products
 //     stay f32 and are reduced across the wave at the end.
 //   * M > 8 (prompt): stage_kernel writes each input row once as half(x * gamma * scale) into the workspace (the
@@ -176,7 +176,7 @@ __device__ __forceinline__ void store_col16(const LinearParams & p, int mi, int 
     }
 }
 
-// ---- M <= 8: f32 input rows in LDS, 4 weight rows per wave ----
+// ---- M <= 8: f32 input rows in LDS, 2 or 4 weight rows per wave ----
 constexpr int kGemvRows = 4;       // weight rows per wave (the most)
 constexpr int kGemvMaxWaves = 8;   // waves per workgroup (the launch sizes workgroups so that each CU gets one)
 // 64-lane sweeps of 16-byte weight loads in flight per wave: 4, and 8 with eight input rows (more arithmetic per
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kGemvMaxWaves * kWave) void gemv_kernel(LinearParam
     const int nw = blockDim.x / kWave;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 
-    // work item: (matrix, group of 4 rows) per wave
+    // work item: (matrix, group of RW rows) per wave
     const int groups = (p.N + RW - 1) / RW;
     const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * nw + wave);  // wave-uniform: scalar loads of p.w[mi]
     const bool active = item < groups * p.count;
