@@ -275,6 +275,25 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
     return k;
 }
 
+// Waves per workgroup of a causal head-dim-64 prefill (prefill_plan's cost model otherwise). Measured per plan (TFLOP/s,
+// forced plans 4 and 8, Qwen2.5-0.5B-shaped unless stated):
+//   * a chunk behind a prefix at least as long as itself, whose 8-wave grid leaves CUs idle: the 8-wave plan split by
+//     stream-K over every CU (8192 tokens in 2048-row chunks 415 -> 535, 16384 in 2048-row chunks 482 -> 657, 16 heads
+//     8192 in 2048-row chunks 474 -> 576, 8192 in 1024-row chunks 363 (the key-split plan) -> 393);
+//   * otherwise 4 waves (two workgroups per CU, whose barriers do not couple the waves sharing a SIMD) where the cost
+//     model took 8: one-call prompts of 4096 tokens 398 -> 470 (16 heads 388 -> 526, 12 heads 372 -> 411), 8192
+//     tokens 555 -> 688 (32 heads 738 -> 761), a 32-head 8192-token prompt in 2048-row chunks 682 -> 724; one case
+//     measured the other way, a 32-head 4096-token prompt 716 -> 698. The key-split plan for short prompts stays.
+int prefill_choose_plan(const mx_attn_desc & d, int64_t n_kv, bool sk_ok) {
+    const int forced = d.tuning ? d.tuning->prefill_plan : 0;
+    const int plan = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim, forced) / 32;
+    // (a forced stream-K choice, tuning->prefill_stream 1 or -1, keeps the cost model's plan)
+    if (forced != 0 || (d.tuning && d.tuning->prefill_stream != 0) || d.head_dim != 64 || !d.causal) return plan;
+    const int64_t wg8 = (int64_t)((d.n_q + 255) / 256) * d.n_head;
+    if (sk_ok && n_kv >= 2 * (int64_t)d.n_q && wg8 < kSkRanges && prefill_sk_plan(d, n_kv, 8).ranges > 0) return 8;
+    return plan == 2 ? 2 : 4;
+}
+
 int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_cache, const void * v_cache, void * out,
                      float * lse, mx_attn_stream stream, const mx_attn_rope * rope, void * ws = nullptr,
                      size_t ws_bytes = 0) {
@@ -319,8 +338,10 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.p0 = d.p0;
     p.n_kv = (int32_t)n_kv;
     p.causal = d.causal;
-    p.plan = d.tuning ? d.tuning->prefill_plan : 0;
-    const int rows = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim, p.plan);
+    // stream-K when planned and the workspace holds its slots
+    const bool sk_ok = ws && !(reinterpret_cast<uintptr_t>(ws) & 255u) && ws_bytes >= prefill_sk_ws_bytes(d.head_dim);
+    p.plan = prefill_choose_plan(d, n_kv, sk_ok);
+    const int rows = 32 * p.plan;
     p.n_qtiles = (d.n_q + rows - 1) / rows;
     p.scale_log2 = d.scale * 1.4426950408889634f;
     p.rope = rope != nullptr;
@@ -334,9 +355,9 @@ int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_c
     p.sk_total = 0;
     p.sk_part = nullptr;
     p.sk_counters = nullptr;
-    if (ws && !(reinterpret_cast<uintptr_t>(ws) & 255u)) {  // stream-K when planned and the workspace holds its slots
-        const SkPlan k = prefill_sk_plan(d, n_kv, rows / 32);
-        if (k.ranges > 0 && ws_bytes >= prefill_sk_ws_bytes(d.head_dim)) {
+    if (sk_ok) {
+        const SkPlan k = prefill_sk_plan(d, n_kv, p.plan);
+        if (k.ranges > 0) {
             p.sk_ranges = k.ranges;
             p.sk_total = k.total;
             p.sk_counters = static_cast<uint32_t *>(ws);
@@ -787,9 +808,7 @@ MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc) {
         if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim || d.p0 < 0 || d.n_kv < 0) return 0;
         const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
         if (n_kv > INT32_MAX) return 0;
-        const int plan =
-            mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim, d.tuning ? d.tuning->prefill_plan : 0) / 32;
-        return prefill_sk_plan(d, n_kv, plan).ranges > 0 ? prefill_sk_ws_bytes(d.head_dim) : 0;
+        return prefill_sk_plan(d, n_kv, prefill_choose_plan(d, n_kv, true)).ranges > 0 ? prefill_sk_ws_bytes(d.head_dim) : 0;
     }
     const int64_t L = prefill_split_keys(*desc);
     if (L < 1 || L > INT32_MAX) return 0;

@@ -213,11 +213,15 @@ def test_prefill_ws_checks():
     # the decode workspace (the counter region, 32 splits of partials), then room for the rotated f32 query rows of the
     # rope call
     assert n == 2048 * 256 + 32 * 4 * 7 * 16 * 132 * 4 + 16 * 28 * 128 * 4
-    # a 2048-row chunk of 28 heads: 224 tiles of the 8-wave grid for 256 CUs. At head dim 64 the stream-K split is
-    # planned; its workspace is the counter region, then 2 partial slots per range (256 ranges) of 8 waves x 64 lanes
-    # x (32 + 2) floats. At head dim 128 the grid runs (no workspace) unless the tuning forces the split.
-    big64 = desc(n_head=28, n_head_kv=4, head_dim=64, n_q=2048, p0=0, q_stride=1792, kv_stride=256, out_stride=1792)
+    # a 2048-row chunk of 28 heads: 224 tiles of the 8-wave grid for 256 CUs. At head dim 64, behind a prefix at least
+    # as long as the chunk, the stream-K split of the 8-wave plan is planned; its workspace is the counter region, then
+    # 2 partial slots per range (256 ranges) of 8 waves x 64 lanes x (32 + 2) floats. The same chunk as a whole prompt
+    # (p0 0) runs the 4-wave grid (no workspace). At head dim 128 the grid runs (no workspace) unless the tuning forces
+    # the split.
+    big64 = desc(n_head=28, n_head_kv=4, head_dim=64, n_q=2048, p0=2048, q_stride=1792, kv_stride=256, out_stride=1792)
     assert _lib.prefill_workspace_bytes(big64) == 2048 * 256 + 512 * 8 * 64 * 34 * 4
+    first64 = desc(n_head=28, n_head_kv=4, head_dim=64, n_q=2048, p0=0, q_stride=1792, kv_stride=256, out_stride=1792)
+    assert _lib.prefill_workspace_bytes(first64) == 0
     big = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584)
     assert _lib.prefill_workspace_bytes(big) == 0
     forced = desc(n_head=28, n_head_kv=4, n_q=2048, p0=0, q_stride=3584, kv_stride=512, out_stride=3584,
@@ -226,10 +230,9 @@ def test_prefill_ws_checks():
     off = desc(n_head=28, n_head_kv=4, head_dim=64, n_q=2048, p0=0, q_stride=1792, kv_stride=256, out_stride=1792,
                tuning=dict(prefill_stream=-1))
     assert _lib.prefill_workspace_bytes(off) == 0  # the flash kernel's own grid, no workspace
-    # a causal 4096-token prompt of 14 heads at head dim 64 (224 tiles): planned; of 32 heads (512 tiles, which the
-    # grid's heaviest-first dealing balances): not
+    # a causal 4096-token prompt at head dim 64 (no prefix: the 4-wave grid), of 14 heads or of 32: no workspace
     assert _lib.prefill_workspace_bytes(desc(n_head=14, n_head_kv=2, head_dim=64, n_q=4096, q_stride=896,
-                                             kv_stride=128, out_stride=896)) == 2048 * 256 + 512 * 8 * 64 * 34 * 4
+                                             kv_stride=128, out_stride=896)) == 0
     assert _lib.prefill_workspace_bytes(desc(n_head=32, n_head_kv=8, head_dim=64, n_q=4096, q_stride=2048,
                                              kv_stride=512, out_stride=2048)) == 0
     # 256 equal tiles (non-causal, 2048 rows of 32 heads): one full round of the grid, nothing to balance

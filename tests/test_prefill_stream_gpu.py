@@ -65,9 +65,10 @@ def test_qwen7b_chunk(device):
     run_case(device, 1, 2048, 6144, 28, 4, 128, forced=True, rows=rows)
 
 
-def test_qwen05b_prompt_planned(device):
-    # a 4096-token Qwen2.5-0.5B prompt (head dim 64, 224 tiles): the planner takes the split
-    run_case(device, 8, 4096, 0, 14, 2, 64, rows=list(range(0, 4096, 37)) + [4095])
+def test_qwen05b_chunk_planned(device):
+    # a 2048-row Qwen2.5-0.5B chunk behind a 4096-token prefix (head dim 64, 112 tiles of the 8-wave grid): the planner
+    # takes the split
+    run_case(device, 8, 2048, 4096, 14, 2, 64, rows=list(range(0, 2048, 37)) + [2047])
 
 
 def test_many_ranges_per_tile(device):
