@@ -245,7 +245,11 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
     SkPlan k;
     const int forced = d.tuning ? d.tuning->prefill_stream : 0;
     if (forced < 0 || plan != 8 || (d.head_dim != 64 && d.head_dim != 128)) return k;
-    if (forced == 0 && d.head_dim != 64) return k;
+    if (forced == 0 && d.head_dim != 64) {
+        // head dim 128: only a chunk of at most 128 tiles (half the CUs) behind a prefix at least 3x its length
+        const int64_t wg8 = (int64_t)((d.n_q + mx::kPrefillSkRows - 1) / mx::kPrefillSkRows) * d.n_head;
+        if (wg8 > kSkRanges / 2 || n_kv < 4 * (int64_t)d.n_q) return k;
+    }
     const int32_t n_qtiles = (d.n_q + mx::kPrefillSkRows - 1) / mx::kPrefillSkRows;
     const int64_t n_tiles = (int64_t)n_qtiles * d.n_head;
     if (n_tiles > kSkMaxTiles || (forced == 0 && n_tiles >= 4 * kSkRanges)) return k;
@@ -284,14 +288,27 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
 //     model took 8: one-call prompts of 4096 tokens 398 -> 470 (16 heads 388 -> 526, 12 heads 372 -> 411), 8192
 //     tokens 555 -> 688 (32 heads 738 -> 761), a 32-head 8192-token prompt in 2048-row chunks 682 -> 724; one case
 //     measured the other way, a 32-head 4096-token prompt 716 -> 698. The key-split plan for short prompts stays.
+// At head dim 128: a chunk of at most 128 8-wave tiles behind a prefix at least 3x its length takes the split 8-wave
+// plan (the grid leaves over half the CUs idle, which the clock under this kernel's power draw does not repay):
+// Qwen2.5-7B 16384 tokens in 1024-row chunks 777 -> 882, 8192 in 512-row chunks 481 -> 589, Llama-3-8B 16384 in
+// 1024-row chunks 863 -> 958, 8192 in 256-row chunks 294 -> 439; a whole prompt whose 8-wave grid is one round takes
+// 4 waves: Llama-3-8B 2048 tokens 508-539 -> 585-594, Qwen2.5-7B 2048 443-465 -> 554-559. 2048-row chunks (cfg5),
+// 4096-token prompts and short prompts unchanged.
 int prefill_choose_plan(const mx_attn_desc & d, int64_t n_kv, bool sk_ok) {
     const int forced = d.tuning ? d.tuning->prefill_plan : 0;
     const int plan = mx::prefill_rows_per_workgroup(d.n_q, d.n_head, (int)n_kv, d.head_dim, forced) / 32;
     // (a forced stream-K choice, tuning->prefill_stream 1 or -1, keeps the cost model's plan)
-    if (forced != 0 || (d.tuning && d.tuning->prefill_stream != 0) || d.head_dim != 64 || !d.causal) return plan;
+    if (forced != 0 || (d.tuning && d.tuning->prefill_stream != 0) || !d.causal) return plan;
     const int64_t wg8 = (int64_t)((d.n_q + 255) / 256) * d.n_head;
-    if (sk_ok && n_kv >= 2 * (int64_t)d.n_q && wg8 < kSkRanges && prefill_sk_plan(d, n_kv, 8).ranges > 0) return 8;
-    return plan == 2 ? 2 : 4;
+    if (d.head_dim == 64) {
+        if (sk_ok && n_kv >= 2 * (int64_t)d.n_q && wg8 < kSkRanges && prefill_sk_plan(d, n_kv, 8).ranges > 0) return 8;
+        return plan == 2 ? 2 : 4;
+    }
+    if (d.head_dim == 128) {
+        if (sk_ok && prefill_sk_plan(d, n_kv, 8).ranges > 0) return 8;
+        if (d.p0 == 0 && n_kv == d.n_q && plan == 8 && wg8 <= kSkRanges) return 4;
+    }
+    return plan;
 }
 
 int32_t prefill_impl(const mx_attn_desc * desc, const void * q, const void * k_cache, const void * v_cache, void * out,
