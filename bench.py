@@ -635,7 +635,9 @@ def main():
                            "chunks of 2048 queries against the growing f16 cache, N(0, 0.5) inputs; FLOPs count "
                            "unmasked pairs only (7.697 TFLOP per step)",
                "flops_per_step": fl,
-               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128,true,8,false,1,0>", "achieved": round(tflops, 1),
+               "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128,true,8,false,1,0> (chunks 1-15; chunk 0, the "
+                                                        "whole first 2048 rows, on prefill_kernel<128,true,4,false,1,0>)",
+                            "achieved": round(tflops, 1),
                             "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / F16_PEAK_TFLOPS, 4),
                             "traffic": measured_traffic("prefill_qwen7b_32k"), "avg_launch_us": round(avg_us, 2),
                             "launch_timing": "graph-timed region / launches; FLOPs per launch differ by chunk, so "
