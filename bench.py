@@ -467,9 +467,12 @@ def trace_decode(args):
         t = t[t[:, 0] >= last - 5000]  # the last launch's workgroups (older stamps are > 50 us earlier)
         t0 = t[:, 0].min()
         rel = lambda col, sel: (col[sel] - t0) / 100.0  # the real-time clock ticks at 100 MHz
-        waves = t[:, 1:9]
-        walk = np.where(waves > 0, waves, 0).max(axis=1)
-        cols = [walk, t[:, 9], t[:, 10], t[:, 11], t[:, 12], t[:, 13], t[:, 15]]
+        # stamps older than the workgroup's own start are left from earlier launches (a workgroup of the grid's
+        # padding returns after its start stamp)
+        fresh = lambda col: np.where(col >= t[:, 0], col, 0)
+        waves = np.where(t[:, 1:9] >= t[:, :1], t[:, 1:9], 0)
+        walk = waves.max(axis=1)
+        cols = [walk] + [fresh(t[:, c]) for c in (9, 10, 11, 12, 13, 15)]
         phases = {}
         for nm, col in zip(names, cols):
             sel = col > 0
@@ -477,7 +480,7 @@ def trace_decode(args):
                 x = rel(col, sel)
                 phases[nm] = {"p50": round(float(np.median(x)), 2), "max": round(float(x.max()), 2), "n": int(sel.sum())}
         print(json.dumps({"workload": name, "us_per_launch_graph": round(ms * 1000 / layers, 3),
-                          "workgroups": int(len(t)), "start_spread_us": round(float((t[:, 0].max() - t0) / 100), 2),
+                          "workgroups": int((walk > 0).sum()), "start_spread_us": round(float((t[:, 0].max() - t0) / 100), 2),
                           "phases_us_from_first_start": phases}), flush=True)
     return 0
 
