@@ -562,12 +562,23 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
 // 607 vs 640 us, the one measured loss at that bound).
 constexpr int64_t kPrefillSplitRows = 512, kPrefillSplitRowsLong = 1024, kPrefillSplitKeysPerRow = 64;
 int64_t prefill_split_keys(const mx_attn_desc & d);
+// At head dim 128 the flash kernel split by stream-K over the CUs (planned for a chunk of few tiles behind a long
+// prefix) takes the chunks of 128 rows and more, and of 64 rows over at least 16k keys, from this route (A/B on one box,
+// us: Qwen2.5-7B 128 rows at 30k keys 248 -> 135-139, Llama-3-8B 128 rows at 30k 244-247 -> 133, 256 rows at 30k
+// 452-465 -> 148, 128 rows at 8k 80-82 -> 56, 64 rows at 30k 134-139 -> 120-122; the route stays ahead up to 48 rows
+// at every length measured, and for 64 rows over 2k-8k keys).
 bool prefill_split_route(const mx_attn_desc & d) {
     if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim) return false;
     const int64_t rows = (int64_t)d.n_q * (d.n_head / d.n_head_kv);
     if (decode_seqs_per_launch(&d, decode_shape(&d).n_rowtiles) < 1) return false;
-    return rows <= kPrefillSplitRows ||
-           (rows <= kPrefillSplitRowsLong && prefill_split_keys(d) >= kPrefillSplitKeysPerRow * d.n_q);
+    const int64_t keys = prefill_split_keys(d);
+    if (!(rows <= kPrefillSplitRows || (rows <= kPrefillSplitRowsLong && keys >= kPrefillSplitKeysPerRow * d.n_q)))
+        return false;
+    if (d.head_dim == 128 && d.causal && d.p0 >= 0 && (d.n_q >= 128 || (d.n_q >= 64 && keys >= 16384))) {
+        const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
+        if (n_kv <= INT32_MAX && prefill_sk_plan(d, n_kv, prefill_choose_plan(d, n_kv, true)).ranges > 0) return false;
+    }
+    return true;
 }
 // keys the decode kernel walks: a causal chunk's rows see keys up to p0 + n_q - 1 (keys past them are masked anyway)
 int64_t prefill_split_keys(const mx_attn_desc & d) {

@@ -177,10 +177,11 @@ def test_prefill_ws_routes(device, N, chunk, n_head, n_head_kv, hd):
     check_prefill(device, 400 + N, N, n_head, n_head_kv, hd, rows=rows, chunk=chunk, workspace="auto")
 
 
-@pytest.mark.parametrize("M", [16, 128, 200])
+@pytest.mark.parametrize("M", [16, 48, 64, 128, 200])
 def test_prefill_ws_long_context(device, M):
-    # the last M prompt rows at the end of a 131072-token context (Qwen2.5-7B shape): 16 and 128 rows take the split-KV
-    # route, 200 rows (1400 packed rows per kv head) the flash kernel
+    # the last M prompt rows at the end of a 131072-token context (Qwen2.5-7B shape): 16 and 48 rows take the split-KV
+    # route, 64 and 128 rows (within its packed-row bound) the flash kernel split by stream-K over the CUs, 200 rows
+    # (1400 packed rows per kv head) the flash kernel as well
     rng = np.random.default_rng(420 + M)
     L, hd, heads = 131072, 128, [0, 6, 7, 27]
     q = torch.from_numpy(normal_f16(rng, (M, 28 * hd))).to(device)
