@@ -227,6 +227,7 @@ constexpr int32_t kSkRanges = 256;  // one range per CU
 constexpr int64_t kSkMaxTiles = (int64_t)kCounterRegion / 4;
 // At least this many blocks per range (below, the merge and the lost prefetch at the segment edges cost more).
 constexpr int64_t kSkMinBlocksPerRange = 8;
+constexpr int32_t kSkMinRanges = 192;
 
 size_t prefill_sk_ws_bytes(int head_dim) {
     const int64_t slot = head_dim == 64 ? mx::kPrefillSlotFloats<64> : mx::kPrefillSlotFloats<128>;
@@ -256,7 +257,11 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
     int64_t total = 0;
     for (int32_t qt = 0; qt < n_qtiles; qt++)
         total += (int64_t)d.n_head * mx::prefill_tile_blocks(qt, d.n_q, d.p0, (int32_t)n_kv, d.causal);
-    if (total < kSkMinBlocksPerRange * kSkRanges) return k;
+    // fewer ranges (down to kSkMinRanges) when the launch has too few blocks to give every CU kSkMinBlocksPerRange
+    // (A/B on one box, us: Qwen2.5-0.5B 128 rows at 8k keys 75 -> 41, 512 rows at 4k 46.5 -> 37.8, Qwen2.5-7B 128
+    // rows at 4k 61 -> 49; at ~130 ranges, chunks at 2k keys, the split was 7 % slower, hence the floor of 192)
+    const int32_t R = (int32_t)std::min<int64_t>(kSkRanges, total / kSkMinBlocksPerRange);
+    if (R < kSkMinRanges) return k;
     if (forced == 0) {
         // the grid: tiles heaviest first (causal: by query tile descending), each to the CU that frees first
         std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> cu;
@@ -272,9 +277,9 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
                 grid_time = std::max(grid_time, t);
             }
         }
-        if ((double)total / kSkRanges > 0.92 * (double)grid_time) return k;
+        if ((double)total / R > 0.92 * (double)grid_time) return k;
     }
-    k.ranges = kSkRanges;
+    k.ranges = R;
     k.total = total;
     return k;
 }
@@ -566,7 +571,9 @@ int64_t prefill_split_keys(const mx_attn_desc & d);
 // prefix) takes the chunks of 128 rows and more, and of 64 rows over at least 16k keys, from this route (A/B on one box,
 // us: Qwen2.5-7B 128 rows at 30k keys 248 -> 135-139, Llama-3-8B 128 rows at 30k 244-247 -> 133, 256 rows at 30k
 // 452-465 -> 148, 128 rows at 8k 80-82 -> 56, 64 rows at 30k 134-139 -> 120-122; the route stays ahead up to 48 rows
-// at every length measured, and for 64 rows over 2k-8k keys).
+// at every length measured, and for 64 rows over 2k-8k keys). At head dim 64 from 96 rows over at least 16k keys
+// (Qwen2.5-0.5B at 30k keys: 96 rows 71 -> 66, 128 rows 86 -> 67, 144 rows 77 -> 67; 20 heads of 64, 128 rows 100 ->
+// 78; below 96 rows, or over 8k keys, the route is ahead or level).
 bool prefill_split_route(const mx_attn_desc & d) {
     if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim) return false;
     const int64_t rows = (int64_t)d.n_q * (d.n_head / d.n_head_kv);
@@ -574,7 +581,9 @@ bool prefill_split_route(const mx_attn_desc & d) {
     const int64_t keys = prefill_split_keys(d);
     if (!(rows <= kPrefillSplitRows || (rows <= kPrefillSplitRowsLong && keys >= kPrefillSplitKeysPerRow * d.n_q)))
         return false;
-    if (d.head_dim == 128 && d.causal && d.p0 >= 0 && (d.n_q >= 128 || (d.n_q >= 64 && keys >= 16384))) {
+    const bool flash = d.head_dim == 128 ? d.n_q >= 128 || (d.n_q >= 64 && keys >= 16384)
+                                         : d.head_dim == 64 && d.n_q >= 96 && keys >= 16384;
+    if (flash && d.causal && d.p0 >= 0) {
         const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
         if (n_kv <= INT32_MAX && prefill_sk_plan(d, n_kv, prefill_choose_plan(d, n_kv, true)).ranges > 0) return false;
     }

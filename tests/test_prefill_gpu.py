@@ -196,6 +196,24 @@ def test_prefill_ws_long_context(device, M):
                  lse.cpu().numpy()[rows][:, heads], rl)
 
 
+@pytest.mark.parametrize("M", [64, 128])
+def test_prefill_ws_long_context_hd64(device, M):
+    # Qwen2.5-0.5B shape (14 q / 2 kv heads of 64), the last M rows of a 32768-token context: 64 rows on the split-KV
+    # route, 128 rows on the flash kernel split by stream-K
+    rng = np.random.default_rng(440 + M)
+    L, hd, heads = 32768, 64, [0, 6, 7, 13]
+    q = torch.from_numpy(normal_f16(rng, (M, 14 * hd))).to(device)
+    kn, vn = normal_f16(rng, (L, 2 * hd)), normal_f16(rng, (L, 2 * hd))
+    k, v = torch.from_numpy(kn).to(device), torch.from_numpy(vn).to(device)
+    out, lse = A.prefill(q, k, v, n_head=14, n_head_kv=2, head_dim=hd, p0=L - M, want_lse=True, workspace="auto")
+    torch.cuda.synchronize()
+    rows = [0, M // 2, M - 1]
+    ro, rl = ref_attention(q.cpu().numpy(), kn, vn, 14, 2, hd, 1 / np.sqrt(hd), p0=L - M, rows=rows, heads=heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    assert_close(out.cpu().numpy().astype(np.float64)[rows][:, cols], ro, hd, f"M={M}",
+                 lse.cpu().numpy()[rows][:, heads], rl)
+
+
 def test_prefill_ws_noncausal_and_extra_keys(device):
     # non-causal rows over n_kv keys, and a causal chunk with cache rows past its own (masked, not read)
     rng = np.random.default_rng(410)
