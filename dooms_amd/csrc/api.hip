@@ -38,8 +38,8 @@ bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) =
 
 int32_t check_tuning(const mx_attn_tuning * t) {
     if (!t) return MX_ATTN_OK;
-    if (t->decode_splits < 0 || t->decode_splits > 32)
-        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_splits (%d) must be 0 (planned) or 1..32", t->decode_splits);
+    if (t->decode_splits < 0 || t->decode_splits > 64)
+        return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_splits (%d) must be 0 (planned) or 1..64", t->decode_splits);
     if (t->decode_waves != 0 && t->decode_waves != 4 && t->decode_waves != 8)
         return fail(MX_ATTN_INVALID_ARGUMENT, "tuning->decode_waves (%d) must be 0 (planned), 4 or 8", t->decode_waves);
     if (t->decode_max_workgroups < 0)
@@ -95,6 +95,16 @@ int32_t hip_status(hipError_t e, const char * what) {
 // 7.25 us, Llama-3-8B at 1024 keys 8.9 -> 8.1 us).
 // The bound n_split <= ceil(len / quantum) keeps the workspace a function of the longest sequence alone.
 constexpr int kMaxSplits = 32;
+// One head-dim-128 sequence of at least 32k keys whose 32-split grid would leave CUs idle (fewer than 8 kv heads x row
+// tiles) takes up to 64 splits: Qwen2.5-7B (4 kv heads) at 32768 keys 24.4 -> 22.3 us, at 131072 keys 72-73 -> 62 us.
+// Shorter sequences keep 32 (at 8192 keys 64 splits ran 10.6 -> 12.4 us: the longer merge outweighs the stream), as do
+// head dim 64 (Qwen2.5-0.5B at 32768 keys 12.2 -> 13.0) and batches (4 x 8192 keys 20.6 -> 24.9).
+constexpr int kMaxSplitsFew = 64;
+constexpr int64_t kMaxSplitsFewKeys = 32768;
+int max_splits(const mx_attn_desc * d, int n_rowtiles, int64_t n_seq, int64_t lmax) {
+    const bool few = (int64_t)d->n_head_kv * n_rowtiles * kMaxSplits < 256;
+    return few && d->head_dim == 128 && n_seq == 1 && lmax >= kMaxSplitsFewKeys ? kMaxSplitsFew : kMaxSplits;
+}
 int workgroup_cap(const mx_attn_tuning * t) {
     return t && t->decode_max_workgroups > 0 ? t->decode_max_workgroups : 1536;
 }
@@ -147,7 +157,9 @@ WsLayout decode_ws_layout(const mx_attn_desc * d, int32_t batch, int32_t max_kv_
     const DecodeShape s = decode_shape(d);
     const int64_t seqs = std::min<int64_t>(batch, std::max<int64_t>(1, decode_seqs_per_launch(d, s.n_rowtiles)));
     // the split plan never makes more than kMaxSplits splits of a sequence, nor more than one per quantum of keys
-    const int64_t max_split = std::min<int64_t>(kMaxSplits, ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum);
+    const int64_t max_split = std::min<int64_t>(std::max(max_splits(d, s.n_rowtiles, batch, max_kv_len),
+                                                         d->tuning ? d->tuning->decode_splits : 0),
+                                                ((int64_t)max_kv_len + mx::kDecodeChunkQuantum - 1) / mx::kDecodeChunkQuantum);
     WsLayout w{0, 0};
     if (max_split <= 1 || d->head_dim < kMfmaMinHeadDim) return w;  // one split per sequence (or the per-query kernel)
     w.counter_bytes = kCounterRegion;
@@ -515,7 +527,8 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         int64_t lmax = 0;
         for (int i = 0; i < n_seq; i++) lmax = std::max<int64_t>(lmax, kv_len[b0 + i]);
         auto round_up = [&](int64_t x) { return (x + quantum - 1) / quantum * quantum; };
-        int64_t chunk = round_up((lmax + kMaxSplits - 1) / kMaxSplits);
+        const int64_t msplit = max_splits(&d, s.n_rowtiles, n_seq, lmax);
+        int64_t chunk = round_up((lmax + msplit - 1) / msplit);
         auto launch_wgs = [&](int64_t c) {
             int64_t n = 0;
             for (int i = 0; i < n_seq; i++) n += (kv_len[b0 + i] + c - 1) / c;
@@ -551,6 +564,7 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
         // self-attention at 449 keys 5.25 -> 4.89, Qwen2.5-7B at 1024 keys 6.67 -> 6.42; 16 splits (Qwen2.5-0.5B at
         // 2048 keys, two XCDs streaming) measured 5.87 -> 6.02, Whisper cross-attention (12 splits, 7.7 MB) no gain.
         if (n_seq == 1 && p.max_split <= 8 && kv_bytes <= ((int64_t)4 << 20)) p.xcd_heads = 1;
+        if (p.max_split > 32) p.xcd_heads = 0;  // the XCD-local counter counts at most 63 splits per XCD field
         const int waves = decode_waves(d.tuning, p.chunk, launch_wgs(p.chunk));
         if (int32_t rc = hip_status(mx::launch_decode(p, n_seq, d.head_dim, s.rt, waves, st), "decode launch")) return rc;
     }

@@ -51,7 +51,7 @@ constexpr int kBlockKeys = 32;  // keys per wave iteration
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMergeChunk = 16;  // splits whose partials one thread has in flight at once during the merge
-constexpr int kMaxSplitsPerTile = 32;  // the host's split plan never makes more
+constexpr int kMaxSplitsPerTile = 64;  // the host's split plan never makes more
 
 // Relaxed device-scope atomic accesses of float pairs: coherent across the XCDs without cache maintenance.
 __device__ __forceinline__ void publish2(float * p, float a, float b) {
@@ -92,8 +92,8 @@ __device__ __forceinline__ void publish2_xcd(float * p, float a, float b) {
 }
 // The XCD this wave runs on (HW_REG_XCC_ID, bits 0..3).
 __device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 7u; }
-// XCD-local split counter: 64 bits, six per XCD (at most kMaxSplitsPerTile = 32 splits), each split adding one to its
-// XCD's field. The split that completes the count merges only if every field but its own is zero.
+// XCD-local split counter: 64 bits, six per XCD (the host keeps the XCD-mapped grid to at most 32 splits), each split
+// adding one to its XCD's field. The split that completes the count merges only if every field but its own is zero.
 constexpr int kXccField = 6;
 
 // K/V loads; NT: non-temporal (the cache lines are not kept), for launches whose keys and values stream from HBM once

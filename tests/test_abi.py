@@ -100,7 +100,7 @@ def decode(d, lens=(100,), kp=None, vp=None, q=A, out=A, lse=0, ws=A, ws_bytes=1
     (dict(kv_stride=1016), _lib.INVALID_ARGUMENT, "kv_stride"),
     (dict(out_stride=100), _lib.INVALID_ARGUMENT, "out_stride"),
     (dict(q_stride=4100), _lib.INVALID_ARGUMENT, "multiples of 8"),
-    (dict(tuning=dict(decode_splits=33)), _lib.INVALID_ARGUMENT, "decode_splits"),
+    (dict(tuning=dict(decode_splits=65)), _lib.INVALID_ARGUMENT, "decode_splits"),
     (dict(tuning=dict(decode_splits=-1)), _lib.INVALID_ARGUMENT, "decode_splits"),
     (dict(tuning=dict(decode_waves=6)), _lib.INVALID_ARGUMENT, "decode_waves"),
     (dict(tuning=dict(decode_max_workgroups=-2)), _lib.INVALID_ARGUMENT, "decode_max_workgroups"),

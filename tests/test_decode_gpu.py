@@ -87,6 +87,15 @@ def test_llama3_8b_decode_128k(device):
     run_decode(device, 76, 32, 8, 128, [131072], check_heads=[0, 9, 31])
 
 
+@pytest.mark.parametrize("L", [32768, 131072])
+def test_qwen7b_decode_64_splits(device, L):
+    # 4 kv heads at 32k+ keys: up to 64 splits of the sequence (the 32-split grid would leave CUs idle), merged by the
+    # last of them
+    run_decode(device, 77, 28, 4, 128, [L], check_heads=[0, 13, 27])
+    if L == 32768:
+        run_decode_f32(device, 78, 28, 4, 128, [L], check_heads=[0, 13, 27])
+
+
 @pytest.mark.parametrize("batch", [4, 16])
 def test_llama3_8b_decode_batched(device, batch):
     # every head of every sequence against the oracle (a per-split or per-XCD indexing slip cannot hide in an

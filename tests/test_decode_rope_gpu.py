@@ -91,6 +91,11 @@ def test_qwen05b_rope_decode_513(device):
     run_rope(device, 2, 14, 2, 64, [513], 1, 1000000.0)
 
 
+def test_qwen7b_rope_decode_32k(device):
+    # the fused step over 64 splits (4 kv heads at 32768 keys), the new row in the last split
+    run_rope(device, 5, 28, 4, 128, [32768], 1, 1000000.0, check_heads=[0, 13, 27])
+
+
 @pytest.mark.parametrize("L", [1, 64, 65, 1000])
 def test_neox_hd128_rope_decode(device, L):
     run_rope(device, 30 + L, 28, 4, 128, [L], 1, 1000000.0)
