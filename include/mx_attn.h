@@ -69,7 +69,7 @@ typedef void * mx_attn_stream;
  * library reads no environment variable: these fields are the only way to change a plan.
  */
 typedef struct mx_attn_tuning {
-    int32_t decode_splits;         /* decode: splits of each sequence's keys, 1..32 (cross_splits); 0: planned */
+    int32_t decode_splits;         /* decode: splits of each sequence's keys, 1..64 (cross_splits); 0: planned */
     int32_t decode_waves;          /* decode: waves per workgroup, 4 or 8; 0: planned */
     int32_t decode_max_workgroups; /* decode: workgroup cap of one launch for the split plan, >= 1; 0: 1536 */
     int32_t prefill_plan;          /* flash prefill workgroups (prefill_tile): 8 = 8 waves x 32 query rows, 4 = 4 waves x
