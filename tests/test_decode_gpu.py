@@ -87,6 +87,16 @@ def test_llama3_8b_decode_128k(device):
     run_decode(device, 76, 32, 8, 128, [131072], check_heads=[0, 9, 31])
 
 
+@pytest.mark.parametrize("n_head,n_head_kv,hd,lens", [
+    (28, 4, 128, [6841, 1638, 2310, 2721]),          # Qwen2.5-7B batch 4
+    (28, 4, 128, [3000, 129, 4097]),                 # an odd batch
+    (14, 2, 64, [1024, 77, 3000, 513, 2048, 1, 700, 4096]),  # Qwen2.5-0.5B batch 8
+    (8, 1, 128, [5000, 300, 1000, 64, 2000, 33, 4000, 129])])  # one kv head
+def test_batched_few_kv_heads(device, n_head, n_head_kv, hd, lens):
+    # ragged batches of sequences with fewer than 8 kv heads, every sequence and head checked
+    run_decode(device, 60 + len(lens) + n_head_kv, n_head, n_head_kv, hd, lens)
+
+
 @pytest.mark.parametrize("L", [32768, 131072])
 def test_qwen7b_decode_64_splits(device, L):
     # 4 kv heads at 32k+ keys: up to 64 splits of the sequence (the 32-split grid would leave CUs idle), merged by the
