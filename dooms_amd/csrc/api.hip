@@ -588,7 +588,12 @@ int64_t prefill_split_keys(const mx_attn_desc & d);
 // at every length measured, and for 64 rows over 2k-8k keys). At head dim 64 from 96 rows over at least 16k keys
 // (Qwen2.5-0.5B at 30k keys: 96 rows 71 -> 66, 128 rows 86 -> 67, 144 rows 77 -> 67; 20 heads of 64, 128 rows 100 ->
 // 78; below 96 rows, or over 8k keys, the route is ahead or level).
-bool prefill_split_route(const mx_attn_desc & d) {
+bool prefill_sk_room(const mx_attn_desc & d, const void * ws, size_t ws_bytes) {
+    return !(reinterpret_cast<uintptr_t>(ws) & 255u) && ws_bytes >= prefill_sk_ws_bytes(d.head_dim);
+}
+// sk_room: the workspace holds the stream-K slots (a chunk that the split flash kernel would take stays on this route
+// when it does not)
+bool prefill_split_route(const mx_attn_desc & d, bool sk_room) {
     if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim) return false;
     const int64_t rows = (int64_t)d.n_q * (d.n_head / d.n_head_kv);
     if (decode_seqs_per_launch(&d, decode_shape(&d).n_rowtiles) < 1) return false;
@@ -597,7 +602,7 @@ bool prefill_split_route(const mx_attn_desc & d) {
         return false;
     const bool flash = d.head_dim == 128 ? d.n_q >= 128 || (d.n_q >= 64 && keys >= 16384)
                                          : d.head_dim == 64 && d.n_q >= 96 && keys >= 16384;
-    if (flash && d.causal && d.p0 >= 0) {
+    if (flash && sk_room && d.causal && d.p0 >= 0) {
         const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
         if (n_kv <= INT32_MAX && prefill_sk_plan(d, n_kv, prefill_choose_plan(d, n_kv, true)).ranges > 0) return false;
     }
@@ -854,7 +859,7 @@ MX_ATTN_API int32_t mx_attn_prefill(const mx_attn_desc * desc, const uint16_t * 
 
 MX_ATTN_API size_t mx_attn_prefill_workspace_bytes(const mx_attn_desc * desc) {
     if (check_desc(desc)) return 0;
-    if (!prefill_split_route(*desc)) {  // the flash kernel: the stream-K slots when that plan is taken
+    if (!prefill_split_route(*desc, true)) {  // the flash kernel: the stream-K slots when that plan is taken
         const mx_attn_desc & d = *desc;
         if (d.n_q < 1 || d.head_dim < kMfmaMinHeadDim || d.p0 < 0 || d.n_kv < 0) return 0;
         const int64_t n_kv = d.n_kv == 0 ? (int64_t)d.p0 + d.n_q : d.n_kv;
@@ -871,7 +876,7 @@ MX_ATTN_API int32_t mx_attn_prefill_ws(const mx_attn_desc * desc, const uint16_t
                                        size_t ws_bytes, mx_attn_stream stream) {
     if (int32_t rc = check_desc(desc)) return rc;
     const mx_attn_desc & d = *desc;
-    if (!workspace || !prefill_split_route(d))
+    if (!workspace || !prefill_split_route(d, prefill_sk_room(d, workspace, ws_bytes)))
         return prefill_impl(desc, q, k_cache, v_cache, out, lse, stream, nullptr, workspace, ws_bytes);
     if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
     if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);
@@ -899,7 +904,7 @@ MX_ATTN_API int32_t mx_attn_prefill_rope_ws(const mx_attn_desc * desc, const mx_
     if (int32_t rc = check_desc(desc)) return rc;
     if (int32_t rc = check_rope(*desc, rope)) return rc;
     const mx_attn_desc & d = *desc;
-    if (!workspace || !prefill_split_route(d))
+    if (!workspace || !prefill_split_route(d, prefill_sk_room(d, workspace, ws_bytes)))
         return prefill_impl(desc, qkv, k_cache, v_cache, out, lse, stream, rope, workspace, ws_bytes);
     if (d.p0 < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "p0 (%d) must be >= 0", d.p0);
     if (d.n_kv < 0) return fail(MX_ATTN_INVALID_ARGUMENT, "n_kv (%d) must be >= 0", d.n_kv);

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from dooms_amd import _lib
 from dooms_amd import attention as A
 from helpers import assert_close, normal_f16, ref_attention
 from oracle import oracle as O
@@ -212,6 +213,29 @@ def test_prefill_ws_long_context_hd64(device, M):
     cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
     assert_close(out.cpu().numpy().astype(np.float64)[rows][:, cols], ro, hd, f"M={M}",
                  lse.cpu().numpy()[rows][:, heads], rl)
+
+
+def test_prefill_ws_short_workspace_keeps_route(device):
+    # 128 rows at 30k keys would take the stream-K flash kernel; with a workspace sized for the decode route only (no
+    # room for the stream-K slots) the chunk stays on the route, with the same results
+    rng = np.random.default_rng(450)
+    M, p0, hd, heads = 128, 30000, 128, [0, 6, 7, 27]
+    L = p0 + M
+    q = torch.from_numpy(normal_f16(rng, (M, 28 * hd))).to(device)
+    kn, vn = normal_f16(rng, (L, 4 * hd)), normal_f16(rng, (L, 4 * hd))
+    k, v = torch.from_numpy(kn).to(device), torch.from_numpy(vn).to(device)
+    d128 = _lib.make_desc(28, 4, hd, M, 28 * hd, 4 * hd, 28 * hd, 1 / np.sqrt(hd), p0=p0, causal=1)
+    small = _lib.decode_workspace_bytes(d128, 1, L)  # the route's own size for this chunk
+    assert 0 < small < _lib.prefill_workspace_bytes(d128)
+    ws = A.new_workspace(small, device)
+    out, lse = A.prefill(q, k, v, n_head=28, n_head_kv=4, head_dim=hd, p0=p0, want_lse=True, workspace=ws)
+    full, lfull = A.prefill(q, k, v, n_head=28, n_head_kv=4, head_dim=hd, p0=p0, want_lse=True, workspace="auto")
+    torch.cuda.synchronize()
+    rows = [0, 64, M - 1]
+    ro, rl = ref_attention(q.cpu().numpy(), kn, vn, 28, 4, hd, 1 / np.sqrt(hd), p0=p0, rows=rows, heads=heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    for o, l, what in ((out, lse, "route"), (full, lfull, "stream-K")):
+        assert_close(o.cpu().numpy().astype(np.float64)[rows][:, cols], ro, hd, what, l.cpu().numpy()[rows][:, heads], rl)
 
 
 def test_prefill_ws_noncausal_and_extra_keys(device):
