@@ -296,8 +296,9 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
     return k;
 }
 
-// Waves per workgroup of a causal head-dim-64 prefill (prefill_plan's cost model otherwise). Measured per plan (TFLOP/s,
-// forced plans 4 and 8, Qwen2.5-0.5B-shaped unless stated):
+// Waves per workgroup of a causal prefill at head dims 64 and 128 (prefill_plan's cost model otherwise; sk_ok: the
+// workspace holds the stream-K slots). At head dim 64, measured per plan (TFLOP/s, forced plans 4 and 8,
+// Qwen2.5-0.5B-shaped unless stated):
 //   * a chunk behind a prefix at least as long as itself, whose 8-wave grid leaves CUs idle: the 8-wave plan split by
 //     stream-K over every CU (8192 tokens in 2048-row chunks 415 -> 535, 16384 in 2048-row chunks 482 -> 657, 16 heads
 //     8192 in 2048-row chunks 474 -> 576, 8192 in 1024-row chunks 363 (the key-split plan) -> 393);
@@ -591,6 +592,9 @@ int32_t decode_impl(const mx_attn_desc * desc, int32_t batch, const int32_t * kv
 // 607 vs 640 us, the one measured loss at that bound).
 constexpr int64_t kPrefillSplitRows = 512, kPrefillSplitRowsLong = 1024, kPrefillSplitKeysPerRow = 64;
 int64_t prefill_split_keys(const mx_attn_desc & d);
+bool prefill_sk_room(const mx_attn_desc & d, const void * ws, size_t ws_bytes) {
+    return !(reinterpret_cast<uintptr_t>(ws) & 255u) && ws_bytes >= prefill_sk_ws_bytes(d.head_dim);
+}
 // At head dim 128 the flash kernel split by stream-K over the CUs (planned for a chunk of few tiles behind a long
 // prefix) takes the chunks of 128 rows and more, and of 64 rows over at least 16k keys, from this route (A/B on one box,
 // us: Qwen2.5-7B 128 rows at 30k keys 248 -> 135-139, Llama-3-8B 128 rows at 30k 244-247 -> 133, 256 rows at 30k
@@ -598,9 +602,6 @@ int64_t prefill_split_keys(const mx_attn_desc & d);
 // at every length measured, and for 64 rows over 2k-8k keys). At head dim 64 from 96 rows over at least 16k keys
 // (Qwen2.5-0.5B at 30k keys: 96 rows 71 -> 66, 128 rows 86 -> 67, 144 rows 77 -> 67; 20 heads of 64, 128 rows 100 ->
 // 78; below 96 rows, or over 8k keys, the route is ahead or level).
-bool prefill_sk_room(const mx_attn_desc & d, const void * ws, size_t ws_bytes) {
-    return !(reinterpret_cast<uintptr_t>(ws) & 255u) && ws_bytes >= prefill_sk_ws_bytes(d.head_dim);
-}
 // sk_room: the workspace holds the stream-K slots (a chunk that the split flash kernel would take stays on this route
 // when it does not)
 bool prefill_split_route(const mx_attn_desc & d, bool sk_room) {
