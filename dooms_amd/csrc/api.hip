@@ -272,7 +272,8 @@ SkPlan prefill_sk_plan(const mx_attn_desc & d, int64_t n_kv, int plan) {
     // fewer ranges (down to kSkMinRanges) when the launch has too few blocks to give every CU kSkMinBlocksPerRange
     // (A/B on one box, us: Qwen2.5-0.5B 128 rows at 8k keys 75 -> 41, 512 rows at 4k 46.5 -> 37.8, Qwen2.5-7B 128
     // rows at 4k 61 -> 49; at ~130 ranges, chunks at 2k keys, the split was 7 % slower, hence the floor of 192)
-    const int32_t R = (int32_t)std::min<int64_t>(kSkRanges, total / kSkMinBlocksPerRange);
+    // (a multiple of 8: the kernel deals range (b % 8) R / 8 + b / 8 to workgroup b, one eighth per XCD)
+    const int32_t R = (int32_t)(std::min<int64_t>(kSkRanges, total / kSkMinBlocksPerRange) / 8 * 8);
     if (R < kSkMinRanges) return k;
     if (forced == 0) {
         // the grid: tiles heaviest first (causal: by query tile descending), each to the CU that frees first

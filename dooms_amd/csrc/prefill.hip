@@ -777,7 +777,7 @@ void prefill_kernel(PrefillParams p) {
 // idles while another finishes a tile (a 2048-row chunk of 28 heads is 224 equal tiles for 256 CUs; a causal prompt's
 // tiles differ in length). Workgroup b runs on XCD b % 8 (workgroups are dealt to the XCDs round-robin) and takes range
 // (b % 8) R / 8 + b / 8: each XCD walks one contiguous eighth of the kv-head-major order, so its L2 streams the K/V of
-// few kv heads.
+// few kv heads. R is a multiple of 8 (the host's plan), so every range is dealt exactly once.
 template <int HD, bool POS, bool ROPE>
 __global__ __launch_bounds__(8 * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_sk_kernel(PrefillParams p) {

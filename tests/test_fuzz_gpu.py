@@ -79,3 +79,31 @@ def test_prefill_fuzz(device, seed):
     got = out.cpu().numpy().astype(np.float64)[rows][:, cols]
     assert_close(got, ro, hd, f"seed {seed}: {nh}/{nkv} hd {hd} M {M} p0 {p0} plan {plan} ws {ws} sigma {sigma}",
                  lse.cpu().numpy()[rows][:, heads], rl)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_long_prefix_fuzz(device, seed):
+    # chunks behind prefixes of 3..20x their length through mx_attn_prefill_ws with the planned route: the decode route
+    # for few rows, the flash kernel split by stream-K (all CUs, or fewer ranges for small launches), or its grid
+    rng = np.random.default_rng(3000 + seed)
+    nh, nkv = GROUPS[rng.integers(len(GROUPS))]
+    hd = [64, 128][rng.integers(2)]
+    M = int(rng.integers(32, 1101))
+    p0 = int(rng.integers(3 * M, min(20 * M, 20000) + 1))
+    sigma = float(rng.choice([0.25, 0.5, 1.0]))
+    N = p0 + M
+    q = normal_f16(rng, (M, nh * hd), sigma)
+    k = normal_f16(rng, (N, nkv * hd), sigma)
+    v = normal_f16(rng, (N, nkv * hd), sigma)
+    scale = 1.0 / np.sqrt(hd)
+    out, lse = A.prefill(torch.from_numpy(q).to(device), torch.from_numpy(k).to(device),
+                         torch.from_numpy(v).to(device), n_head=nh, n_head_kv=nkv, head_dim=hd, p0=p0, scale=scale,
+                         want_lse=True, workspace="auto")
+    torch.cuda.synchronize()
+    rows = sorted({0, M - 1, int(rng.integers(M)), int(rng.integers(M))})
+    heads = sorted({0, nh - 1, int(rng.integers(nh))})
+    ro, rl = ref_attention(q, k, v, nh, nkv, hd, scale, p0=p0, causal=True, rows=rows, heads=heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    got = out.cpu().numpy().astype(np.float64)[rows][:, cols]
+    assert_close(got, ro, hd, f"seed {seed}: {nh}/{nkv} hd {hd} M {M} p0 {p0} sigma {sigma}",
+                 lse.cpu().numpy()[rows][:, heads], rl)

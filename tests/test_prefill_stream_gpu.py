@@ -71,6 +71,14 @@ def test_qwen05b_chunk_planned(device):
     run_case(device, 8, 2048, 4096, 14, 2, 64, rows=list(range(0, 2048, 37)) + [2047])
 
 
+@pytest.mark.parametrize("n_q,p0,nh,nkv", [(128, 4000, 28, 4), (447, 7648, 8, 2)])
+def test_fewer_ranges_than_cus(device, n_q, p0, nh, nkv):
+    # launches of fewer than 8 blocks per CU: the split takes fewer ranges (224 and 248, multiples of 8, each dealt to
+    # exactly one workgroup); the second shape ran 250 ranges, two of them on one workgroup and one on none, before the
+    # plan rounded the count to a multiple of 8
+    run_case(device, 9, n_q, p0, nh, nkv, 128, rows=list(range(0, n_q, 11)) + [n_q - 1])
+
+
 def test_many_ranges_per_tile(device):
     # 2 query tiles x 8 heads of ~136 blocks over 256 ranges of ~8.5 blocks: each tile is merged from ~16 slots
     run_case(device, 2, 512, 8192, 8, 2, 128, forced=True, rows=list(range(0, 512, 7)) + [511])
