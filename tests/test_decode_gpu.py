@@ -114,6 +114,14 @@ def test_llama3_8b_decode_batched(device, batch):
     run_decode(device, 30 + batch, 32, 8, 128, lens)
 
 
+@pytest.mark.parametrize("n_head,n_head_kv,lens", [(32, 8, [8192, 7000, 6000, 7800]), (28, 4, [4096] * 8),
+                                                    (32, 8, [5000, 4500, 4100, 6000, 5900])])
+def test_uniform_batches_8_splits(device, n_head, n_head_kv, lens):
+    # batches of about one length (within 1.5x) of at least 4096 keys: at most 8 splits per sequence, each walking
+    # several 32-key blocks per wave; every sequence and head checked
+    run_decode(device, 50 + len(lens), n_head, n_head_kv, 128, lens)
+
+
 def test_batch_over_launch_limit(device):
     # 40 sequences > 32 per launch: two launches reuse the workspace
     lens = list(np.random.default_rng(7).integers(1, 700, size=40))
