@@ -1,7 +1,8 @@
 """Randomized parity sweep of the decode and prefill entry points against the f64 oracle (the same tolerance as the
 directed suites, helpers.assert_close). Every case draws its shape from a seeded generator: GQA groups of 1..16 query
 heads per kv head, head dims 4..256, cache lengths 1..6000, 1..5 sequences, 1..8 query rows, causal or not, input
-scales 0.25..2; prefill chunks of 1..600 rows at offsets 0..1500 with every plan. The seed of a failing case is in its
+scales 0.25..2; prefill chunks of 1..600 rows at offsets 0..1500 with every plan; long caches (single sequences up to
+40k keys, batches of about one length and ragged ones) and chunks behind prefixes of 3..20x their length. The seed of a failing case is in its
 test id, so the case reruns alone. Mirrors the reference's shape sweeps over its attention kernels
 (tests/unit/test_metal_llama_decoder.cpp, tests/unit/test_backend_ggml.cpp:677-745)."""
 import numpy as np
@@ -107,3 +108,39 @@ def test_prefill_long_prefix_fuzz(device, seed):
     got = out.cpu().numpy().astype(np.float64)[rows][:, cols]
     assert_close(got, ro, hd, f"seed {seed}: {nh}/{nkv} hd {hd} M {M} p0 {p0} sigma {sigma}",
                  lse.cpu().numpy()[rows][:, heads], rl)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_decode_long_fuzz(device, seed):
+    # long caches: one sequence of up to 40k keys (few kv heads: up to 64 splits) or batches of 4..6 of about one length
+    # (the 8-split plan) or ragged; head dims 64 and 128, one query row
+    rng = np.random.default_rng(4000 + seed)
+    nh, nkv = GROUPS[rng.integers(len(GROUPS))]
+    hd = [64, 128][rng.integers(2)]
+    kind = seed % 3
+    if kind == 0:
+        lens = [int(rng.integers(20000, 40001))]
+    elif kind == 1:
+        base = int(rng.integers(4096, 9001))
+        lens = [int(base * rng.uniform(1.0, 1.4)) for _ in range(int(rng.integers(4, 7)))]
+    else:
+        lens = [int(x) for x in rng.integers(1, 12001, size=int(rng.integers(2, 6)))]
+    batch = len(lens)
+    sigma = float(rng.choice([0.25, 0.5, 1.0]))
+    kvw = nkv * hd
+    q = normal_f16(rng, (batch, nh * hd), sigma)
+    ks = [normal_f16(rng, (L, kvw), sigma) for L in lens]
+    vs = [normal_f16(rng, (L, kvw), sigma) for L in lens]
+    scale = 1.0 / np.sqrt(hd)
+    out, lse = A.decode(torch.from_numpy(q).to(device), [torch.from_numpy(k).to(device) for k in ks],
+                        [torch.from_numpy(v).to(device) for v in vs], lens, n_head=nh, n_head_kv=nkv, head_dim=hd,
+                        want_lse=True)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy()
+    heads = sorted({0, nh - 1, int(rng.integers(nh))})
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    for b in range(batch):
+        ro, rl = ref_attention(q[b:b + 1], ks[b], vs[b], nh, nkv, hd, scale, p0=lens[b] - 1, causal=False, heads=heads)
+        assert_close(out[b:b + 1][:, cols], ro, hd, f"seed {seed}: {nh}/{nkv} hd {hd} lens {lens} sigma {sigma}",
+                     lse[b:b + 1][:, heads], rl)
