@@ -2,9 +2,12 @@
 directed suites, helpers.assert_close). Every case draws its shape from a seeded generator: GQA groups of 1..16 query
 heads per kv head, head dims 4..256, cache lengths 1..6000, 1..5 sequences, 1..8 query rows, causal or not, input
 scales 0.25..2; prefill chunks of 1..600 rows at offsets 0..1500 with every plan; long caches (single sequences up to
-40k keys, batches of about one length and ragged ones) and chunks behind prefixes of 3..20x their length. The seed of a failing case is in its
-test id, so the case reruns alone. Mirrors the reference's shape sweeps over its attention kernels
+40k keys, batches of about one length and ragged ones), chunks behind prefixes of 3..20x their length, and chunks with
+the plan or the stream-K split forced, causal or not (MX_FUZZ_SEEDS widens that sweep). The seed of a failing case is
+in its test id, so the case reruns alone. Mirrors the reference's shape sweeps over its attention kernels
 (tests/unit/test_metal_llama_decoder.cpp, tests/unit/test_backend_ggml.cpp:677-745)."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -144,3 +147,34 @@ def test_decode_long_fuzz(device, seed):
         ro, rl = ref_attention(q[b:b + 1], ks[b], vs[b], nh, nkv, hd, scale, p0=lens[b] - 1, causal=False, heads=heads)
         assert_close(out[b:b + 1][:, cols], ro, hd, f"seed {seed}: {nh}/{nkv} hd {hd} lens {lens} sigma {sigma}",
                      lse[b:b + 1][:, heads], rl)
+
+
+@pytest.mark.parametrize("seed", range(int(os.environ.get("MX_FUZZ_SEEDS", "12"))))
+def test_prefill_forced_fuzz(device, seed):
+    # chunks through mx_attn_prefill_ws with the plan or the stream-K split forced by the tuning fields, causal behind a
+    # prefix or not causal over a cache of any length (every query row sees every key)
+    rng = np.random.default_rng(3500 + seed)
+    nh, nkv = GROUPS[rng.integers(len(GROUPS))]
+    hd = [64, 128][rng.integers(2)]
+    M = int(rng.integers(1, 1101))
+    causal = bool(rng.random() < 0.6)
+    N = (M + int(rng.integers(0, 12001))) if causal else int(rng.integers(1, 12001))
+    p0 = N - M if causal else 0
+    tuning = {"prefill_stream": int(rng.choice([1, 1, -1]))} if rng.random() < 0.5 else {"prefill_plan": int(rng.choice([2, 4, 8]))}
+    sigma = float(rng.choice([0.25, 0.5, 1.0]))
+    q = normal_f16(rng, (M, nh * hd), sigma)
+    k = normal_f16(rng, (N, nkv * hd), sigma)
+    v = normal_f16(rng, (N, nkv * hd), sigma)
+    scale = 1.0 / np.sqrt(hd)
+    what = f"seed {seed}: {nh}/{nkv} hd {hd} M {M} N {N} causal {causal} tuning {tuning} sigma {sigma}"
+    print(what, flush=True)
+    out, lse = A.prefill(torch.from_numpy(q).to(device), torch.from_numpy(k).to(device),
+                         torch.from_numpy(v).to(device), n_head=nh, n_head_kv=nkv, head_dim=hd, p0=p0, causal=causal,
+                         n_kv=N, scale=scale, want_lse=True, workspace="auto", tuning=tuning)
+    torch.cuda.synchronize()
+    rows = sorted({0, M - 1, int(rng.integers(M)), int(rng.integers(M))})
+    heads = sorted({0, nh - 1, int(rng.integers(nh))})
+    ro, rl = ref_attention(q, k, v, nh, nkv, hd, scale, p0=p0, causal=causal, rows=rows, heads=heads)
+    cols = np.concatenate([np.arange(h * hd, (h + 1) * hd) for h in heads])
+    got = out.cpu().numpy().astype(np.float64)[rows][:, cols]
+    assert_close(got, ro, hd, what, lse.cpu().numpy()[rows][:, heads], rl)
