@@ -3,8 +3,8 @@ directed suites, helpers.assert_close). Every case draws its shape from a seeded
 heads per kv head, head dims 4..256, cache lengths 1..6000, 1..5 sequences, 1..8 query rows, causal or not, input
 scales 0.25..2; prefill chunks of 1..600 rows at offsets 0..1500 with every plan; long caches (single sequences up to
 40k keys, batches of about one length and ragged ones), chunks behind prefixes of 3..20x their length, and chunks with
-the plan or the stream-K split forced, causal or not (MX_FUZZ_SEEDS widens that sweep). The seed of a failing case is
-in its test id, so the case reruns alone. Mirrors the reference's shape sweeps over its attention kernels
+the plan or the stream-K split forced, causal or not. MX_FUZZ_SEEDS sets the seeds of every sweep. The seed of a
+failing case is in its test id, so the case reruns alone. Mirrors the reference's shape sweeps over its attention kernels
 (tests/unit/test_metal_llama_decoder.cpp, tests/unit/test_backend_ggml.cpp:677-745)."""
 import os
 
@@ -21,7 +21,11 @@ GROUPS = [(1, 1), (4, 1), (7, 1), (8, 2), (14, 2), (16, 1), (20, 20), (28, 4), (
 HEAD_DIMS = [64, 128, 64, 128, 256, 32, 16]
 
 
-@pytest.mark.parametrize("seed", range(24))
+def _seeds(default):
+    return int(os.environ.get("MX_FUZZ_SEEDS", default))
+
+
+@pytest.mark.parametrize("seed", range(_seeds(24)))
 def test_decode_fuzz(device, seed):
     rng = np.random.default_rng(1000 + seed)
     nh, nkv = GROUPS[rng.integers(len(GROUPS))]
@@ -54,7 +58,7 @@ def test_decode_fuzz(device, seed):
                      lse[b * n_q:(b + 1) * n_q][:, heads], rl)
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(_seeds(24)))
 def test_prefill_fuzz(device, seed):
     rng = np.random.default_rng(2000 + seed)
     nh, nkv = GROUPS[rng.integers(len(GROUPS))]
@@ -85,7 +89,7 @@ def test_prefill_fuzz(device, seed):
                  lse.cpu().numpy()[rows][:, heads], rl)
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(_seeds(12)))
 def test_prefill_long_prefix_fuzz(device, seed):
     # chunks behind prefixes of 3..20x their length through mx_attn_prefill_ws with the planned route: the decode route
     # for few rows, the flash kernel split by stream-K (all CUs, or fewer ranges for small launches), or its grid
@@ -113,7 +117,7 @@ def test_prefill_long_prefix_fuzz(device, seed):
                  lse.cpu().numpy()[rows][:, heads], rl)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(_seeds(8)))
 def test_decode_long_fuzz(device, seed):
     # long caches: one sequence of up to 40k keys (few kv heads: up to 64 splits) or batches of 4..6 of about one length
     # (the 8-split plan) or ragged; head dims 64 and 128, one query row
@@ -149,7 +153,7 @@ def test_decode_long_fuzz(device, seed):
                      lse[b:b + 1][:, heads], rl)
 
 
-@pytest.mark.parametrize("seed", range(int(os.environ.get("MX_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(_seeds(12)))
 def test_prefill_forced_fuzz(device, seed):
     # chunks through mx_attn_prefill_ws with the plan or the stream-K split forced by the tuning fields, causal behind a
     # prefix or not causal over a cache of any length (every query row sees every key)
